@@ -1,0 +1,223 @@
+/*
+ * wc_abi.h -- C ABI of libwide_hip.so, the gfx950 (MI355X) kernels behind the
+ * N-first wide-primitive forward path of wide_compiler.
+ *
+ * The reference (WideCompiler, pure PyTorch) has no FFI: every entry point
+ * below replaces one or more PyTorch library calls made by a reference
+ * primitive.  Each declaration cites the reference call site it replaces
+ * (paths relative to the reference repository root).
+ *
+ * Conventions
+ *   - All pointers are device pointers unless stated otherwise.  The library
+ *     never allocates or frees device memory and keeps no pointer after a call
+ *     returns.
+ *   - `stream` is a hipStream_t passed as void* (NULL = legacy default stream).
+ *     Every launch is asynchronous on that stream; no host synchronisation.
+ *   - Strides are in ELEMENTS unless the name ends in `_bytes`.
+ *   - Return value: 0 = success; < 0 = argument / shape / dtype error detected
+ *     on the host before any launch (nothing was launched); > 0 = a hipError_t
+ *     reported by the runtime at launch.  wc_last_error() returns a
+ *     thread-local message describing the last non-zero status.
+ *   - Functions are stateless and re-entrant; concurrent calls on different
+ *     streams are safe.
+ */
+#ifndef WC_ABI_H
+#define WC_ABI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WC_ABI_VERSION 1
+
+/* element types */
+enum {
+  WC_F32 = 0,
+  WC_BF16 = 1,
+  WC_F16 = 2
+};
+
+/* status codes (negative: host-side argument errors) */
+enum {
+  WC_OK = 0,
+  WC_ERR_NULL = -1,      /* required pointer is NULL */
+  WC_ERR_SHAPE = -2,     /* inconsistent or unsupported sizes */
+  WC_ERR_DTYPE = -3,     /* unsupported element type */
+  WC_ERR_ALIGN = -4,     /* pointer / stride alignment the kernel requires */
+  WC_ERR_LIMIT = -5,     /* size beyond what the kernel supports */
+  WC_ERR_ARG = -6        /* any other invalid argument */
+};
+
+/* epilogue activations */
+enum {
+  WC_ACT_NONE = 0,
+  WC_ACT_RELU = 1
+};
+
+/* recurrent cell kinds */
+enum {
+  WC_CELL_GRU = 0,
+  WC_CELL_LSTM = 1
+};
+
+/* ABI version compiled into the library (== WC_ABI_VERSION). */
+int32_t wc_abi_version(void);
+
+/* Thread-local text of the last error returned on this thread ("" if none). */
+const char* wc_last_error(void);
+
+/* Number of HIP devices visible (0 without a GPU); never launches work. */
+int32_t wc_device_count(void);
+
+/*
+ * pack_inputs -- replaces torch.stack(inputs, dim=1) + view
+ * (wide_compiler/core/ensemble_util.py:44-60, alias api.pack api.py:310-316).
+ *   dst[r, i, :] = src_i[r, :]  for r < rows, i < n,
+ * where source i row r starts at srcs[i] + r * src_row_stride_bytes[i] and
+ * holds row_bytes contiguous bytes; dst is contiguous [rows, n, row_bytes].
+ * `srcs` and `src_row_stride_bytes` are HOST arrays of length n holding
+ * device addresses / byte strides.  Bit-exact byte copy.
+ */
+int32_t wc_pack_rows(const void* const* srcs, const int64_t* src_row_stride_bytes,
+                     int64_t n, int64_t rows, int64_t row_bytes,
+                     void* dst, void* stream);
+
+/*
+ * Boundary transpose -- replaces the N-first <-> channel-packed reshapes of
+ * TracedWideModel.forward (wide_compiler/core/traced_wide.py:463-469 in,
+ * 527-532 out) and the permute(...).contiguous() copies of the conv / norm
+ * primitives (wide_conv2d.py:179,192-194; wide_batchnorm_2d.py:63,69-71).
+ *   dst[j, i, :] = src[i, j, :]   i < d0, j < d1,
+ * src element (i, j) starts at src + i*src_stride0_bytes + j*src_stride1_bytes
+ * and holds inner_bytes contiguous bytes; dst is contiguous [d1, d0, inner].
+ * Bit-exact byte copy.
+ */
+int32_t wc_swap01(const void* src, int64_t d0, int64_t d1,
+                  int64_t src_stride0_bytes, int64_t src_stride1_bytes,
+                  int64_t inner_bytes, void* dst, void* stream);
+
+/*
+ * Embedding gather -- replaces weight[:, x] / F.embedding
+ * (wide_compiler/core/primitives/wide_embedding.py:93-131).
+ *   out[i, r, :] = weight[i, ids[r], :]           (ids_shared != 0, ids [rows])
+ *   out[i, r, :] = weight[i, ids[i*rows + r], :]  (ids_shared == 0, ids [n, rows])
+ * weight is contiguous [n, vocab, dim] of `dtype`; ids are int64; out is
+ * contiguous [n, rows, dim].  An id outside [0, vocab) reads nothing, writes a
+ * zero row and, if err_flag != NULL, stores 1 into *err_flag (device int32).
+ * Bit-exact copy.
+ */
+int32_t wc_embedding_gather(const void* weight, int64_t n, int64_t vocab, int64_t dim,
+                            int32_t dtype, const int64_t* ids, int64_t rows,
+                            int32_t ids_shared, void* out, int32_t* err_flag,
+                            void* stream);
+
+/*
+ * LayerNorm over the last dim with per-model affine -- replaces the manual
+ * mean / var(unbiased=False) / normalise / affine sequence of
+ * WideLayerNorm.forward (wide_compiler/core/primitives/wide_layernorm.py:48-67).
+ *   x, y: [n, rows_per_model, dim] (row stride x_row_stride / y_row_stride,
+ *         model stride x_model_stride / y_model_stride, unit inner stride)
+ *   gamma, beta: [n, dim] contiguous of `param_dtype` (beta may be NULL)
+ *   y = (x - mean) / sqrt(var + eps) * gamma + beta, statistics in fp32.
+ */
+int32_t wc_layernorm(const void* x, int64_t x_model_stride, int64_t x_row_stride,
+                     const void* gamma, const void* beta,
+                     void* y, int64_t y_model_stride, int64_t y_row_stride,
+                     int64_t n, int64_t rows_per_model, int64_t dim, float eps,
+                     int32_t dtype, int32_t param_dtype, void* stream);
+
+/*
+ * Eval-mode BatchNorm per (model, channel) on N-first [n, b, c, hw] --
+ * replaces permute + nn.BatchNorm2d(N*C) (eval) + permute().contiguous()
+ * (wide_compiler/core/primitives/wide_batchnorm_2d.py:53-71).
+ *   y = (x - running_mean) / sqrt(running_var + eps) * weight + bias
+ * with the per-channel parameters at index (i*c + ch), computed in fp32.
+ * x strides (x_stride_n, x_stride_b) for the first two dims; the [c, hw]
+ * block of each (i, b) is contiguous.  y is contiguous [n, b, c, hw].
+ * weight / bias may be NULL (affine=False); act = WC_ACT_NONE or WC_ACT_RELU.
+ */
+int32_t wc_bn_eval(const void* x, int64_t x_stride_n, int64_t x_stride_b,
+                   const void* weight, const void* bias,
+                   const void* running_mean, const void* running_var, float eps,
+                   void* y, int64_t n, int64_t b, int64_t c, int64_t hw,
+                   int32_t dtype, int32_t param_dtype, int32_t act, void* stream);
+
+/*
+ * Recurrent layer forward (single layer, unidirectional) -- replaces the fused
+ * input projection einsum + T-step Python loop of
+ *   WideGRU._forward_fused  (wide_compiler/core/primitives/wide_gru.py:148-213)
+ *   WideLSTM._forward_fused (wide_compiler/core/primitives/wide_lstm.py:158-234)
+ * Gate order: GRU (r, z, n); LSTM (i, f, g, o) -- the torch.nn order.
+ */
+typedef struct wc_rnn_args {
+  int32_t cell;              /* WC_CELL_GRU or WC_CELL_LSTM */
+  int32_t dtype;             /* element type of x, weights, h, out */
+  int64_t n, batch, steps, input_size, hidden;
+  const void* x;             /* [n, batch, steps, input_size] with strides below */
+  int64_t x_stride_n, x_stride_b, x_stride_t;   /* unit stride over input_size */
+  const void* w_ih;          /* [n, G, input_size] contiguous, G = 3H (GRU) / 4H (LSTM) */
+  const void* w_hh;          /* [n, G, hidden] contiguous */
+  const void* b_ih;          /* [n, G] or NULL */
+  const void* b_hh;          /* [n, G] or NULL */
+  const void* h0;            /* [n, batch, hidden] contiguous or NULL (zeros) */
+  const void* c0;            /* LSTM only: [n, batch, hidden] or NULL (zeros) */
+  void* out;                 /* [n, batch, steps, hidden] contiguous */
+  void* h_n;                 /* [n, batch, hidden] contiguous (may be NULL) */
+  void* c_n;                 /* LSTM only: [n, batch, hidden] (may be NULL) */
+  void* workspace;           /* device scratch of >= wc_rnn_workspace_bytes(args) bytes,
+                                16-byte aligned; holds the fp32 input projection */
+  int64_t workspace_bytes;
+} wc_rnn_args;
+
+/* Bytes of workspace wc_rnn_forward needs for these sizes (n*batch*steps*G*4). */
+int64_t wc_rnn_workspace_bytes(const wc_rnn_args* args);
+
+/* Runs wc_rnn_input_projection, then wc_rnn_recurrence. */
+int32_t wc_rnn_forward(const wc_rnn_args* args, void* stream);
+
+/* Phase 1: gates_x = x W_ih^T + b_ih for all steps (grouped MFMA GEMM, fp32
+ * accumulate) into the workspace as fp32 [n, batch*steps, G] -- the einsum
+ * before the reference's time loop (wide_gru.py:168-170, wide_lstm.py:190-193). */
+int32_t wc_rnn_input_projection(const wc_rnn_args* args, void* stream);
+
+/* Phase 2: the time loop (wide_gru.py:181-211, wide_lstm.py:205-232) as one
+ * persistent kernel reading gates_x from the workspace; x and w_ih are not read. */
+int32_t wc_rnn_recurrence(const wc_rnn_args* args, void* stream);
+
+/*
+ * Grouped GEMM with fused epilogue -- replaces torch.einsum('noi,nbi->nbo')
+ * + bias of WideLinear._forward_einsum (wide_compiler/core/primitives/
+ * wide_linear.py:161-171), the projection einsums of WideAttention
+ * (wide_attention.py:199-213, 234-236) and the recurrent input projections
+ * (wide_gru.py:168-170, wide_lstm.py:190-193):
+ *   C[i, m, o] = act( sum_k A[i, m, k] * W[i, o, k] + bias[i, o] + R[i, m, o] )
+ * Row m of A (and of C / R) lives at  i*stride_n + (m / rows_inner)*stride_outer
+ * + (m % rows_inner)*stride_inner; the K (resp. O) dimension is contiguous.
+ * W is [n, o, k] with row stride k and model stride w_stride_n.
+ * dtype in {WC_F32, WC_BF16} (fp32 accumulation on MFMA); out_dtype is WC_F32
+ * or dtype; bias_dtype is WC_F32 or dtype; bias and residual may be NULL.
+ */
+typedef struct wc_gemm_args {
+  int32_t dtype, out_dtype, bias_dtype, act;
+  int64_t n, m, o, k;
+  const void* a;
+  int64_t a_stride_n, a_stride_outer, a_stride_inner, a_rows_inner;
+  const void* w;
+  int64_t w_stride_n;
+  const void* bias;
+  int64_t bias_stride_n;
+  const void* residual;
+  int64_t r_stride_n, r_stride_outer, r_stride_inner;   /* rows as C */
+  void* c;
+  int64_t c_stride_n, c_stride_outer, c_stride_inner, c_rows_inner;
+} wc_gemm_args;
+
+int32_t wc_grouped_gemm(const wc_gemm_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WC_ABI_H */

@@ -1,0 +1,328 @@
+// Grouped (per-model) GEMM on MFMA with a fused bias / residual / ReLU
+// epilogue:
+//   C[i][m][o] = act( sum_k A[i][m][k] * W[i][o][k] + bias[i][o] + R[i][m][o] )
+// A and W are K-contiguous ("NT"), which is exactly the operand layout MFMA
+// wants: every lane feeds 8 consecutive k values of one row.
+//
+// Tiling: a workgroup of WM x WN waves computes a (WM*TM) x (WN*TN) tile of C;
+// each wave owns a TM x TN sub-tile made of 16x16 MFMA tiles accumulated in
+// fp32.  K advances in steps of 32.  A and W tiles are staged in LDS (double
+// buffered: the next K-step is fetched into registers while the current one
+// feeds the MFMAs); rows are padded by 16 bytes so the 16-byte fragment reads
+// of a quarter-wave hit 64 distinct banks.
+//
+// bf16 uses v_mfma_f32_16x16x32_bf16 (one instruction per K-step of 32);
+// fp32 uses v_mfma_f32_16x16x4_f32 with the K-step permuted so that lane
+// group g (lanes 16g..16g+15) contributes k = 8g .. 8g+7 over eight
+// instructions -- a reordering of the k summation only.
+//
+// Rows of A / C may be addressed through a two-level decomposition
+// m = outer * rows_inner + inner, so strided N-first views (e.g. the
+// channel-packed boundary layout, or [N,B,T,I] inputs) are read in place.
+#include "wc_gemm.h"
+
+namespace wc {
+
+
+namespace {
+
+constexpr int kBK = 32;
+
+template <typename TA> struct Frag;
+template <> struct Frag<bf16> { typedef bf16x8 type; };
+template <> struct Frag<float> { typedef f32x4 type; };  // two per K-step
+
+__device__ __forceinline__ float relu_f(float v) { return v > 0.f ? v : 0.f; }
+
+template <typename TA, typename TC, typename TB, int TM, int TN, int WM, int WN, bool VEC>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmParams p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BM = WM * TM, BN = WN * TN;
+  constexpr int ES = sizeof(TA);
+  constexpr int VE = 16 / ES;                 // elements per 16-byte vector
+  constexpr int PITCH = kBK + VE;             // padded LDS row (elements)
+  constexpr int CPR = kBK / VE;               // 16-byte chunks per tile row
+  constexpr int A_CH = BM * CPR, B_CH = BN * CPR;
+  constexpr int A_PT = (A_CH + NT - 1) / NT, B_PT = (B_CH + NT - 1) / NT;
+  constexpr int FM = TM / 16, FN = TN / 16;
+
+  __shared__ __attribute__((aligned(16))) TA As[2][BM * PITCH];
+  __shared__ __attribute__((aligned(16))) TA Bs[2][BN * PITCH];
+
+  // ---- tile coordinates (XCD-aware: neighbouring tiles share an L2) ----
+  const int tiles_per_model = p.tiles_m * p.tiles_o;
+  const int nblk = p.n * tiles_per_model;
+  int bid = blockIdx.x;
+  if (p.remap) bid = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
+  const int mdl = bid / tiles_per_model;
+  const int rem = bid - mdl * tiles_per_model;
+  const int to = rem / p.tiles_m;
+  const int tm = rem - to * p.tiles_m;
+  const int m0 = tm * BM, o0 = to * BN;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave / WN, wn = wave - (wave / WN) * WN;
+
+  const TA* abase = static_cast<const TA*>(p.a) + static_cast<int64_t>(mdl) * p.a_sn;
+  const TA* wbase = static_cast<const TA*>(p.w) + static_cast<int64_t>(mdl) * p.w_sn;
+
+  // per-thread global row pointers of the chunks it stages (fixed over K)
+  const TA* arow[A_PT];
+  int acol[A_PT], aslot[A_PT];
+#pragma unroll
+  for (int q = 0; q < A_PT; ++q) {
+    const int ch = tid + q * NT;
+    const int r = ch / CPR;
+    acol[q] = (ch - r * CPR) * VE;
+    aslot[q] = (ch < A_CH) ? r * PITCH + acol[q] : -1;
+    const int gm = m0 + r;
+    arow[q] = nullptr;
+    if (ch < A_CH && gm < p.m) {
+      const uint32_t outer = fdiv(static_cast<uint32_t>(gm), p.a_ri);
+      const uint32_t inner = gm - outer * p.a_ri.d;
+      arow[q] = abase + static_cast<int64_t>(outer) * p.a_so + static_cast<int64_t>(inner) * p.a_si;
+    }
+  }
+  const TA* brow[B_PT];
+  int bcol[B_PT], bslot[B_PT];
+#pragma unroll
+  for (int q = 0; q < B_PT; ++q) {
+    const int ch = tid + q * NT;
+    const int r = ch / CPR;
+    bcol[q] = (ch - r * CPR) * VE;
+    bslot[q] = (ch < B_CH) ? r * PITCH + bcol[q] : -1;
+    const int go = o0 + r;
+    brow[q] = (ch < B_CH && go < p.o) ? wbase + static_cast<int64_t>(go) * p.k : nullptr;
+  }
+
+  uint4 areg[A_PT], breg[B_PT];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < A_PT; ++q) {
+      const int kk = k0 + acol[q];
+      if (VEC) {
+        areg[q] = (arow[q] && kk < p.k) ? *reinterpret_cast<const uint4*>(arow[q] + kk)
+                                        : make_uint4(0, 0, 0, 0);
+      } else {
+        TA tmp[VE];
+#pragma unroll
+        for (int e = 0; e < VE; ++e)
+          tmp[e] = (arow[q] && kk + e < p.k) ? arow[q][kk + e] : from_f32<TA>(0.f);
+        areg[q] = *reinterpret_cast<uint4*>(tmp);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < B_PT; ++q) {
+      const int kk = k0 + bcol[q];
+      if (VEC) {
+        breg[q] = (brow[q] && kk < p.k) ? *reinterpret_cast<const uint4*>(brow[q] + kk)
+                                        : make_uint4(0, 0, 0, 0);
+      } else {
+        TA tmp[VE];
+#pragma unroll
+        for (int e = 0; e < VE; ++e)
+          tmp[e] = (brow[q] && kk + e < p.k) ? brow[q][kk + e] : from_f32<TA>(0.f);
+        breg[q] = *reinterpret_cast<uint4*>(tmp);
+      }
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < A_PT; ++q)
+      if (aslot[q] >= 0) *reinterpret_cast<uint4*>(&As[buf][aslot[q]]) = areg[q];
+#pragma unroll
+    for (int q = 0; q < B_PT; ++q)
+      if (bslot[q] >= 0) *reinterpret_cast<uint4*>(&Bs[buf][bslot[q]]) = breg[q];
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int ktiles = (p.k + kBK - 1) / kBK;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+
+  const int fr = lane & 15;          // fragment row / column
+  const int fk = (lane >> 4) * 8;    // first k of this lane group
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ktiles) fetch((kt + 1) * kBK);
+    const TA* as = As[buf];
+    const TA* bs = Bs[buf];
+    if constexpr (sizeof(TA) == 2) {
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&as[(wm * TM + i * 16 + fr) * PITCH + fk]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&bs[(wn * TN + j * 16 + fr) * PITCH + fk]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    } else {
+      f32x4 af[FM][2], bfr[FN][2];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const float* src = reinterpret_cast<const float*>(&as[(wm * TM + i * 16 + fr) * PITCH + fk]);
+        af[i][0] = *reinterpret_cast<const f32x4*>(src);
+        af[i][1] = *reinterpret_cast<const f32x4*>(src + 4);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const float* src = reinterpret_cast<const float*>(&bs[(wn * TN + j * 16 + fr) * PITCH + fk]);
+        bfr[j][0] = *reinterpret_cast<const f32x4*>(src);
+        bfr[j][1] = *reinterpret_cast<const f32x4*>(src + 4);
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s >> 2][s & 3], bfr[j][s >> 2][s & 3],
+                                                             acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < ktiles) {
+      stash(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue: bias, residual, activation, store ----
+  const TB* bias = p.bias ? static_cast<const TB*>(p.bias) + static_cast<int64_t>(mdl) * p.b_sn : nullptr;
+  TC* cbase = static_cast<TC*>(p.c) + static_cast<int64_t>(mdl) * p.c_sn;
+  const TC* rbase = p.r ? static_cast<const TC*>(p.r) + static_cast<int64_t>(mdl) * p.r_sn : nullptr;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int col = o0 + wn * TN + j * 16 + fr;
+    if (col >= p.o) continue;
+    const float bv = bias ? to_f32(bias[col]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + wm * TM + i * 16 + (lane >> 4) * 4 + e;
+        if (row >= p.m) continue;
+        const uint32_t outer = fdiv(static_cast<uint32_t>(row), p.c_ri);
+        const uint32_t inner = row - outer * p.c_ri.d;
+        const int64_t off = static_cast<int64_t>(outer) * p.c_so + static_cast<int64_t>(inner) * p.c_si + col;
+        float v = acc[i][j][e] + bv;
+        if (rbase) {
+          const int64_t roff = static_cast<int64_t>(outer) * p.r_so + static_cast<int64_t>(inner) * p.r_si + col;
+          v += to_f32(rbase[roff]);
+        }
+        if (p.act == WC_ACT_RELU) v = relu_f(v);
+        cbase[off] = from_f32<TC>(v);
+      }
+    }
+  }
+}
+
+template <typename TA, typename TC, typename TB, int TM, int TN, int WM, int WN>
+int32_t launch_cfg(GemmParams p, bool vec, hipStream_t st) {
+  constexpr int BM = WM * TM, BN = WN * TN;
+  p.tiles_m = static_cast<int>(cdiv(p.m, BM));
+  p.tiles_o = static_cast<int>(cdiv(p.o, BN));
+  const int64_t nblk = static_cast<int64_t>(p.n) * p.tiles_m * p.tiles_o;
+  if (nblk >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_grouped_gemm: too many tiles");
+  p.remap = (nblk % 8 == 0) ? 1 : 0;
+  const dim3 grid(static_cast<uint32_t>(nblk)), block(WM * WN * 64);
+  if (vec)
+    gemm_kernel<TA, TC, TB, TM, TN, WM, WN, true><<<grid, block, 0, st>>>(p);
+  else
+    gemm_kernel<TA, TC, TB, TM, TN, WM, WN, false><<<grid, block, 0, st>>>(p);
+  return check_launch("wc_grouped_gemm");
+}
+
+template <typename TA, typename TC, typename TB>
+int32_t launch_gemm_t(const GemmParams& p, bool vec, hipStream_t st) {
+  // small problems: 64x64 tiles keep more workgroups in flight
+  const int64_t tiles128 = static_cast<int64_t>(p.n) * cdiv(p.m, 128) * cdiv(p.o, 128);
+  if (tiles128 >= 512) return launch_cfg<TA, TC, TB, 64, 64, 2, 2>(p, vec, st);
+  return launch_cfg<TA, TC, TB, 32, 32, 2, 2>(p, vec, st);
+}
+
+}  // namespace
+
+// Internal entry shared by other kernel families (e.g. the recurrent input
+// projection).  Dtypes: A/W in {f32, bf16}; C f32 or == A; bias f32 or == A.
+int32_t grouped_gemm(const GemmParams& p0, int32_t dtype, int32_t out_dtype, int32_t bias_dtype,
+                     hipStream_t st) {
+  GemmParams p = p0;
+  const int es = dtype_size(dtype);
+  const bool vec = common_vec_bytes({reinterpret_cast<uintptr_t>(p.a), reinterpret_cast<uintptr_t>(p.w),
+                                     static_cast<uint64_t>(p.k * es), static_cast<uint64_t>(p.a_sn * es),
+                                     static_cast<uint64_t>(p.a_so * es), static_cast<uint64_t>(p.a_si * es),
+                                     static_cast<uint64_t>(p.w_sn * es)}) >= 16;
+  if (dtype == WC_F32) {
+    if (out_dtype != WC_F32 || (p.bias && bias_dtype != WC_F32))
+      return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: f32 inputs need f32 output and bias");
+    return launch_gemm_t<float, float, float>(p, vec, st);
+  }
+  if (dtype == WC_BF16) {
+    const bool bias_f32 = p.bias && bias_dtype == WC_F32;
+    if (p.bias && bias_dtype != WC_F32 && bias_dtype != WC_BF16)
+      return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: bias dtype %s", dtype_name(bias_dtype));
+    if (out_dtype == WC_BF16)
+      return bias_f32 ? launch_gemm_t<bf16, bf16, float>(p, vec, st)
+                      : launch_gemm_t<bf16, bf16, bf16>(p, vec, st);
+    if (out_dtype == WC_F32)
+      return bias_f32 ? launch_gemm_t<bf16, float, float>(p, vec, st)
+                      : launch_gemm_t<bf16, float, bf16>(p, vec, st);
+    return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: output dtype %s", dtype_name(out_dtype));
+  }
+  return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: unsupported dtype %s", dtype_name(dtype));
+}
+
+}  // namespace wc
+
+using namespace wc;
+
+extern "C" int32_t wc_grouped_gemm(const wc_gemm_args* g, void* stream) {
+  clear_error();
+  WC_REQUIRE(g != nullptr, WC_ERR_NULL, "wc_grouped_gemm: null args");
+  WC_REQUIRE(g->n >= 0 && g->m >= 0 && g->o >= 0 && g->k >= 0, WC_ERR_SHAPE,
+             "wc_grouped_gemm: negative size");
+  if (g->n == 0 || g->m == 0 || g->o == 0) return WC_OK;
+  WC_REQUIRE(g->a && g->w && g->c, WC_ERR_NULL, "wc_grouped_gemm: null pointer");
+  WC_REQUIRE(g->act == WC_ACT_NONE || g->act == WC_ACT_RELU, WC_ERR_ARG, "wc_grouped_gemm: bad act");
+  WC_REQUIRE(g->m < 0x7fffffffll && g->o < 0x7fffffffll && g->k < 0x7fffffffll && g->n < 0x7fffffffll,
+             WC_ERR_LIMIT, "wc_grouped_gemm: sizes too large");
+  WC_REQUIRE(g->a_rows_inner > 0 && g->c_rows_inner > 0, WC_ERR_ARG,
+             "wc_grouped_gemm: rows_inner must be positive");
+  WC_REQUIRE(g->residual == nullptr || g->out_dtype == g->dtype || g->out_dtype == WC_F32,
+             WC_ERR_DTYPE, "wc_grouped_gemm: residual dtype");
+  GemmParams p;
+  p.n = (int)g->n;
+  p.m = (int)g->m;
+  p.o = (int)g->o;
+  p.k = (int)g->k;
+  p.act = g->act;
+  p.a = g->a;
+  p.a_sn = g->a_stride_n;
+  p.a_so = g->a_stride_outer;
+  p.a_si = g->a_stride_inner;
+  p.a_ri = make_fastdiv(static_cast<uint32_t>(g->a_rows_inner));
+  p.w = g->w;
+  p.w_sn = g->w_stride_n;
+  p.bias = g->bias;
+  p.b_sn = g->bias_stride_n;
+  p.r = g->residual;
+  p.r_sn = g->r_stride_n;
+  p.r_so = g->r_stride_outer;
+  p.r_si = g->r_stride_inner;
+  p.c = g->c;
+  p.c_sn = g->c_stride_n;
+  p.c_so = g->c_stride_outer;
+  p.c_si = g->c_stride_inner;
+  p.c_ri = make_fastdiv(static_cast<uint32_t>(g->c_rows_inner));
+  return grouped_gemm(p, g->dtype, g->out_dtype, g->bias_dtype, as_stream(stream));
+}

@@ -1,0 +1,280 @@
+// N-first normalisation kernels: LayerNorm with per-model affine, and
+// eval-mode BatchNorm per (model, channel).  Both are HBM-bound: one read and
+// one write of the activation, statistics in fp32 registers.
+#include "wc_common.h"
+
+namespace wc {
+namespace {
+
+constexpr int kNormBlock = 256;
+
+template <typename T, int V> struct LoadV;
+template <typename T> struct LoadV<T, 1> {
+  static __device__ __forceinline__ void ld(const T* p, float* o) { o[0] = to_f32(p[0]); }
+  static __device__ __forceinline__ void st(T* p, const float* o) { p[0] = from_f32<T>(o[0]); }
+};
+template <> struct LoadV<float, 4> {
+  static __device__ __forceinline__ void ld(const float* p, float* o) {
+    const float4 v = *reinterpret_cast<const float4*>(p);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  }
+  static __device__ __forceinline__ void st(float* p, const float* o) {
+    *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+};
+template <typename H> struct LoadV8x16 {
+  static __device__ __forceinline__ void ld(const H* p, float* o) {
+    typedef H h8 __attribute__((ext_vector_type(8)));
+    const h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = static_cast<float>(v[i]);
+  }
+  static __device__ __forceinline__ void st(H* p, const float* o) {
+    typedef H h8 __attribute__((ext_vector_type(8)));
+    h8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = static_cast<H>(o[i]);
+    *reinterpret_cast<h8*>(p) = v;
+  }
+};
+template <> struct LoadV<bf16, 8> : LoadV8x16<bf16> {};
+template <> struct LoadV<f16, 8> : LoadV8x16<f16> {};
+
+__device__ __forceinline__ float lanes_sum(float v, int lanes) {
+  for (int off = lanes >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// One group of `lanes` adjacent lanes per row; lane j of the group owns the
+// V-element vectors at (it * lanes + j) * V for it < ITEMS.
+template <typename T, typename P, int V, int ITEMS>
+__global__ __launch_bounds__(kNormBlock) void layernorm_kernel(
+    const T* __restrict__ x, int64_t xms, int64_t xrs, const P* __restrict__ gamma,
+    const P* __restrict__ beta, T* __restrict__ y, int64_t yms, int64_t yrs, uint32_t rows_total,
+    FastDiv rows_per_model, int dim, int lanes_log2, float eps) {
+  const int lanes = 1 << lanes_log2;
+  const int tid = threadIdx.x;
+  const int j = tid & (lanes - 1);
+  const uint32_t row = blockIdx.x * (kNormBlock >> lanes_log2) + (tid >> lanes_log2);
+  if (row >= rows_total) return;  // whole lane groups leave together
+  const uint32_t m = fdiv(row, rows_per_model);
+  const uint32_t r = row - m * rows_per_model.d;
+  const T* xr = x + static_cast<int64_t>(m) * xms + static_cast<int64_t>(r) * xrs;
+  T* yr = y + static_cast<int64_t>(m) * yms + static_cast<int64_t>(r) * yrs;
+  const P* g = gamma + static_cast<int64_t>(m) * dim;
+  const P* b = beta ? beta + static_cast<int64_t>(m) * dim : nullptr;
+
+  float v[ITEMS][V];
+  float s = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * lanes + j) * V;
+    if (e < dim) {
+      LoadV<T, V>::ld(xr + e, v[it]);
+#pragma unroll
+      for (int q = 0; q < V; ++q) s += v[it][q];
+    }
+  }
+  const float mean = lanes_sum(s, lanes) / static_cast<float>(dim);
+  float s2 = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * lanes + j) * V;
+    if (e < dim) {
+#pragma unroll
+      for (int q = 0; q < V; ++q) {
+        const float d = v[it][q] - mean;
+        s2 += d * d;
+      }
+    }
+  }
+  const float var = lanes_sum(s2, lanes) / static_cast<float>(dim);
+  const float denom = sqrtf(var + eps);
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * lanes + j) * V;
+    if (e < dim) {
+      float o[V];
+#pragma unroll
+      for (int q = 0; q < V; ++q) {
+        const float bq = b ? to_f32(b[e + q]) : 0.f;
+        o[q] = ((v[it][q] - mean) / denom) * to_f32(g[e + q]) + bq;
+      }
+      LoadV<T, V>::st(yr + e, o);
+    }
+  }
+}
+
+// eval BatchNorm: one 16-byte (or narrower) vector per thread per unroll slot
+template <typename T, typename P, int V>
+__global__ __launch_bounds__(kNormBlock) void bn_eval_kernel(
+    const T* __restrict__ x, int64_t xsn, int64_t xsb, const P* __restrict__ w,
+    const P* __restrict__ bias, const P* __restrict__ rm, const P* __restrict__ rv, float eps,
+    T* __restrict__ y, uint32_t total_chunks, FastDiv cpp, FastDiv nch, FastDiv nb, int hw,
+    int relu) {
+  const uint32_t k = blockIdx.x * kNormBlock + threadIdx.x;
+  if (k >= total_chunks) return;
+  const uint32_t p = fdiv(k, cpp);            // plane = (i * B + b) * C + ch
+  const uint32_t c = k - p * cpp.d;
+  const uint32_t ib = fdiv(p, nch);
+  const uint32_t ch = p - ib * nch.d;
+  const uint32_t i = fdiv(ib, nb);
+  const uint32_t bb = ib - i * nb.d;
+  const uint32_t pi = i * nch.d + ch;          // parameter index (model, channel)
+  const float invstd = 1.0f / sqrtf(to_f32(rv[pi]) + eps);
+  const float alpha = w ? invstd * to_f32(w[pi]) : invstd;
+  const float beta = (bias ? to_f32(bias[pi]) : 0.f) - to_f32(rm[pi]) * alpha;
+  const int64_t e = static_cast<int64_t>(c) * V;
+  const T* xp = x + static_cast<int64_t>(i) * xsn + static_cast<int64_t>(bb) * xsb +
+                static_cast<int64_t>(ch) * hw + e;
+  T* yp = y + static_cast<int64_t>(p) * hw + e;
+  float v[V];
+  LoadV<T, V>::ld(xp, v);
+#pragma unroll
+  for (int q = 0; q < V; ++q) {
+    float o = v[q] * alpha + beta;
+    if (relu) o = o > 0.f ? o : 0.f;
+    v[q] = o;
+  }
+  LoadV<T, V>::st(yp, v);
+}
+
+template <typename T, typename P, int V>
+int32_t launch_layernorm_v(const T* x, int64_t xms, int64_t xrs, const P* g, const P* b, T* y,
+                           int64_t yms, int64_t yrs, int64_t n, int64_t rpm, int dim, float eps,
+                           hipStream_t st) {
+  const int64_t nvec = cdiv(dim, V);
+  int lanes_log2 = 0;
+  while ((1 << lanes_log2) < nvec && lanes_log2 < 6) ++lanes_log2;
+  const int lanes = 1 << lanes_log2;
+  const int items = static_cast<int>(cdiv(nvec, lanes));
+  const uint32_t rows_total = static_cast<uint32_t>(n * rpm);
+  const int rows_per_block = kNormBlock >> lanes_log2;
+  const dim3 grid(static_cast<uint32_t>(cdiv(rows_total, rows_per_block)));
+  const FastDiv fr = make_fastdiv(static_cast<uint32_t>(rpm));
+#define WC_LN_CASE(IT)                                                                        \
+  if (items <= IT) {                                                                          \
+    layernorm_kernel<T, P, V, IT><<<grid, kNormBlock, 0, st>>>(x, xms, xrs, g, b, y, yms, yrs, \
+                                                               rows_total, fr, dim, lanes_log2, eps); \
+    return check_launch("wc_layernorm");                                                      \
+  }
+  WC_LN_CASE(1)
+  WC_LN_CASE(2)
+  WC_LN_CASE(4)
+  WC_LN_CASE(8)
+  WC_LN_CASE(16)
+#undef WC_LN_CASE
+  return set_error(WC_ERR_LIMIT, "wc_layernorm: dim %d too large", dim);
+}
+
+template <typename T, typename P>
+int32_t launch_layernorm(const void* x, int64_t xms, int64_t xrs, const void* g, const void* b,
+                         void* y, int64_t yms, int64_t yrs, int64_t n, int64_t rpm, int64_t dim,
+                         float eps, hipStream_t st) {
+  constexpr int VMAX = 16 / sizeof(T);
+  const int es = sizeof(T);
+  const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(y),
+                                   reinterpret_cast<uintptr_t>(g), reinterpret_cast<uintptr_t>(b),
+                                   static_cast<uint64_t>(dim * es),
+                                   static_cast<uint64_t>(xms * es), static_cast<uint64_t>(xrs * es),
+                                   static_cast<uint64_t>(yms * es), static_cast<uint64_t>(yrs * es),
+                                   static_cast<uint64_t>(dim * sizeof(P))});
+  const bool vec_ok = vb >= 16;
+  if (vec_ok && dim <= 16 * 64 * VMAX)
+    return launch_layernorm_v<T, P, VMAX>(static_cast<const T*>(x), xms, xrs,
+                                          static_cast<const P*>(g), static_cast<const P*>(b),
+                                          static_cast<T*>(y), yms, yrs, n, rpm, (int)dim, eps, st);
+  return launch_layernorm_v<T, P, 1>(static_cast<const T*>(x), xms, xrs, static_cast<const P*>(g),
+                                     static_cast<const P*>(b), static_cast<T*>(y), yms, yrs, n, rpm,
+                                     (int)dim, eps, st);
+}
+
+template <typename T, typename P>
+int32_t launch_bn(const void* x, int64_t xsn, int64_t xsb, const void* w, const void* bias,
+                  const void* rm, const void* rv, float eps, void* y, int64_t n, int64_t b,
+                  int64_t c, int64_t hw, int act, hipStream_t st) {
+  constexpr int VMAX = 16 / sizeof(T);
+  const int es = sizeof(T);
+  const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(y),
+                                   static_cast<uint64_t>(hw * es), static_cast<uint64_t>(xsn * es),
+                                   static_cast<uint64_t>(xsb * es)});
+  const int v = (vb >= 16) ? VMAX : 1;
+  const uint64_t planes = static_cast<uint64_t>(n * b * c);
+  const uint64_t cpp = static_cast<uint64_t>(hw / v);
+  const uint64_t total = planes * cpp;
+  if (total >= 0x7fffffffull) return set_error(WC_ERR_LIMIT, "wc_bn_eval: tensor too large");
+  const dim3 grid(static_cast<uint32_t>(cdiv(total, kNormBlock)));
+  const FastDiv fcpp = make_fastdiv(static_cast<uint32_t>(cpp));
+  const FastDiv fc = make_fastdiv(static_cast<uint32_t>(c));
+  const FastDiv fb = make_fastdiv(static_cast<uint32_t>(b));
+  if (v == VMAX)
+    bn_eval_kernel<T, P, VMAX><<<grid, kNormBlock, 0, st>>>(
+        static_cast<const T*>(x), xsn, xsb, static_cast<const P*>(w), static_cast<const P*>(bias),
+        static_cast<const P*>(rm), static_cast<const P*>(rv), eps, static_cast<T*>(y),
+        static_cast<uint32_t>(total), fcpp, fc, fb, (int)hw, act == WC_ACT_RELU);
+  else
+    bn_eval_kernel<T, P, 1><<<grid, kNormBlock, 0, st>>>(
+        static_cast<const T*>(x), xsn, xsb, static_cast<const P*>(w), static_cast<const P*>(bias),
+        static_cast<const P*>(rm), static_cast<const P*>(rv), eps, static_cast<T*>(y),
+        static_cast<uint32_t>(total), fcpp, fc, fb, (int)hw, act == WC_ACT_RELU);
+  return check_launch("wc_bn_eval");
+}
+
+}  // namespace
+}  // namespace wc
+
+using namespace wc;
+
+extern "C" int32_t wc_layernorm(const void* x, int64_t x_model_stride, int64_t x_row_stride,
+                                const void* gamma, const void* beta, void* y,
+                                int64_t y_model_stride, int64_t y_row_stride, int64_t n,
+                                int64_t rows_per_model, int64_t dim, float eps, int32_t dtype,
+                                int32_t param_dtype, void* stream) {
+  clear_error();
+  WC_REQUIRE(n >= 0 && rows_per_model >= 0 && dim >= 0, WC_ERR_SHAPE, "wc_layernorm: negative size");
+  if (n == 0 || rows_per_model == 0 || dim == 0) return WC_OK;
+  WC_REQUIRE(x && y && gamma, WC_ERR_NULL, "wc_layernorm: null pointer");
+  WC_REQUIRE(n * rows_per_model < 0x7fffffffll, WC_ERR_LIMIT, "wc_layernorm: too many rows");
+  hipStream_t st = as_stream(stream);
+  if (dtype == WC_F32 && param_dtype == WC_F32)
+    return launch_layernorm<float, float>(x, x_model_stride, x_row_stride, gamma, beta, y,
+                                          y_model_stride, y_row_stride, n, rows_per_model, dim, eps, st);
+  if (dtype == WC_BF16 && param_dtype == WC_BF16)
+    return launch_layernorm<bf16, bf16>(x, x_model_stride, x_row_stride, gamma, beta, y,
+                                        y_model_stride, y_row_stride, n, rows_per_model, dim, eps, st);
+  if (dtype == WC_BF16 && param_dtype == WC_F32)
+    return launch_layernorm<bf16, float>(x, x_model_stride, x_row_stride, gamma, beta, y,
+                                         y_model_stride, y_row_stride, n, rows_per_model, dim, eps, st);
+  if (dtype == WC_F16 && param_dtype == WC_F16)
+    return launch_layernorm<f16, f16>(x, x_model_stride, x_row_stride, gamma, beta, y,
+                                      y_model_stride, y_row_stride, n, rows_per_model, dim, eps, st);
+  return set_error(WC_ERR_DTYPE, "wc_layernorm: unsupported dtype pair (%s, %s)", dtype_name(dtype),
+                   dtype_name(param_dtype));
+}
+
+extern "C" int32_t wc_bn_eval(const void* x, int64_t x_stride_n, int64_t x_stride_b,
+                              const void* weight, const void* bias, const void* running_mean,
+                              const void* running_var, float eps, void* y, int64_t n, int64_t b,
+                              int64_t c, int64_t hw, int32_t dtype, int32_t param_dtype,
+                              int32_t act, void* stream) {
+  clear_error();
+  WC_REQUIRE(n >= 0 && b >= 0 && c >= 0 && hw >= 0, WC_ERR_SHAPE, "wc_bn_eval: negative size");
+  if (n == 0 || b == 0 || c == 0 || hw == 0) return WC_OK;
+  WC_REQUIRE(x && y && running_mean && running_var, WC_ERR_NULL, "wc_bn_eval: null pointer");
+  WC_REQUIRE(act == WC_ACT_NONE || act == WC_ACT_RELU, WC_ERR_ARG, "wc_bn_eval: bad act %d", act);
+  hipStream_t st = as_stream(stream);
+  if (dtype == WC_F32 && param_dtype == WC_F32)
+    return launch_bn<float, float>(x, x_stride_n, x_stride_b, weight, bias, running_mean,
+                                   running_var, eps, y, n, b, c, hw, act, st);
+  if (dtype == WC_BF16 && param_dtype == WC_BF16)
+    return launch_bn<bf16, bf16>(x, x_stride_n, x_stride_b, weight, bias, running_mean,
+                                 running_var, eps, y, n, b, c, hw, act, st);
+  if (dtype == WC_BF16 && param_dtype == WC_F32)
+    return launch_bn<bf16, float>(x, x_stride_n, x_stride_b, weight, bias, running_mean,
+                                  running_var, eps, y, n, b, c, hw, act, st);
+  if (dtype == WC_F16 && param_dtype == WC_F16)
+    return launch_bn<f16, f16>(x, x_stride_n, x_stride_b, weight, bias, running_mean, running_var,
+                               eps, y, n, b, c, hw, act, st);
+  return set_error(WC_ERR_DTYPE, "wc_bn_eval: unsupported dtype pair (%s, %s)", dtype_name(dtype),
+                   dtype_name(param_dtype));
+}

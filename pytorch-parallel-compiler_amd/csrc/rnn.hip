@@ -1,0 +1,469 @@
+// Persistent recurrent kernels (GRU / LSTM forward, one layer, unidirectional).
+//
+// Two launches.  (1) The input projection gates_x = x W_ih^T + b_ih for all
+// steps at once, as a grouped MFMA GEMM into an fp32 workspace [N, B*T, G]
+// (the reference computes the same einsum before its time loop).  (2) The
+// recurrence: one workgroup owns one (model, batch row) pair for all T steps;
+// batch rows never interact in a recurrence, so no cross-workgroup
+// synchronisation is needed.  Every lane holds a K-slice of one gate row of
+// W_hh in registers for the whole sequence (loaded once).
+//
+// The step loop issues no vector-memory instruction at all: gates_x for a
+// chunk of XT steps is staged into LDS with coalesced loads before the chunk,
+// and the chunk's hidden states are collected in LDS and written out with
+// coalesced stores after it.  (Global loads and stores in flight together
+// inside the loop make the compiler wait for all outstanding memory at every
+// iteration, exposing the full memory latency once per step.)
+//
+// Lane layout: lanes form groups of LG = 8 or 16 adjacent lanes (a DPP
+// half-row or row).  Group g owns UPG hidden units u = g*UPG + k and therefore
+// the GATES*UPG gate rows q*H + u of W_hh; lane j of the group holds columns
+// [j*KL, (j+1)*KL) of those rows in registers (loaded once, 16-byte vector
+// loads).  Per step a lane reads only its KL hidden values from LDS (padded,
+// bank-conflict-free layout), forms GATES*UPG partial dot products and folds
+// them across the group with log2(LG) DPP butterfly adds (no LDS traffic).
+// Lane k < UPG of the group then applies the cell update of unit g*UPG + k and
+// writes h into LDS; one barrier per step.
+#include "wc_gemm.h"
+
+namespace wc {
+namespace {
+
+constexpr int kRnnMaxThreads = 1024;
+constexpr int kRnnLdsBudget = 144 * 1024;   // of gfx950's 160 KB per workgroup
+
+struct RnnParams {
+  int n, batch, steps, in, hid;
+  int lg;             // lanes per group (8 or 16)
+  int kl;             // hidden columns per lane (multiple of 4)
+  int upg;            // hidden units per group
+  int wvec;           // W_hh rows can be read with 16-byte vector loads
+  int xt;             // steps per LDS chunk of gates_x / outputs
+  int remap;          // XCD-aware workgroup order
+  const float* gx;    // [N, B, T, G] fp32 input projection incl. b_ih
+  const void* w_hh;
+  const void* b_hh;
+  const void* h0;
+  const void* c0;
+  void* out;
+  void* hn;
+  void* cn;
+};
+
+// v_exp_f32 / v_rcp_f32 based activations, branch-free.  sigmoid has ~1e-7
+// relative error; tanh(x) = 1 - 2 / (e^2x + 1) has ~1e-7 absolute error
+// (its relative error grows only where |tanh| itself is below ~1e-3), both
+// far inside the parity bars.
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
+__device__ __forceinline__ float tanh_f(float x) {
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * x) + 1.0f);
+}
+
+// DPP lane permutations inside a 16-lane row (register-to-register, no LDS)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF,
+                                                               0xF, true));
+}
+
+// sum over groups of LG adjacent lanes (8: half-row, 16: row), delivered to
+// every lane of the group
+template <int LG>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);   // row_half_mirror: lane i <- 7 - i within each 8 lanes
+  if (LG == 16) v += dpp<0x140>(v);   // row_mirror: lane i <- 15 - i
+  return v;
+}
+
+// KL consecutive elements of a W_hh row as floats (16-byte loads when allowed)
+template <typename T, int KL>
+__device__ __forceinline__ void load_cols(const T* row, int col0, int h, bool vec, float* dst) {
+  constexpr int VE = 16 / sizeof(T);
+  if (vec && col0 + KL <= h) {
+#pragma unroll
+    for (int i = 0; i < KL; i += VE) {
+      if constexpr (sizeof(T) == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(row + col0 + i);
+        dst[i] = v.x;
+        dst[i + 1] = v.y;
+        dst[i + 2] = v.z;
+        dst[i + 3] = v.w;
+      } else {
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        const t8 v = *reinterpret_cast<const t8*>(row + col0 + i);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (i + e < KL) dst[i + e] = static_cast<float>(v[e]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) dst[i] = (col0 + i < h) ? to_f32(row[col0 + i]) : 0.f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float ldf(const void* p, int64_t i) {
+  return to_f32(static_cast<const T*>(p)[i]);
+}
+
+// LDS-only barrier: waits for this wave's LDS traffic, not for its global
+// loads, so the gates_x prefetches stay in flight across steps.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Lanes holding more than 64 weight registers run at most 8 waves per
+// workgroup (two per SIMD), which doubles the VGPRs each may use.
+constexpr int rnn_bound(int gates, int upg, int kl) { return gates * upg * kl > 64 ? 512 : 1024; }
+
+template <typename T, int CELL, int LG, int UPG, int KL>
+__global__ __launch_bounds__(rnn_bound(CELL == WC_CELL_GRU ? 3 : 4, UPG, KL)) void rnn_seq_kernel(RnnParams p) {
+  constexpr int GATES = (CELL == WC_CELL_GRU) ? 3 : 4;
+  constexpr int KLP = KL + 4;                        // padded LDS pitch per lane slice
+  constexpr int HP = LG * KLP;                       // padded h buffer length
+  const int H = p.hid;
+  const int G = GATES * H;
+  extern __shared__ float4 smem4[];
+  float* sh_h = reinterpret_cast<float*>(smem4);    // [2][HP]
+  float* sgx = sh_h + 2 * HP;                        // [xt][G]
+  float* sout = sgx + static_cast<int64_t>(p.xt) * G;  // [xt][H]
+
+  // workgroup -> (model, batch row); with remap, consecutive ids (the batch
+  // rows of one model, which read the same weights) share an XCD's L2.
+  const int nwg = p.n * p.batch;
+  int id = blockIdx.x;
+  if (p.remap) id = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  const int mdl = id / p.batch;
+  const int bb = id - mdl * p.batch;
+
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int j = tid & (LG - 1);           // lane in the group
+  const int grp = tid / LG;               // group
+  const int u0 = grp * UPG;               // first unit of the group
+
+  // ---- registers: W_hh[q*H + u0 + k][j*KL .. +KL] and b_hh ----
+  float w[UPG][GATES][KL];
+  float bhh[UPG][GATES];
+  {
+    const T* wb = static_cast<const T*>(p.w_hh) + static_cast<int64_t>(mdl) * G * H;
+#pragma unroll
+    for (int k = 0; k < UPG; ++k)
+#pragma unroll
+      for (int q = 0; q < GATES; ++q) {
+        const int u = u0 + k;
+        if (u < H) {
+          load_cols<T, KL>(wb + static_cast<int64_t>(q * H + u) * H, j * KL, H, p.wvec != 0, w[k][q]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < KL; ++i) w[k][q][i] = 0.f;
+        }
+        bhh[k][q] = (u < H && p.b_hh) ? ldf<T>(p.b_hh, static_cast<int64_t>(mdl) * G + q * H + u) : 0.f;
+      }
+  }
+
+  // ---- LDS init: h0 in the padded layout, zeros elsewhere ----
+  const int64_t st_off = (static_cast<int64_t>(mdl) * p.batch + bb) * H;  // [n, b, H] offset
+  for (int e = tid; e < 2 * HP; e += nthreads) {
+    const int pos = e < HP ? e : e - HP;
+    const int sl = pos / KLP, off = pos - sl * KLP;
+    const int col = sl * KL + off;
+    float v = 0.f;
+    if (e < HP && off < KL && col < H && p.h0) v = ldf<T>(p.h0, st_off + col);
+    sh_h[e] = v;
+  }
+  const int my_u = u0 + j;                     // unit updated by this lane (j < UPG)
+  const bool leader = (j < UPG) && (my_u < H);
+  const int my_pos = (my_u / KL) * KLP + (my_u % KL);
+  float h_reg = 0.f, c_reg = 0.f;
+  if (leader) {
+    h_reg = p.h0 ? ldf<T>(p.h0, st_off + my_u) : 0.f;
+    if (CELL == WC_CELL_LSTM) c_reg = p.c0 ? ldf<T>(p.c0, st_off + my_u) : 0.f;
+  }
+  T* outb = static_cast<T*>(p.out) + (static_cast<int64_t>(mdl) * p.batch + bb) *
+                                          static_cast<int64_t>(p.steps) * H;
+  const float* gxb = p.gx + (static_cast<int64_t>(mdl) * p.batch + bb) * static_cast<int64_t>(p.steps) * G;
+
+  int prev_t0 = 0, prev_nt = 0;
+  for (int t0 = 0; t0 < p.steps; t0 += p.xt) {
+    const int nt = (p.steps - t0 < p.xt) ? (p.steps - t0) : p.xt;
+    // flush the previous chunk's hidden states (contiguous rows of out)
+    for (int e = tid; e < prev_nt * H; e += nthreads)
+      outb[static_cast<int64_t>(prev_t0) * H + e] = from_f32<T>(sout[e]);
+    // stage this chunk's gates_x (contiguous in the workspace)
+    const float4* src4 = reinterpret_cast<const float4*>(gxb + static_cast<int64_t>(t0) * G);
+    float4* dst4 = reinterpret_cast<float4*>(sgx);
+    for (int e = tid; e < (nt * G) >> 2; e += nthreads) dst4[e] = src4[e];
+    for (int e = ((nt * G) & ~3) + tid; e < nt * G; e += nthreads)
+      sgx[e] = gxb[static_cast<int64_t>(t0) * G + e];
+    __syncthreads();
+
+    for (int tt = 0; tt < nt; ++tt) {
+      const int cur = (t0 + tt) & 1;
+      float hv[KL];
+      const float* hs = sh_h + cur * HP + j * KLP;
+#pragma unroll
+      for (int i = 0; i < KL; i += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(hs + i);
+        hv[i] = a.x;
+        hv[i + 1] = a.y;
+        hv[i + 2] = a.z;
+        hv[i + 3] = a.w;
+      }
+      // gates_h = h W_hh^T + b_hh for the group's rows, summed over the group
+      float gh[UPG][GATES];
+#pragma unroll
+      for (int k = 0; k < UPG; ++k)
+#pragma unroll
+        for (int q = 0; q < GATES; ++q) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < KL; ++i) acc += w[k][q][i] * hv[i];
+          gh[k][q] = group_sum_dpp<LG>(acc) + bhh[k][q];
+        }
+      if (leader) {
+        // this lane's unit: pick its gates from the group sums (j == k)
+        float g_h[GATES];
+#pragma unroll
+        for (int q = 0; q < GATES; ++q) {
+          g_h[q] = gh[0][q];
+#pragma unroll
+          for (int k = 1; k < UPG; ++k)
+            if (j == k) g_h[q] = gh[k][q];
+        }
+        const float* gxt = sgx + tt * G + my_u;   // gates_x = x W_ih^T + b_ih
+        float hnew;
+        if (CELL == WC_CELL_GRU) {
+          const float rg = sigmoid_f(gxt[0] + g_h[0]);
+          const float zg = sigmoid_f(gxt[H] + g_h[1]);
+          const float nn = tanh_f(gxt[2 * H] + rg * g_h[2]);
+          hnew = (1.0f - zg) * nn + zg * h_reg;
+        } else {
+          const float ig = sigmoid_f(gxt[0] + g_h[0]);
+          const float fg = sigmoid_f(gxt[H] + g_h[1]);
+          const float gg = tanh_f(gxt[2 * H] + g_h[2]);
+          const float og = sigmoid_f(gxt[3 * H] + g_h[3]);
+          c_reg = fg * c_reg + ig * gg;
+          hnew = og * tanh_f(c_reg);
+        }
+        h_reg = hnew;
+        sh_h[(cur ^ 1) * HP + my_pos] = hnew;
+        sout[tt * H + my_u] = hnew;
+      }
+      lds_barrier();
+    }
+    prev_t0 = t0;
+    prev_nt = nt;
+  }
+  for (int e = tid; e < prev_nt * H; e += nthreads)
+    outb[static_cast<int64_t>(prev_t0) * H + e] = from_f32<T>(sout[e]);
+  if (leader) {
+    if (p.hn) static_cast<T*>(p.hn)[st_off + my_u] = from_f32<T>(h_reg);
+    if (CELL == WC_CELL_LSTM && p.cn) static_cast<T*>(p.cn)[st_off + my_u] = from_f32<T>(c_reg);
+  }
+}
+
+template <typename K>
+int32_t launch_lds(K kernel, const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_rnn_recurrence: LDS of %zu bytes refused: %s", lds,
+                       hipGetErrorString(e));
+  }
+  kernel<<<grid, block, lds, st>>>(p);
+  return check_launch("wc_rnn_recurrence");
+}
+
+template <typename T, int CELL, int LG, int UPG>
+int32_t launch_kl(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  switch (p.kl) {
+    case 4: return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, 4>, p, grid, block, lds, st);
+    case 8: return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, 8>, p, grid, block, lds, st);
+    case 16: return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, 16>, p, grid, block, lds, st);
+    default: return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: %d columns per lane unsupported", p.kl);
+  }
+}
+
+template <typename T, int CELL, int LG>
+int32_t launch_upg(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  switch (p.upg) {
+    case 1: return launch_kl<T, CELL, LG, 1>(p, grid, block, lds, st);
+    case 2: return launch_kl<T, CELL, LG, 2>(p, grid, block, lds, st);
+    case 4: return launch_kl<T, CELL, LG, 4>(p, grid, block, lds, st);
+    default: return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: %d units per group unsupported", p.upg);
+  }
+}
+
+template <typename T, int CELL>
+int32_t launch_rec(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  if (p.lg == 8) return launch_upg<T, CELL, 8>(p, grid, block, lds, st);
+  return launch_upg<T, CELL, 16>(p, grid, block, lds, st);
+}
+
+inline int round4(int v) { return (v + 3) & ~3; }
+inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+}  // namespace
+}  // namespace wc
+
+using namespace wc;
+
+// Chooses the lane layout of the register-resident kernel; false when the
+// weights of one (model, batch row) do not fit the register file.
+static bool rnn_plan(int gates, int hid, RnnParams& p) {
+  for (int lg = 8; lg <= 16; lg <<= 1) {
+    const int kl = round4((hid + lg - 1) / lg);
+    if (kl > 16) continue;
+    for (int upg = 1; upg <= 4; upg <<= 1) {
+      const int threads = ((hid + upg - 1) / upg) * lg;
+      const int regs = gates * upg * kl;              // weight registers per lane
+      if (regs > 176) break;
+      if (round_up(threads, 64) > rnn_bound(gates, upg, kl)) continue;
+      p.lg = lg;
+      p.kl = kl;
+      p.upg = upg;
+      return true;
+    }
+  }
+  return false;
+}
+
+static int64_t rnn_ws_bytes(const wc_rnn_args* a) {
+  const int64_t gates = a->cell == WC_CELL_GRU ? 3 : 4;
+  return a->n * a->batch * a->steps * gates * a->hidden * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int64_t wc_rnn_workspace_bytes(const wc_rnn_args* a) {
+  if (!a || a->n < 0 || a->batch < 0 || a->steps < 0 || a->hidden < 0) return -1;
+  return rnn_ws_bytes(a);
+}
+
+static int32_t rnn_check(const wc_rnn_args* a, const char* what, RnnParams& p, int& gates) {
+  WC_REQUIRE(a != nullptr, WC_ERR_NULL, "%s: null args", what);
+  WC_REQUIRE(a->cell == WC_CELL_GRU || a->cell == WC_CELL_LSTM, WC_ERR_ARG, "%s: unknown cell %d", what,
+             a->cell);
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "%s: unsupported dtype %s", what,
+             dtype_name(a->dtype));
+  WC_REQUIRE(a->n >= 0 && a->batch >= 0 && a->steps >= 0 && a->input_size > 0 && a->hidden > 0,
+             WC_ERR_SHAPE, "%s: bad sizes", what);
+  gates = a->cell == WC_CELL_GRU ? 3 : 4;
+  WC_REQUIRE(a->n * a->batch < 0x7fffffffll && a->batch * a->steps < 0x7fffffffll &&
+                 gates * a->hidden < 0x7fffffffll && a->input_size < 0x7fffffffll,
+             WC_ERR_LIMIT, "%s: sizes too large", what);
+  p.n = (int)a->n;
+  p.batch = (int)a->batch;
+  p.steps = (int)a->steps;
+  p.in = (int)a->input_size;
+  p.hid = (int)a->hidden;
+  if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
+  WC_REQUIRE(a->workspace, WC_ERR_NULL, "%s: null workspace", what);
+  WC_REQUIRE(a->workspace_bytes >= rnn_ws_bytes(a), WC_ERR_ARG, "%s: workspace of %lld bytes < %lld needed",
+             what, (long long)a->workspace_bytes, (long long)rnn_ws_bytes(a));
+  WC_REQUIRE(aligned(a->workspace, 16), WC_ERR_ALIGN, "%s: workspace not 16-byte aligned", what);
+  return WC_OK;
+}
+
+extern "C" int32_t wc_rnn_input_projection(const wc_rnn_args* a, void* stream) {
+  clear_error();
+  RnnParams p;
+  int gates = 0;
+  int32_t rc = rnn_check(a, "wc_rnn_input_projection", p, gates);
+  if (rc) return rc;
+  if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
+  WC_REQUIRE(a->x && a->w_ih, WC_ERR_NULL, "wc_rnn_input_projection: null pointer");
+  const int G = gates * p.hid;
+  // gates_x = x W_ih^T + b_ih  ->  workspace [N, B*T, G] fp32
+  GemmParams g;
+  g.n = p.n;
+  g.m = p.batch * p.steps;
+  g.o = G;
+  g.k = p.in;
+  g.act = WC_ACT_NONE;
+  g.a = a->x;
+  g.a_sn = a->x_stride_n;
+  g.a_so = a->x_stride_b;
+  g.a_si = a->x_stride_t;
+  g.a_ri = make_fastdiv(static_cast<uint32_t>(p.steps));
+  g.w = a->w_ih;
+  g.w_sn = static_cast<int64_t>(G) * p.in;
+  g.bias = a->b_ih;
+  g.b_sn = G;
+  g.r = nullptr;
+  g.r_sn = g.r_so = g.r_si = 0;
+  g.c = a->workspace;
+  g.c_sn = static_cast<int64_t>(p.batch) * p.steps * G;
+  g.c_so = 0;
+  g.c_si = G;
+  g.c_ri = make_fastdiv(static_cast<uint32_t>(p.batch * p.steps));
+  return grouped_gemm(g, a->dtype, WC_F32, a->dtype, as_stream(stream));
+}
+
+extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
+  clear_error();
+  RnnParams p;
+  int gates = 0;
+  int32_t rc = rnn_check(a, "wc_rnn_recurrence", p, gates);
+  if (rc) return rc;
+  if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
+  WC_REQUIRE(a->w_hh && a->out, WC_ERR_NULL, "wc_rnn_recurrence: null pointer");
+  if (!rnn_plan(gates, p.hid, p))
+    return set_error(WC_ERR_LIMIT,
+                     "wc_rnn_recurrence: hidden=%d exceeds the register-resident recurrent kernel "
+                     "(W_hh of one model must fit the register file of one workgroup)",
+                     p.hid);
+  const int nwg = p.n * p.batch;
+  p.remap = (nwg % 8 == 0) ? 1 : 0;
+  p.gx = static_cast<const float*>(a->workspace);
+  p.w_hh = a->w_hh;
+  p.b_hh = a->b_hh;
+  p.h0 = a->h0;
+  p.c0 = a->c0;
+  p.out = a->out;
+  p.hn = a->h_n;
+  p.cn = a->c_n;
+  const int G = gates * p.hid;
+  const size_t fixed = sizeof(float) * 2 * static_cast<size_t>(p.lg) * (p.kl + 4);
+  const size_t per_step = sizeof(float) * static_cast<size_t>(G + p.hid);
+  if (fixed + per_step > static_cast<size_t>(kRnnLdsBudget))
+    return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: hidden=%d needs more LDS than available", p.hid);
+  p.xt = static_cast<int>((kRnnLdsBudget - fixed) / per_step);
+  if (p.xt > p.steps) p.xt = p.steps;
+  const int threads = round_up(((p.hid + p.upg - 1) / p.upg) * p.lg, 64);
+  const int es = dtype_size(a->dtype);
+  p.wvec = (aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && (p.kl * es) % 16 == 0) ? 1 : 0;
+  const dim3 grid(nwg), block(threads);
+  const size_t lds = fixed + per_step * static_cast<size_t>(p.xt);
+  hipStream_t st = as_stream(stream);
+  if (a->dtype == WC_F32) {
+    if (a->cell == WC_CELL_GRU) return launch_rec<float, WC_CELL_GRU>(p, grid, block, lds, st);
+    return launch_rec<float, WC_CELL_LSTM>(p, grid, block, lds, st);
+  }
+  if (a->cell == WC_CELL_GRU) return launch_rec<bf16, WC_CELL_GRU>(p, grid, block, lds, st);
+  return launch_rec<bf16, WC_CELL_LSTM>(p, grid, block, lds, st);
+}
+
+extern "C" int32_t wc_rnn_forward(const wc_rnn_args* a, void* stream) {
+  clear_error();
+  RnnParams p;
+  int gates = 0;
+  int32_t rc = rnn_check(a, "wc_rnn_forward", p, gates);
+  if (rc) return rc;
+  if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
+  // refuse sizes the recurrence cannot take before launching the projection
+  if (!rnn_plan(gates, p.hid, p))
+    return set_error(WC_ERR_LIMIT,
+                     "wc_rnn_forward: hidden=%d exceeds the register-resident recurrent kernel "
+                     "(W_hh of one model must fit the register file of one workgroup)",
+                     p.hid);
+  rc = wc_rnn_input_projection(a, stream);
+  if (rc) return rc;
+  return wc_rnn_recurrence(a, stream);
+}

@@ -1,0 +1,265 @@
+"""
+ctypes binding of libwide_hip.so, the gfx950 kernels behind every wide primitive.
+
+The library exposes a plain C ABI (see include/wc_abi.h at the repository root).  This
+module loads it once, declares the entry points, and offers thin Python wrappers that
+
+  * check that every tensor lives on a ROCm device, has the dtype / shape / inner
+    contiguity the kernel needs, and that no autograd graph is requested (the kernels
+    are forward-only);
+  * pass raw device pointers, sizes and strides plus torch's current HIP stream;
+  * turn a non-zero status into an exception carrying ``wc_last_error()``.
+
+There is no CPU path and no fallback: when the library is missing, or a tensor is on
+the CPU, the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import List, Optional, Sequence
+
+import torch
+from torch import Tensor
+
+ABI_VERSION = 1
+
+F32, BF16, F16 = 0, 1, 2
+ACT_NONE, ACT_RELU = 0, 1
+CELL_GRU, CELL_LSTM = 0, 1
+
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwide_hip.so")
+
+_lib = None
+
+
+class WideKernelError(RuntimeError):
+    """A libwide_hip.so entry point returned a non-zero status."""
+
+
+class _RnnArgs(ctypes.Structure):
+    _fields_ = [
+        ("cell", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("n", ctypes.c_int64), ("batch", ctypes.c_int64), ("steps", ctypes.c_int64),
+        ("input_size", ctypes.c_int64), ("hidden", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("x_stride_n", ctypes.c_int64), ("x_stride_b", ctypes.c_int64), ("x_stride_t", ctypes.c_int64),
+        ("w_ih", ctypes.c_void_p), ("w_hh", ctypes.c_void_p),
+        ("b_ih", ctypes.c_void_p), ("b_hh", ctypes.c_void_p),
+        ("h0", ctypes.c_void_p), ("c0", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("h_n", ctypes.c_void_p), ("c_n", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+class _GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("out_dtype", ctypes.c_int32),
+        ("bias_dtype", ctypes.c_int32), ("act", ctypes.c_int32),
+        ("n", ctypes.c_int64), ("m", ctypes.c_int64), ("o", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("a", ctypes.c_void_p),
+        ("a_stride_n", ctypes.c_int64), ("a_stride_outer", ctypes.c_int64),
+        ("a_stride_inner", ctypes.c_int64), ("a_rows_inner", ctypes.c_int64),
+        ("w", ctypes.c_void_p), ("w_stride_n", ctypes.c_int64),
+        ("bias", ctypes.c_void_p), ("bias_stride_n", ctypes.c_int64),
+        ("residual", ctypes.c_void_p),
+        ("r_stride_n", ctypes.c_int64), ("r_stride_outer", ctypes.c_int64), ("r_stride_inner", ctypes.c_int64),
+        ("c", ctypes.c_void_p),
+        ("c_stride_n", ctypes.c_int64), ("c_stride_outer", ctypes.c_int64),
+        ("c_stride_inner", ctypes.c_int64), ("c_rows_inner", ctypes.c_int64),
+    ]
+
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); the single source of truth for the exported ABI
+SIGNATURES = {
+    "wc_abi_version": (_I32, []),
+    "wc_last_error": (ctypes.c_char_p, []),
+    "wc_device_count": (_I32, []),
+    "wc_pack_rows": (_I32, [ctypes.POINTER(_P), ctypes.POINTER(_I64), _I64, _I64, _I64, _P, _P]),
+    "wc_swap01": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
+    "wc_embedding_gather": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _P, _P, _P]),
+    "wc_layernorm": (_I32, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I32, _I32, _P]),
+    "wc_bn_eval": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P]),
+    "wc_rnn_workspace_bytes": (_I64, [ctypes.POINTER(_RnnArgs)]),
+    "wc_rnn_forward": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
+    "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
+    "wc_rnn_recurrence": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
+    "wc_grouped_gemm": (_I32, [ctypes.POINTER(_GemmArgs), _P]),
+}
+
+
+def lib():
+    """Load libwide_hip.so (once) after torch's HIP runtime; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"wide_compiler: {LIB_PATH} is not built. Build it with "
+            f"`make -C {os.path.dirname(os.path.dirname(LIB_PATH))}` or __graft_entry__.build(); "
+            "this build has no fallback path."
+        )
+    # torch is imported first so its libamdhip64.so.7 is the runtime the library binds to
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    got = handle.wc_abi_version()
+    if got != ABI_VERSION:
+        raise ImportError(f"wide_compiler: libwide_hip.so ABI {got} != expected {ABI_VERSION}")
+    _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().wc_last_error().decode(errors="replace")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise WideKernelError(f"{what} failed (status {rc}): {last_error()}")
+
+
+def dtype_code(t: torch.dtype, what: str) -> int:
+    try:
+        return _DTYPES[t]
+    except KeyError:
+        raise TypeError(f"{what}: dtype {t} is not supported (float32, bfloat16, float16)") from None
+
+
+def require_device(what: str, *tensors: Optional[Tensor]) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                f"{what}: wide_compiler's MI355X build executes on ROCm device tensors only "
+                f"(got a tensor on {t.device}); move the model and inputs to 'cuda'"
+            )
+
+
+def require_forward_only(what: str, *tensors: Optional[Tensor]) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise RuntimeError(
+            f"{what}: the HIP wide kernels are forward-only; run under torch.no_grad() or "
+            "torch.inference_mode()"
+        )
+
+
+def stream_of(t: Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------------------
+# wrappers
+# ---------------------------------------------------------------------------------------
+
+def pack_rows(srcs: Sequence[Tensor], dst: Tensor, rows: int, row_bytes: int,
+              row_strides_bytes: Sequence[int]) -> None:
+    n = len(srcs)
+    arr_p = (_P * n)(*[s.data_ptr() for s in srcs])
+    arr_s = (_I64 * n)(*row_strides_bytes)
+    _check(lib().wc_pack_rows(arr_p, arr_s, n, rows, row_bytes, dst.data_ptr(), stream_of(dst)),
+           "wc_pack_rows")
+
+
+def swap01(src: Tensor, d0: int, d1: int, s0_bytes: int, s1_bytes: int, inner_bytes: int,
+           dst: Tensor) -> None:
+    _check(lib().wc_swap01(src.data_ptr(), d0, d1, s0_bytes, s1_bytes, inner_bytes, dst.data_ptr(),
+                           stream_of(src)), "wc_swap01")
+
+
+def embedding_gather(weight: Tensor, ids: Tensor, out: Tensor, shared: bool,
+                     err_flag: Optional[Tensor] = None) -> None:
+    n, vocab, dim = weight.shape
+    rows = ids.numel() if shared else ids.numel() // max(n, 1)
+    _check(lib().wc_embedding_gather(weight.data_ptr(), n, vocab, dim, dtype_code(weight.dtype, "embedding"),
+                                     ids.data_ptr(), rows, 1 if shared else 0, out.data_ptr(),
+                                     ptr(err_flag), stream_of(weight)), "wc_embedding_gather")
+
+
+def layernorm(x: Tensor, x_ms: int, x_rs: int, gamma: Tensor, beta: Optional[Tensor], y: Tensor,
+              y_ms: int, y_rs: int, n: int, rows_per_model: int, dim: int, eps: float) -> None:
+    _check(lib().wc_layernorm(x.data_ptr(), x_ms, x_rs, gamma.data_ptr(), ptr(beta), y.data_ptr(), y_ms, y_rs,
+                              n, rows_per_model, dim, float(eps), dtype_code(x.dtype, "layernorm"),
+                              dtype_code(gamma.dtype, "layernorm"), stream_of(x)), "wc_layernorm")
+
+
+def bn_eval(x: Tensor, xsn: int, xsb: int, weight: Optional[Tensor], bias: Optional[Tensor],
+            rmean: Tensor, rvar: Tensor, eps: float, y: Tensor, n: int, b: int, c: int, hw: int,
+            relu: bool = False) -> None:
+    _check(lib().wc_bn_eval(x.data_ptr(), xsn, xsb, ptr(weight), ptr(bias), rmean.data_ptr(), rvar.data_ptr(),
+                            float(eps), y.data_ptr(), n, b, c, hw, dtype_code(x.dtype, "batchnorm"),
+                            dtype_code(rmean.dtype, "batchnorm"), ACT_RELU if relu else ACT_NONE,
+                            stream_of(x)), "wc_bn_eval")
+
+
+def grouped_gemm(*, n: int, m: int, o: int, k: int,
+                 a: Tensor, a_sn: int, a_so: int, a_si: int, a_rows_inner: int,
+                 w: Tensor, w_sn: int,
+                 c: Tensor, c_sn: int, c_so: int, c_si: int, c_rows_inner: int,
+                 bias: Optional[Tensor] = None, bias_sn: int = 0,
+                 residual: Optional[Tensor] = None, r_sn: int = 0, r_so: int = 0, r_si: int = 0,
+                 relu: bool = False) -> None:
+    g = _GemmArgs()
+    g.dtype = dtype_code(a.dtype, "grouped_gemm")
+    g.out_dtype = dtype_code(c.dtype, "grouped_gemm")
+    g.bias_dtype = dtype_code(bias.dtype, "grouped_gemm") if bias is not None else g.dtype
+    g.act = ACT_RELU if relu else ACT_NONE
+    g.n, g.m, g.o, g.k = n, m, o, k
+    g.a, g.a_stride_n, g.a_stride_outer, g.a_stride_inner, g.a_rows_inner = a.data_ptr(), a_sn, a_so, a_si, a_rows_inner
+    g.w, g.w_stride_n = w.data_ptr(), w_sn
+    g.bias, g.bias_stride_n = ptr(bias), bias_sn
+    g.residual, g.r_stride_n, g.r_stride_outer, g.r_stride_inner = ptr(residual), r_sn, r_so, r_si
+    g.c, g.c_stride_n, g.c_stride_outer, g.c_stride_inner, g.c_rows_inner = c.data_ptr(), c_sn, c_so, c_si, c_rows_inner
+    _check(lib().wc_grouped_gemm(ctypes.byref(g), stream_of(a)), "wc_grouped_gemm")
+
+
+def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional[Tensor],
+             b_hh: Optional[Tensor], h0: Optional[Tensor], c0: Optional[Tensor], out: Tensor,
+             h_n: Optional[Tensor], c_n: Optional[Tensor], workspace: Optional[Tensor] = None):
+    """Fill the wc_rnn_args struct; allocates the fp32 workspace unless one is given.
+    Returns (args, workspace)."""
+    n, batch, steps, in_size = x.shape
+    hidden = w_hh.shape[-1]
+    a = _RnnArgs()
+    a.cell = cell
+    a.dtype = dtype_code(x.dtype, "rnn")
+    a.n, a.batch, a.steps, a.input_size, a.hidden = n, batch, steps, in_size, hidden
+    a.x = x.data_ptr()
+    a.x_stride_n, a.x_stride_b, a.x_stride_t = x.stride(0), x.stride(1), x.stride(2)
+    a.w_ih, a.w_hh, a.b_ih, a.b_hh = w_ih.data_ptr(), w_hh.data_ptr(), ptr(b_ih), ptr(b_hh)
+    a.h0, a.c0 = ptr(h0), ptr(c0)
+    a.out, a.h_n, a.c_n = out.data_ptr(), ptr(h_n), ptr(c_n)
+    need = int(lib().wc_rnn_workspace_bytes(ctypes.byref(a)))
+    ws = workspace
+    if ws is None or ws.numel() * ws.element_size() < need:
+        ws = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
+    return a, ws
+
+
+def rnn_forward(**kw) -> None:
+    a, ws = rnn_args(**kw)
+    _check(lib().wc_rnn_forward(ctypes.byref(a), stream_of(kw["x"])), "wc_rnn_forward")
+
+
+def rnn_phase(a: _RnnArgs, phase: str, like: Tensor) -> None:
+    """Run one phase ('input_projection' or 'recurrence') of a prepared rnn_args struct."""
+    fn = getattr(lib(), f"wc_rnn_{phase}")
+    _check(fn(ctypes.byref(a), stream_of(like)), f"wc_rnn_{phase}")
+
+
+def exported_symbols() -> List[str]:
+    return list(SIGNATURES)

@@ -1,0 +1,141 @@
+"""
+WideLinear: N independent nn.Linear layers as one grouped MFMA GEMM
+(mirror of wide_compiler/core/primitives/wide_linear.py:35-229).
+
+    x [N, *batch, I]  ->  y [N, *batch, O],   y[i] = x[i] @ weight[i].T + bias[i]
+
+Parameters keep the reference layout (weight [N, O, I], bias [N, O]).  Every strategy
+('einsum', 'sequential', 'auto') is accepted and recorded, and all of them execute the
+same kernel, wc_grouped_gemm (fp32 accumulation; bias and an optional fused ReLU in the
+epilogue).  N-first inputs are read through their strides, so the channel-packed boundary
+view [B, N*I] -> [N, B, I] costs no copy.
+"""
+
+from __future__ import annotations
+
+import math
+from enum import Enum
+from typing import List, Optional, Union
+
+import torch
+from torch import Tensor, nn
+
+from ... import _hip
+from .._layout import rows_of, rows_or_contiguous
+
+
+class LinearStrategy(Enum):
+    EINSUM = "einsum"
+    SEQUENTIAL = "sequential"
+    AUTO = "auto"
+
+
+# Thresholds of the reference's heuristic (wide_linear.py:42-47); they only decide the
+# recorded strategy label here.
+LINEAR_THRESHOLDS = {
+    "n_min_einsum": 8,
+    "b_max_for_low_n": 64,
+    "expansion_max": 8.0,
+    "vocab_size": 10000,
+}
+
+
+def select_linear_strategy(n: int, b: int, in_features: int, out_features: int) -> LinearStrategy:
+    """The reference's label heuristic (wide_linear.py:50-69)."""
+    t = LINEAR_THRESHOLDS
+    if n < t["n_min_einsum"] and b > t["b_max_for_low_n"]:
+        return LinearStrategy.SEQUENTIAL
+    if out_features >= t["vocab_size"]:
+        return LinearStrategy.SEQUENTIAL
+    return LinearStrategy.EINSUM
+
+
+class WideLinear(nn.Module):
+    def __init__(self, n: int, in_features: int, out_features: int, bias: bool = True,
+                 strategy: Union[str, LinearStrategy] = "auto"):
+        super().__init__()
+        self.n = n
+        self.in_features = in_features
+        self.out_features = out_features
+        self.has_bias = bias
+        if isinstance(strategy, str):
+            strategy = LinearStrategy(strategy)
+        if strategy == LinearStrategy.AUTO:
+            strategy = select_linear_strategy(n, 32, in_features, out_features)
+        self._strategy = strategy
+        self.weight = nn.Parameter(torch.empty(n, out_features, in_features))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(n, out_features))
+        else:
+            self.register_parameter("bias", None)
+        # epilogue activation fused in by TracedWideModel ("relu" or None)
+        self.fused_activation: Optional[str] = None
+        self._reset_parameters()
+
+    @property
+    def strategy(self) -> LinearStrategy:
+        return self._strategy
+
+    def _reset_parameters(self) -> None:
+        bound = 1.0 / math.sqrt(self.in_features) if self.in_features > 0 else 0.0
+        for i in range(self.n):
+            nn.init.kaiming_uniform_(self.weight[i], a=math.sqrt(5))
+            if self.bias is not None:
+                nn.init.uniform_(self.bias[i], -bound, bound)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.forward_into(x, None, relu=self.fused_activation == "relu")
+
+    def forward_into(self, x: Tensor, out: Optional[Tensor], relu: bool = False) -> Tensor:
+        """Run the GEMM, writing into ``out`` (any view with unit inner stride) if given."""
+        what = "WideLinear"
+        if x.dim() < 2 or x.shape[0] != self.n or x.shape[-1] != self.in_features:
+            raise RuntimeError(
+                f"{what}: expected input [N={self.n}, ..., {self.in_features}], got {list(x.shape)}"
+            )
+        w = self.weight
+        b = self.bias
+        _hip.require_device(what, x, w, b)
+        _hip.require_forward_only(what, x, w, b)
+        if x.dtype != w.dtype:
+            raise RuntimeError(f"{what}: input dtype {x.dtype} != weight dtype {w.dtype}")
+        x, r = rows_or_contiguous(x)
+        batch = tuple(x.shape[1:-1])
+        if out is None:
+            out = torch.empty((self.n, *batch, self.out_features), dtype=x.dtype, device=x.device)
+        cr = rows_of(out)
+        if cr is None or tuple(out.shape) != (self.n, *batch, self.out_features):
+            raise RuntimeError(f"{what}: output view {list(out.shape)} is not addressable")
+        if r.rows == 0 or self.out_features == 0:
+            return out
+        w = w if w.is_contiguous() else w.contiguous()
+        _hip.grouped_gemm(
+            n=self.n, m=r.rows, o=self.out_features, k=self.in_features,
+            a=x, a_sn=r.stride_n, a_so=r.stride_outer, a_si=r.stride_inner, a_rows_inner=r.rows_inner,
+            w=w, w_sn=self.out_features * self.in_features,
+            c=out, c_sn=cr.stride_n, c_so=cr.stride_outer, c_si=cr.stride_inner, c_rows_inner=cr.rows_inner,
+            bias=b, bias_sn=self.out_features, relu=relu,
+        )
+        return out
+
+    @classmethod
+    def from_modules(cls, modules: List[nn.Linear],
+                     strategy: Union[str, LinearStrategy] = "auto") -> "WideLinear":
+        t = modules[0]
+        wide = cls(n=len(modules), in_features=t.in_features, out_features=t.out_features,
+                   bias=t.bias is not None, strategy=strategy)
+        wide = wide.to(device=t.weight.device, dtype=t.weight.dtype)
+        with torch.no_grad():
+            for i, m in enumerate(modules):
+                wide.weight[i].copy_(m.weight)
+                if m.bias is not None:
+                    wide.bias[i].copy_(m.bias)
+        return wide
+
+    def __repr__(self) -> str:
+        act = ", +relu" if self.fused_activation == "relu" else ""
+        return (f"WideLinear({self.n}x[{self.in_features}->{self.out_features}], "
+                f"strategy={self._strategy.value}{act})")
+
+
+__all__ = ["WideLinear", "LinearStrategy", "select_linear_strategy", "LINEAR_THRESHOLDS"]

@@ -1,0 +1,465 @@
+"""
+TracedWideModel: N structurally identical models traced with torch.fx and rebuilt as one
+wide model whose stages are wide primitives (mirror of wide_compiler/core/traced_wide.py:
+94-573).
+
+Boundary layout (traced_wide.py:450-534): the forward takes a channel-packed tensor
+[B, N*C, *S], walks the stages on N-first tensors [N, B, C, *S], and returns [B, N*C, *S].
+
+This build differs from the reference in three places, none of which changes results
+beyond floating-point rounding:
+
+* Module types are resolved through the global WideRegistry first (then WIDE_BUILDERS), so
+  user-registered primitives are honoured.
+* A fusion pass folds ReLU, eval-mode BatchNorm and a residual ``+`` into the epilogue of
+  the wide kernel that produces their input when that input has no other consumer (e.g.
+  Linear->ReLU, Conv->BN->ReLU, Conv->BN->(+x)->ReLU).  The folded stages become aliases.
+* Boundaries cost no extra pass where avoidable: the N-first input is a strided view that
+  the first kernel reads in place, and when the last stage is a WideLinear it writes the
+  packed output layout directly; otherwise the output is transposed once by wc_swap01.
+"""
+
+from __future__ import annotations
+
+import operator
+from dataclasses import dataclass
+from typing import Any, Callable, Dict, List, Optional, Tuple
+
+import torch
+import torch.fx as fx
+import torch.nn as nn
+import torch.nn.functional as F
+from torch import Tensor
+
+from .. import _hip
+from .ensemble_util import pack_inputs, unpack_outputs  # noqa: F401  (re-exported like upstream)
+from .primitives import (
+    WideAttention, WideBatchNorm1d, WideBatchNorm2d, WideConv1d, WideConv2d, WideConv3d, WideEmbedding,
+    WideGRU, WideGroupNorm, WideInstanceNorm1d, WideInstanceNorm2d, WideLayerNorm, WideLinear, WideLSTM,
+)
+from .registry import get_registry
+
+WIDE_BUILDERS = {
+    "Linear": WideLinear.from_modules,
+    "Conv1d": WideConv1d.from_modules,
+    "Conv2d": WideConv2d.from_modules,
+    "Conv3d": WideConv3d.from_modules,
+    "BatchNorm1d": WideBatchNorm1d.from_modules,
+    "BatchNorm2d": WideBatchNorm2d.from_modules,
+    "LayerNorm": WideLayerNorm.from_modules,
+    "GroupNorm": WideGroupNorm.from_modules,
+    "InstanceNorm1d": WideInstanceNorm1d.from_modules,
+    "InstanceNorm2d": WideInstanceNorm2d.from_modules,
+    "Embedding": WideEmbedding.from_modules,
+    "MultiheadAttention": WideAttention.from_modules,
+    "GRU": WideGRU.from_modules,
+    "LSTM": WideLSTM.from_modules,
+}
+
+
+@dataclass
+class TraceNode:
+    order: int
+    op: str
+    name: str
+    target: Any
+    args: Tuple
+    kwargs: Dict
+
+
+def analyze_trace(graph: fx.Graph) -> List[TraceNode]:
+    return [TraceNode(i, nd.op, nd.name, nd.target, nd.args, dict(nd.kwargs))
+            for i, nd in enumerate(graph.nodes)]
+
+
+def print_trace(traced: fx.GraphModule) -> str:
+    lines = ["FX Trace:", "=" * 60]
+    for nd in traced.graph.nodes:
+        if nd.op == "placeholder":
+            lines.append(f"  [input] {nd.name}")
+        elif nd.op == "call_module":
+            lines.append(f"  [module] {nd.target}")
+        elif nd.op == "call_function":
+            lines.append(f"  [func] {getattr(nd.target, '__name__', str(nd.target))}")
+        elif nd.op == "call_method":
+            lines.append(f"  [method] .{nd.target}()")
+        elif nd.op == "get_attr":
+            lines.append(f"  [attr] {nd.target}")
+        elif nd.op == "output":
+            lines.append("  [output]")
+    return "\n".join(lines)
+
+
+class FunctionalOp(nn.Module):
+    """A traced function / method / unknown module applied to N-first tensors."""
+
+    def __init__(self, fn: Callable, name: str = ""):
+        super().__init__()
+        self.fn = fn
+        self.name = name or getattr(fn, "__name__", "func")
+
+    def forward(self, *args, **kwargs):
+        return self.fn(*args, **kwargs)
+
+    def __repr__(self) -> str:
+        return f"FunctionalOp({self.name})"
+
+
+class BinaryOp(nn.Module):
+    _OPS = {"add": operator.add, "mul": operator.mul, "sub": operator.sub,
+            "div": operator.truediv, "matmul": operator.matmul}
+
+    def __init__(self, op: str):
+        super().__init__()
+        self.op = op
+
+    def forward(self, a: Tensor, b: Tensor) -> Tensor:
+        fn = self._OPS.get(self.op)
+        if fn is None:
+            raise ValueError(f"Unknown op: {self.op}")
+        return fn(a, b)
+
+    def __repr__(self) -> str:
+        return f"BinaryOp({self.op})"
+
+
+class GetAttrOp(nn.Module):
+    def __init__(self, name: str):
+        super().__init__()
+        self.attr_name = name
+
+    def forward(self, value: Tensor) -> Tensor:
+        return value
+
+    def __repr__(self) -> str:
+        return f"GetAttrOp({self.attr_name})"
+
+
+@dataclass
+class WideStage:
+    order: int
+    name: str
+    op_type: str
+    target: str
+    wide_op: nn.Module
+    n: int
+    num_inputs: int = 1
+
+
+def _get_nested_attr(obj: Any, path: str) -> Any:
+    for part in path.split("."):
+        obj = getattr(obj, part)
+    return obj
+
+
+_RELU_FNS = (F.relu, torch.relu)
+
+
+def _method_caller(name: str):
+    def caller(x, *args, **kwargs):
+        return getattr(x, name)(*args, **kwargs)
+    return caller
+
+
+class TracedWideModel(nn.Module):
+    def __init__(self, n: int):
+        super().__init__()
+        self.n = n
+        self.stages: nn.ModuleDict = nn.ModuleDict()
+        self.stage_info: Dict[str, WideStage] = {}
+        self._graph: Optional[fx.Graph] = None
+        self._execution_order: List[str] = []
+        self._node_args: Dict[str, Tuple] = {}
+        self._node_kwargs: Dict[str, Dict] = {}
+        self._input_name: str = "x"
+        self._output_name: str = ""
+        self._attr_names: List[str] = []
+        # fusion bookkeeping: alias -> source node; conv stage -> residual node
+        self._aliases: Dict[str, str] = {}
+        self._residual_of: Dict[str, str] = {}
+        self._relu_kind: Dict[str, str] = {}
+
+    # ----------------------------------------------------------------------------------
+    @classmethod
+    def from_models(cls, models: List[nn.Module], sample_input: Tensor, fuse: bool = True) -> "TracedWideModel":
+        n = len(models)
+        wide = cls(n)
+        template = models[0]
+        try:
+            traced = fx.symbolic_trace(template)
+        except Exception as e:  # noqa: BLE001 - reported as in the reference
+            raise RuntimeError(f"FX tracing failed: {e}. Model may have dynamic control flow.")
+        wide._graph = traced.graph
+
+        for nd in traced.graph.nodes:
+            if nd.op != "get_attr":
+                continue
+            attrs: Optional[List[Tensor]] = []
+            for m in models:
+                try:
+                    a = _get_nested_attr(m, nd.target)
+                except AttributeError:
+                    attrs = None
+                    break
+                if not isinstance(a, Tensor):
+                    attrs = None
+                    break
+                attrs.append(a.data if isinstance(a, nn.Parameter) else a)
+            safe = nd.name.replace(".", "_")
+            if attrs is not None and len(attrs) == n:
+                merged = torch.stack(attrs) if attrs[0].dim() == 0 else torch.cat(attrs, dim=0)
+                wide.register_buffer(f"_attr_{safe}", merged)
+                wide._attr_names.append(nd.name)
+            else:
+                try:
+                    a = _get_nested_attr(template, nd.target)
+                except AttributeError:
+                    a = None
+                if isinstance(a, Tensor):
+                    wide.register_buffer(f"_attr_{safe}", a.clone())
+                    wide._attr_names.append(nd.name)
+
+        registry = get_registry()
+        for nd in traced.graph.nodes:
+            op = None
+            if nd.op == "placeholder":
+                wide._input_name = nd.name
+                continue
+            if nd.op == "output":
+                if nd.args:
+                    a0 = nd.args[0]
+                    wide._output_name = a0.name if hasattr(a0, "name") else str(a0)
+                continue
+            if nd.op == "get_attr":
+                wide._execution_order.append(nd.name)
+                wide._node_args[nd.name] = ()
+                wide._node_kwargs[nd.name] = {}
+                continue
+            if nd.op == "call_module":
+                modules = [m.get_submodule(nd.target) for m in models]
+                mtype = type(modules[0]).__name__
+                builder = registry.get_builder(mtype) or WIDE_BUILDERS.get(mtype)
+                if builder is not None:
+                    op = builder(modules)
+                else:
+                    op = FunctionalOp(lambda x, m=modules[0]: m(x), f"Passthrough({mtype})")
+                    if isinstance(modules[0], nn.ReLU):
+                        op.is_relu = True
+            elif nd.op == "call_function":
+                fn = nd.target
+                if fn is operator.add or fn is torch.add:
+                    op = BinaryOp("add")
+                elif fn is operator.mul or fn is torch.mul:
+                    op = BinaryOp("mul")
+                elif fn is operator.sub:
+                    op = BinaryOp("sub")
+                elif fn is operator.truediv:
+                    op = BinaryOp("div")
+                elif fn is torch.matmul or fn is operator.matmul:
+                    op = BinaryOp("matmul")
+                else:
+                    op = FunctionalOp(fn, getattr(fn, "__name__", str(fn)))
+                    if fn in _RELU_FNS:
+                        op.is_relu = True
+            elif nd.op == "call_method":
+                op = FunctionalOp(_method_caller(nd.target), f".{nd.target}()")
+                if nd.target in ("relu", "relu_"):
+                    op.is_relu = True
+            if op is None:
+                continue
+            arg_names = [a.name if hasattr(a, "name") else a for a in nd.args]
+            kw = {k: (v.name if hasattr(v, "name") else v) for k, v in nd.kwargs.items()}
+            stage = WideStage(order=len(wide._execution_order), name=nd.name, op_type=nd.op,
+                              target=str(nd.target), wide_op=op, n=n, num_inputs=len(arg_names))
+            wide.stages[nd.name.replace(".", "_")] = op
+            wide.stage_info[nd.name] = stage
+            wide._execution_order.append(nd.name)
+            wide._node_args[nd.name] = tuple(arg_names)
+            wide._node_kwargs[nd.name] = kw
+
+        if fuse:
+            wide._fuse_epilogues()
+        return wide
+
+    # ----------------------------------------------------------------------------------
+    def _users(self) -> Dict[str, List[str]]:
+        users: Dict[str, List[str]] = {}
+        for name in self._execution_order:
+            for a in list(self._node_args.get(name, ())) + list(self._node_kwargs.get(name, {}).values()):
+                if isinstance(a, str):
+                    users.setdefault(a, []).append(name)
+        if self._output_name:
+            users.setdefault(self._output_name, []).append("<output>")
+        return users
+
+    def _resolve(self, name: str) -> str:
+        while name in self._aliases:
+            name = self._aliases[name]
+        return name
+
+    def _op(self, name: str) -> Optional[nn.Module]:
+        return self.stages[name.replace(".", "_")] if name in self.stage_info else None
+
+    def _fuse_epilogues(self) -> None:
+        """Fold BN / residual add / ReLU into the producing kernel (single-consumer chains)."""
+        order = {name: i for i, name in enumerate(self._execution_order)}
+        users = self._users()
+
+        def sole_user(src: str, user: str) -> bool:
+            u = users.get(src, [])
+            return len(u) == 1 and u[0] == user
+
+        for name in self._execution_order:
+            if name not in self.stage_info or name in self._aliases:
+                continue
+            op = self._op(name)
+            args = self._node_args[name]
+            kwargs = self._node_kwargs[name]
+            # eval BatchNorm following a conv -> conv epilogue
+            if isinstance(op, (WideBatchNorm2d, WideBatchNorm1d)) and len(args) == 1 and not kwargs:
+                src = self._resolve(args[0]) if isinstance(args[0], str) else None
+                prod = self._op(src) if src else None
+                if isinstance(prod, (WideConv2d, WideConv1d)) and prod.fused_bn is None and \
+                        prod.fused_activation is None and src not in self._residual_of and \
+                        sole_user(args[0], name):
+                    prod.fused_bn = op
+                    self._aliases[name] = args[0]
+                continue
+            # residual add after a conv (+ folded BN) -> conv epilogue
+            if isinstance(op, BinaryOp) and op.op == "add" and len(args) == 2 and not kwargs:
+                for main, other in ((args[0], args[1]), (args[1], args[0])):
+                    if not (isinstance(main, str) and isinstance(other, str)):
+                        continue
+                    src = self._resolve(main)
+                    prod = self._op(src)
+                    other_src = self._resolve(other)
+                    if isinstance(prod, (WideConv2d, WideConv1d)) and prod.fused_activation is None and \
+                            src not in self._residual_of and sole_user(main, name) and \
+                            order.get(other_src, -1) < order[src] and other_src != src:
+                        self._residual_of[src] = other
+                        self._aliases[name] = main
+                        break
+                continue
+            # ReLU -> producer epilogue
+            if getattr(op, "is_relu", False) and len(args) == 1 and isinstance(args[0], str):
+                if any(k != "inplace" for k in kwargs):
+                    continue
+                src = self._resolve(args[0])
+                prod = self._op(src)
+                if isinstance(prod, (WideLinear, WideConv2d, WideConv1d, WideBatchNorm2d, WideBatchNorm1d)) and \
+                        prod.fused_activation is None and sole_user(args[0], name):
+                    prod.fused_activation = "relu"
+                    self._aliases[name] = args[0]
+
+    # ----------------------------------------------------------------------------------
+    def forward(self, x: Tensor) -> Tensor:
+        b = x.shape[0]
+        c = x.shape[1] // self.n
+        spatial = tuple(x.shape[2:])
+        xn = x.view(b, self.n, c, *spatial).movedim(1, 0)  # N-first view, read in place
+        values: Dict[str, Any] = {self._input_name: xn}
+        for attr in self._attr_names:
+            buf = f"_attr_{attr.replace('.', '_')}"
+            if hasattr(self, buf):
+                values[attr] = getattr(self, buf)
+
+        out_name = self._resolve(self._output_name) if self._output_name else ""
+        packed_out: Optional[Tensor] = None
+        for name in self._execution_order:
+            if name in self._attr_names or name not in self.stage_info:
+                continue
+            if name in self._aliases:
+                values[name] = values[self._aliases[name]]
+                continue
+            op = self.stages[name.replace(".", "_")]
+            args = [values[a] if isinstance(a, str) and a in values else a for a in self._node_args[name]]
+            kwargs = {k: (values[v] if isinstance(v, str) and v in values else v)
+                      for k, v in self._node_kwargs.get(name, {}).items()}
+            if name in self._residual_of:
+                kwargs["residual"] = values[self._residual_of[name]]
+            if name == out_name and isinstance(op, WideLinear) and not kwargs and len(args) == 1 \
+                    and isinstance(args[0], Tensor) and args[0].dim() >= 3:
+                packed_out, values[name] = self._linear_into_packed(op, args[0])
+                continue
+            if kwargs:
+                values[name] = op(*args, **kwargs)
+            elif len(args) == 1:
+                values[name] = op(args[0])
+            else:
+                values[name] = op(*args)
+
+        if packed_out is not None:
+            return packed_out
+        out = values[self._output_name]
+        if isinstance(out, tuple):
+            out = out[0]
+        return self._to_packed(out)
+
+    def _linear_into_packed(self, op: WideLinear, x: Tensor) -> Tuple[Tensor, Tensor]:
+        """Run the final WideLinear writing straight into the packed [B, N*C, *S] layout;
+        returns (packed, N-first view of it)."""
+        n, b = x.shape[0], x.shape[1]
+        mid = tuple(x.shape[2:-1])
+        o = op.out_features
+        nf_shape = (n, b, *mid, o)            # the N-first result
+        c = nf_shape[2]
+        packed = torch.empty((b, n * c, *nf_shape[3:]), dtype=x.dtype, device=x.device)
+        view = packed.view(b, n, *nf_shape[2:]).movedim(1, 0)
+        op.forward_into(x, view, relu=op.fused_activation == "relu")
+        return packed, view
+
+    def _to_packed(self, out: Tensor) -> Tensor:
+        """[N, B, C, *S] -> [B, N*C, *S] (traced_wide.py:527-532) with one wc_swap01 at most."""
+        n, b = out.shape[0], out.shape[1]
+        c = out.shape[2]
+        spatial = tuple(out.shape[3:])
+        moved = out.movedim(0, 1)
+        if moved.is_contiguous():
+            return moved.reshape(b, n * c, *spatial)
+        _hip.require_device("TracedWideModel", out)
+        inner = c
+        for s in spatial:
+            inner *= s
+        src = out
+        # each (n, b) block [C, *S] must be dense for the transpose kernel
+        expected, ok = 1, True
+        for size, stride in reversed(list(zip(out.shape[2:], out.stride()[2:]))):
+            if size != 1 and stride != expected:
+                ok = False
+                break
+            expected *= size
+        if not ok:
+            src = out.contiguous()
+        dst = torch.empty((b, n * c, *spatial), dtype=out.dtype, device=out.device)
+        if dst.numel():
+            es = out.element_size()
+            _hip.swap01(src, n, b, src.stride(0) * es, src.stride(1) * es, inner * es, dst)
+        return dst
+
+    # ----------------------------------------------------------------------------------
+    def summary(self) -> str:
+        lines = [f"TracedWideModel: {self.n} models", "=" * 60,
+                 f"Stages: {len(self.stages)}", f"Attrs: {len(self._attr_names)}", ""]
+        total = 0
+        for name in self._execution_order:
+            if name in self._attr_names:
+                buf = f"_attr_{name.replace('.', '_')}"
+                if hasattr(self, buf):
+                    lines.append(f"  [attr] {name}: {list(getattr(self, buf).shape)}")
+                continue
+            if name not in self.stage_info:
+                continue
+            st = self.stage_info[name]
+            op = self.stages[name.replace(".", "_")]
+            params = sum(p.numel() for p in op.parameters())
+            total += params
+            args = ", ".join(str(a) for a in self._node_args[name])
+            note = f"  -> fused into {self._aliases[name]}" if name in self._aliases else ""
+            lines.append(f"  [{st.order}] {name}({args}): {type(op).__name__} ({params:,} params){note}")
+        lines.append("")
+        lines.append(f"Total: {total:,} params ({total // max(self.n, 1):,} per model)")
+        return "\n".join(lines)
+
+
+__all__ = ["TraceNode", "analyze_trace", "print_trace", "FunctionalOp", "BinaryOp", "GetAttrOp",
+           "WideStage", "TracedWideModel", "WIDE_BUILDERS"]

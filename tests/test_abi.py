@@ -1,0 +1,81 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point declared in
+include/wc_abi.h, and rejects bad arguments on the host with a negative status + message."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "wc_abi.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "wc_rnn_forward" in names and "wc_grouped_gemm" in names and "wc_pack_rows" in names
+
+
+def test_library_exports_every_declared_symbol(hip):
+    lib = hip.lib()
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python binding declares exactly the header's entry points
+    assert sorted(hip.SIGNATURES) == _declared()
+
+
+def test_abi_version(hip):
+    assert hip.lib().wc_abi_version() == hip.ABI_VERSION
+
+
+def test_null_args_rejected_on_host(hip):
+    lib = hip.lib()
+    assert lib.wc_rnn_forward(None, None) == -1
+    assert "null" in hip.last_error()
+    assert lib.wc_grouped_gemm(None, None) == -1
+
+
+def test_bad_dtype_rejected_on_host(hip):
+    a = hip._RnnArgs()
+    a.cell, a.dtype = hip.CELL_GRU, 7
+    a.n, a.batch, a.steps, a.input_size, a.hidden = 1, 1, 1, 1, 1
+    assert hip.lib().wc_rnn_forward(ctypes.byref(a), None) == -3
+    assert "dtype" in hip.last_error()
+
+
+def test_rnn_limit_and_workspace_checks(hip):
+    a = hip._RnnArgs()
+    a.cell, a.dtype = hip.CELL_LSTM, hip.F32
+    a.n, a.batch, a.steps, a.input_size, a.hidden = 2, 3, 4, 8, 16
+    assert hip.lib().wc_rnn_workspace_bytes(ctypes.byref(a)) == 2 * 3 * 4 * 64 * 4
+    a.x = a.w_ih = a.w_hh = a.out = 16  # never dereferenced: rejected before any launch
+    a.workspace, a.workspace_bytes = 16, 8
+    assert hip.lib().wc_rnn_forward(ctypes.byref(a), None) == -6
+    assert "workspace" in hip.last_error()
+
+
+def test_gemm_arg_checks(hip):
+    g = hip._GemmArgs()
+    g.dtype = g.out_dtype = g.bias_dtype = hip.F32
+    g.n, g.m, g.o, g.k = 1, 4, 4, 4
+    g.a = g.w = g.c = 16
+    g.a_rows_inner = 0
+    g.c_rows_inner = 4
+    assert hip.lib().wc_grouped_gemm(ctypes.byref(g), None) == -6
+    g.a_rows_inner = 4
+    g.act = 9
+    assert hip.lib().wc_grouped_gemm(ctypes.byref(g), None) == -6
+
+
+def test_empty_problems_are_noops(hip):
+    lib = hip.lib()
+    assert lib.wc_swap01(None, 0, 5, 0, 0, 16, None, None) == 0
+    assert lib.wc_pack_rows(None, None, 0, 3, 8, None, None) == 0
+    assert lib.wc_layernorm(None, 0, 0, None, None, None, 0, 0, 0, 4, 8, 1e-5, 0, 0, None) == 0

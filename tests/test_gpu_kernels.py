@@ -1,0 +1,328 @@
+"""
+GPU parity of the HIP kernels against the oracle (the CPU restatement of the reference wide
+path) on the same seeded inputs.  Integer / byte work is compared bit-exactly; floating
+point by the normwise relative error max|a-b|/max|ref| against TOL_F32 = 1e-5 (fp32) and
+TOL_BF16 = 2e-2 (bf16), computed against the oracle run in float64 on the same (rounded)
+inputs, and for bf16 additionally against the reference's own bf16 path.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import bytes_ref, wide_ref
+from tests._util import TOL_BF16, TOL_F32, gen, rel_err, tol
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def _rand(shape, g, dtype=torch.float32, scale=1.0):
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+# ----------------------------------------------------------------------------- pack / boundary
+@pytest.mark.parametrize("shape,n", [((32, 64), 100), ((8, 64, 4, 4), 10), ((3, 5), 7), ((5,), 3),
+                                     ((2, 3, 7), 130)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int64, torch.uint8])
+def test_pack_bit_exact(hip, shape, n, dtype):
+    import wide_compiler as wc
+    g = gen(100)
+    ins = [torch.randint(0, 100, shape, generator=g).to(dtype) for _ in range(n)]
+    out = wc.pack([t.to(DEV) for t in ins]).cpu()
+    assert torch.equal(out, wide_ref.pack_inputs(ins))
+    as_np = (lambda t: t.view(torch.int16).numpy()) if dtype == torch.bfloat16 else (lambda t: t.numpy())
+    assert np.array_equal(as_np(out), bytes_ref.pack([as_np(t) for t in ins]))
+
+
+def test_pack_of_unpacked_views_round_trip(hip):
+    import wide_compiler as wc
+    g = gen(101)
+    packed = _rand((4, 12 * 5, 3), g).to(DEV)
+    views = wc.unpack(packed, 12)          # strided views, no copy
+    again = wc.pack(views)
+    assert torch.equal(again, packed)
+
+
+@pytest.mark.parametrize("n,b,inner,dtype", [(100, 32, 64, torch.float32), (7, 5, 3, torch.bfloat16),
+                                             (100, 8, 64 * 16, torch.bfloat16), (3, 2, 1, torch.float32)])
+def test_boundary_transpose_bit_exact(hip, n, b, inner, dtype):
+    g = gen(102)
+    nf = _rand((n, b, inner), g, dtype).to(DEV)
+    dst = torch.empty((b, n * inner), dtype=dtype, device=DEV)
+    es = nf.element_size()
+    hip.swap01(nf, n, b, nf.stride(0) * es, nf.stride(1) * es, inner * es, dst)
+    assert torch.equal(dst.cpu(), wide_ref.to_packed(nf.cpu().view(n, b, inner, 1)).view(b, n * inner))
+
+
+# ----------------------------------------------------------------------------- embedding
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_embedding_shared_bit_exact(hip, dtype):
+    import wide_compiler as wc
+    g = gen(103)
+    torch.manual_seed(103)
+    mods = [nn.Embedding(50, 24) for _ in range(6)]
+    wide = wc.WideEmbedding.from_modules(mods).to(DEV, dtype)
+    ids = torch.randint(0, 50, (3, 9), generator=g)
+    with torch.no_grad():
+        out = wide(ids.to(DEV)).cpu()
+    assert torch.equal(out, wide_ref.embedding(wide.weight.detach().cpu(), ids))
+
+
+def test_embedding_per_model_bit_exact_and_oob_flag(hip):
+    import wide_compiler as wc
+    g = gen(104)
+    wide = wc.WideEmbedding(5, 33, 16).to(DEV, torch.bfloat16)
+    ids = torch.randint(0, 33, (5, 4, 7), generator=g)
+    with torch.no_grad():
+        out = wide(ids.to(DEV), per_model=True).cpu()
+    ref = bytes_ref.embedding_per_model(wide.weight.detach().cpu().float().numpy(), ids.numpy())
+    assert np.array_equal(out.float().numpy(), ref)
+    wide.index_error()  # no error so far
+    bad = ids.clone()
+    bad[1, 2, 3] = 33
+    with torch.no_grad():
+        out = wide(bad.to(DEV), per_model=True).cpu()
+    assert torch.count_nonzero(out[1, 2, 3]) == 0
+    with pytest.raises(IndexError):
+        wide.index_error()
+
+
+# ----------------------------------------------------------------------------- norms
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(4, 3, 5, 256), (2, 7, 96), (3, 2, 1000), (64, 16, 8, 256)])
+def test_layernorm(hip, dtype, shape):
+    import wide_compiler as wc
+    g = gen(105)
+    n, d = shape[0], shape[-1]
+    mod = wc.WideLayerNorm(n, d).to(DEV, dtype)
+    with torch.no_grad():
+        mod.weight.copy_(torch.randn(n * d, generator=g))
+        mod.bias.copy_(torch.randn(n * d, generator=g))
+    x = (_rand(shape, g) * 2 + 0.5).to(dtype)
+    with torch.no_grad():
+        y = mod(x.to(DEV)).cpu()
+    w, b = mod.weight.detach().cpu(), mod.bias.detach().cpu()
+    exact = wide_ref.layernorm(x.double(), w.double(), b.double(), n, mod.eps)
+    assert rel_err(y, exact) <= tol(dtype)
+    if dtype == torch.bfloat16:
+        assert rel_err(y, wide_ref.layernorm(x, w, b, n, mod.eps)) <= TOL_BF16
+
+
+def test_layernorm_strided_view(hip):
+    import wide_compiler as wc
+    g = gen(106)
+    n, d = 5, 64
+    mod = wc.WideLayerNorm(n, d).to(DEV)
+    packed = _rand((6, n * d), g).to(DEV)
+    xv = packed.view(6, n, d).movedim(1, 0)    # N-first strided view
+    with torch.no_grad():
+        y = mod(xv).cpu()
+    exact = wide_ref.layernorm(xv.cpu().double(), mod.weight.detach().cpu().double(),
+                               mod.bias.detach().cpu().double(), n, mod.eps)
+    assert rel_err(y, exact) <= TOL_F32
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("relu", [False, True])
+def test_batchnorm2d_eval(hip, dtype, relu):
+    import wide_compiler as wc
+    g = gen(107)
+    n, c = 6, 8
+    torch.manual_seed(107)
+    mods = [nn.BatchNorm2d(c) for _ in range(n)]
+    for m in mods:
+        with torch.no_grad():
+            m.running_mean.normal_()
+            m.running_var.uniform_(0.5, 2)
+            m.weight.normal_(1, 0.1)
+            m.bias.normal_(0, 0.1)
+    wide = wc.WideBatchNorm2d.from_modules(mods).to(DEV, dtype).eval()
+    wide.fused_activation = "relu" if relu else None
+    x = _rand((n, 3, c, 5, 7), g, dtype)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    op = wide.op
+    exact = wide_ref.batchnorm_eval(x.double(), *(t.detach().cpu().double() for t in
+                                                  (op.weight, op.bias, op.running_mean, op.running_var)),
+                                    op.eps, n)
+    if relu:
+        exact = F.relu(exact)
+    assert rel_err(y, exact) <= tol(dtype)
+
+
+def test_batchnorm_training_mode_raises(hip):
+    import wide_compiler as wc
+    wide = wc.WideBatchNorm2d(2, 3).to(DEV).train()
+    with torch.no_grad(), pytest.raises(RuntimeError, match="eval"):
+        wide(torch.zeros(2, 1, 3, 2, 2, device=DEV))
+
+
+# ----------------------------------------------------------------------------- grouped GEMM
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,batch,i,o", [(100, (32,), 64, 128), (3, (5, 7), 33, 17), (2, (130,), 256, 200),
+                                         (4, (1,), 8, 8), (1, (300,), 512, 96), (8, (2, 3), 1, 5)])
+@pytest.mark.parametrize("bias", [True, False])
+def test_linear(hip, dtype, n, batch, i, o, bias):
+    import wide_compiler as wc
+    g = gen(108)
+    torch.manual_seed(108)
+    mods = [nn.Linear(i, o, bias=bias) for _ in range(n)]
+    wide = wc.WideLinear.from_modules(mods).to(DEV, dtype)
+    x = _rand((n, *batch, i), g, dtype)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    w = wide.weight.detach().cpu()
+    b = wide.bias.detach().cpu() if bias else None
+    exact = wide_ref.linear(x.double(), w.double(), None if b is None else b.double())
+    assert rel_err(y, exact) <= tol(dtype)
+    if dtype == torch.bfloat16:
+        assert rel_err(y, wide_ref.linear(x, w, b)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_strided_boundary_view_and_relu(hip, dtype):
+    import wide_compiler as wc
+    g = gen(109)
+    n, b, i, o = 10, 6, 48, 40
+    wide = wc.WideLinear(n, i, o).to(DEV, dtype)
+    packed = _rand((b, n * i), g, dtype).to(DEV)
+    xv = packed.view(b, n, i).movedim(1, 0)
+    with torch.no_grad():
+        y = wide.forward_into(xv, None, relu=True).cpu()
+    exact = F.relu(wide_ref.linear(xv.cpu().double(), wide.weight.detach().cpu().double(),
+                                   wide.bias.detach().cpu().double()))
+    assert rel_err(y, exact) <= tol(dtype)
+
+
+def test_linear_forward_only(hip):
+    import wide_compiler as wc
+    wide = wc.WideLinear(2, 4, 4).to(DEV)
+    with pytest.raises(RuntimeError, match="forward-only"):
+        wide(torch.zeros(2, 3, 4, device=DEV))
+
+
+# ----------------------------------------------------------------------------- recurrent
+def _rnn_modules(cls, n, i, h, seed, dtype):
+    torch.manual_seed(seed)
+    return [cls(i, h, batch_first=True).to(dtype) for _ in range(n)]
+
+
+def _per_step_err(out, exact):
+    return [rel_err(out[:, :, t], exact[:, :, t]) for t in range(out.shape[2])]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,b,t,i,h", [(32, 4, 32, 64, 128), (3, 2, 5, 8, 16), (5, 3, 9, 20, 40),
+                                       (2, 1, 3, 130, 24), (4, 2, 6, 16, 64)])
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_gru(hip, dtype, n, b, t, i, h, with_h0):
+    import wide_compiler as wc
+    g = gen(110)
+    mods = _rnn_modules(nn.GRU, n, i, h, 110, torch.float32)
+    wide = wc.WideGRU.from_modules(mods).to(DEV, dtype)
+    x = _rand((n, b, t, i), g, dtype)
+    h0 = _rand((n, b, h), g, dtype) if with_h0 else None
+    with torch.no_grad():
+        out, hn = wide(x.to(DEV), None if h0 is None else h0.to(DEV))
+    out, hn = out.cpu(), hn.cpu()
+    p = [getattr(wide, k).detach().cpu() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    eo, eh = wide_ref.gru(x.double(), *(q.double() for q in p), h_0=None if h0 is None else h0.double())
+    errs = _per_step_err(out, eo)
+    # per-timestep bar: TOL at every step t (the error does not compound past it here)
+    assert max(errs) <= tol(dtype), errs
+    assert rel_err(hn, eh) <= tol(dtype)
+    if dtype == torch.bfloat16:
+        ro, _ = wide_ref.gru(x, *p, h_0=h0)
+        assert max(_per_step_err(out, ro)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,b,t,i,h", [(32, 8, 32, 64, 128), (3, 2, 5, 8, 16), (2, 3, 7, 12, 100)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_lstm(hip, dtype, n, b, t, i, h, with_state):
+    import wide_compiler as wc
+    g = gen(111)
+    mods = _rnn_modules(nn.LSTM, n, i, h, 111, torch.float32)
+    wide = wc.WideLSTM.from_modules(mods).to(DEV, dtype)
+    x = _rand((n, b, t, i), g, dtype)
+    hx = (_rand((n, b, h), g, dtype), _rand((n, b, h), g, dtype)) if with_state else None
+    with torch.no_grad():
+        out, (hn, cn) = wide(x.to(DEV), None if hx is None else (hx[0].to(DEV), hx[1].to(DEV)))
+    p = [getattr(wide, k).detach().cpu() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    eo, (eh, ec) = wide_ref.lstm(x.double(), *(q.double() for q in p),
+                                 hx=None if hx is None else (hx[0].double(), hx[1].double()))
+    errs = _per_step_err(out.cpu(), eo)
+    assert max(errs) <= tol(dtype), errs
+    assert rel_err(hn.cpu(), eh) <= tol(dtype)
+    assert rel_err(cn.cpu(), ec) <= tol(dtype)
+
+
+def test_gru_matches_nn_gru_per_model(hip):
+    """The kernel against torch.nn.GRU itself (the reference's validation target)."""
+    import wide_compiler as wc
+    g = gen(112)
+    mods = _rnn_modules(nn.GRU, 4, 10, 32, 112, torch.float32)
+    wide = wc.WideGRU.from_modules(mods).to(DEV)
+    x = _rand((4, 3, 11, 10), g)
+    with torch.no_grad():
+        out, _ = wide(x.to(DEV))
+        for k in range(4):
+            e, _ = mods[k](x[k])
+            assert rel_err(out[k].cpu(), e) <= TOL_F32
+
+
+# ----------------------------------------------------------------------------- traced models
+class MLP(nn.Module):
+    """cli.py:59-67."""
+
+    def __init__(self, d_in=64, d_hidden=128, d_out=64):
+        super().__init__()
+        self.fc1 = nn.Linear(d_in, d_hidden)
+        self.fc2 = nn.Linear(d_hidden, d_out)
+
+    def forward(self, x):
+        return self.fc2(F.relu(self.fc1(x)))
+
+
+def test_traced_mlp_config(hip):
+    """TracedWideModel of N=100 MLP(64,128,64), B=32, fp32 (the CPU-runnable headline model)."""
+    import wide_compiler as wc
+    n, b = 100, 32
+    models = []
+    for i in range(n):
+        torch.manual_seed(1000 + i)
+        models.append(MLP())
+    g = gen(113)
+    ins = [torch.randn(b, 64, generator=g) for _ in range(n)]
+    packed = wide_ref.pack_inputs(ins)
+    wide = wc.compile([m.to(DEV) for m in models], ins[0].to(DEV))
+    summary = wide.summary()
+    assert "fused into fc1" in summary
+    with torch.no_grad():
+        y = wide(packed.to(DEV)).cpu()
+    st = lambda k: torch.stack([getattr(getattr(m, k.split('.')[0]), k.split('.')[1]).detach().cpu().double()
+                                for m in models])  # noqa: E731
+    exact = wide_ref.mlp_wide(packed.double(), n, st("fc1.weight"), st("fc1.bias"), st("fc2.weight"), st("fc2.bias"))
+    assert rel_err(y, exact) <= TOL_F32
+    outs = wc.unpack(y, n)
+    with torch.no_grad():
+        for k in (0, 57, 99):
+            assert rel_err(outs[k], models[k].cpu()(ins[k])) <= TOL_F32
+
+
+def test_compile_validate_true(hip):
+    import wide_compiler as wc
+    models = [MLP(16, 32, 8).to(DEV) for _ in range(12)]
+    wide = wc.compile(models, torch.randn(4, 16, device=DEV), validate=True)
+    assert isinstance(wide, wc.TracedWideModel)
+
+
+def test_cpu_tensors_raise(hip):
+    import wide_compiler as wc
+    wide = wc.WideLinear(2, 4, 4)
+    with torch.no_grad(), pytest.raises(RuntimeError, match="ROCm device"):
+        wide(torch.zeros(2, 3, 4))
