@@ -216,6 +216,52 @@ typedef struct wc_gemm_args {
 
 int32_t wc_grouped_gemm(const wc_gemm_args* args, void* stream);
 
+/*
+ * Convolution weights packed for wc_conv2d: out[i, co, r, s, c] = w[i*c_out + co, c, r, s]
+ * for c < c_in and 0 for c_in <= c < Ci32 (c_in rounded up to 32).  w is the grouped
+ * filter bank [n*c_out, c_in, kh, kw] of WideConv2d.grouped_conv / WideConv1d.op
+ * (wide_conv2d.py:149-158, wide_conv1d.py:85-94).  out holds
+ * wc_conv_packed_weight_elems(...) elements of `dtype`, 16-byte aligned.
+ */
+int32_t wc_conv_pack_weights(const void* w, int64_t n, int64_t c_out, int64_t c_in, int64_t kh,
+                             int64_t kw, int32_t dtype, void* out, void* stream);
+int64_t wc_conv_packed_weight_elems(int64_t n, int64_t c_out, int64_t c_in, int64_t kh, int64_t kw);
+
+/*
+ * Grouped 2-D convolution (1-D as h = 1) with fused epilogue -- replaces the
+ * permute/reshape + grouped nn.Conv2d / nn.Conv1d + permute().contiguous() of
+ * WideConv2d.forward (wide_conv2d.py:176-194) and WideConv1d.forward
+ * (wide_conv1d.py:125-141), and, when a BatchNorm / add / ReLU stage follows,
+ * WideBatchNorm2d.forward (wide_batchnorm_2d.py:60-71) and the traced add / relu
+ * stages (traced_wide.py:174-211):
+ *   y = act( BN(conv(x, W) + bias) + residual )
+ * x: [n, batch, c_in, h, w] where each (i, b) block [c_in, h, w] is contiguous
+ * (strides x_stride_n, x_stride_b); y and residual likewise with [c_out, h_out, w_out]
+ * blocks.  BN is eval-mode (y = (v - mean) / sqrt(var + eps) * weight + bias),
+ * applied when bn_mean != NULL.  Parameters are [n*c_out] of param_dtype.
+ * dtype in {WC_F32, WC_BF16}; fp32 accumulation on MFMA.
+ */
+typedef struct wc_conv_args {
+  int32_t dtype, param_dtype, act;
+  int64_t n, batch, c_in, c_out, h, w, kh, kw;
+  int64_t stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, h_out, w_out;
+  const void* x;
+  int64_t x_stride_n, x_stride_b;
+  const void* packed_weight;   /* from wc_conv_pack_weights */
+  const void* bias;
+  const void* bn_weight;
+  const void* bn_bias;
+  const void* bn_mean;
+  const void* bn_var;
+  float bn_eps;
+  const void* residual;
+  int64_t r_stride_n, r_stride_b;
+  void* y;
+  int64_t y_stride_n, y_stride_b;
+} wc_conv_args;
+
+int32_t wc_conv2d(const wc_conv_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,444 @@
+// Implicit-GEMM grouped convolution (N independent Conv1d / Conv2d layers) on
+// MFMA with a fused epilogue:
+//   y[i,b,co,p] = act( BN_i,co( sum_{ci,r,s} x[i,b,ci,p@(r,s)] W[i,co,ci,r,s] + bias )
+//                      + R[i,b,co,p] )
+// Per model the GEMM is  M = output pixels, N = C_out, K = C_in * kh * kw.
+//
+// Workgroup = (model, image, pixel tile, 64-channel output tile), 4 waves.
+//  * The input tile (output tile + halo) is staged once in LDS as
+//    channels-last [row][col][ci] with a padded channel pitch, so an MFMA A
+//    fragment (8 consecutive input channels of one pixel) is one 16-byte LDS
+//    read, and the tile is reused by all kh*kw taps.
+//  * Weights are pre-packed (wc_conv_pack_weights) to [N, C_out, kh, kw, Ci32]
+//    so a B fragment (8 consecutive input channels of one tap and one output
+//    channel) is one 16-byte load that stays resident in L2/L1; B fragments of
+//    the next K-step are fetched while the current one runs.
+//  * Each wave computes FM x 4 MFMA tiles (FM*16 pixels x 64 channels): every
+//    A fragment feeds four MFMAs.
+//  * Epilogue: bias, eval-BatchNorm folded as (v * alpha + beta), written to
+//    LDS as [co][pixel] in the output type, then residual add + ReLU during
+//    coalesced NCHW stores.
+#include "wc_common.h"
+
+namespace wc {
+namespace {
+
+struct ConvParams {
+  int n, batch, ci, co, h, w, kh, kw, sh, sw, ph, pw, dh, dw, ho, wo;
+  int ci32;                 // input channels padded to a multiple of 32
+  int cc;                   // input channels staged per LDS chunk (multiple of 32)
+  int tr, tc;               // output tile rows / cols
+  int ir, ic;               // input tile rows / cols
+  int tiles_r, tiles_c, tiles_co;
+  int remap, act, vec_out;
+  const void* x;
+  int64_t x_sn, x_sb;
+  const void* wp;           // packed weights [n][co][kh][kw][ci32]
+  const void* bias;         // [n*co] or null
+  const void* bn_w;         // eval BN params [n*co] (bn_mean null: no BN)
+  const void* bn_b;
+  const void* bn_mean;
+  const void* bn_var;
+  float bn_eps;
+  int pdt;                  // element type of bias / BN params
+  const void* res;
+  int64_t r_sn, r_sb;
+  void* y;
+  int64_t y_sn, y_sb;
+};
+
+constexpr int kConvThreads = 256;
+constexpr int kFN = 4;            // 16-wide MFMA tiles along output channels (64)
+
+__device__ __forceinline__ float ldp(const void* p, int dt, int64_t i) {
+  return dt == WC_F32 ? static_cast<const float*>(p)[i] : static_cast<float>(static_cast<const bf16*>(p)[i]);
+}
+
+template <typename T> struct ConvTraits;
+template <> struct ConvTraits<bf16> {
+  static constexpr int kFM = 8;    // 128 pixels per wave
+  static constexpr int kPad = 8;   // channel pitch padding (elements)
+};
+template <> struct ConvTraits<float> {
+  static constexpr int kFM = 4;    // 64 pixels per wave
+  static constexpr int kPad = 4;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
+  constexpr int FM = ConvTraits<T>::kFM;
+  constexpr int PAD = ConvTraits<T>::kPad;
+  constexpr int TPIX = 4 * FM * 16;                   // pixels per tile
+  extern __shared__ float4 smem4[];
+  T* xs = reinterpret_cast<T*>(smem4);
+  const int cip = p.cc + PAD;                         // LDS channel pitch
+
+  // ---- tile coordinates ----
+  const int per_img = p.tiles_r * p.tiles_c * p.tiles_co;
+  const int nblk = p.n * p.batch * per_img;
+  int bid = blockIdx.x;
+  if (p.remap) bid = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
+  const int img = bid / per_img;                      // (model, image)
+  int rem = bid - img * per_img;
+  const int tco = rem / (p.tiles_r * p.tiles_c);
+  rem -= tco * (p.tiles_r * p.tiles_c);
+  const int trr = rem / p.tiles_c;
+  const int tcc = rem - trr * p.tiles_c;
+  const int mdl = img / p.batch;
+  const int bb = img - mdl * p.batch;
+  const int ho0 = trr * p.tr, wo0 = tcc * p.tc, co0 = tco * 64;
+  const int hi0 = ho0 * p.sh - p.ph, wi0 = wo0 * p.sw - p.pw;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+
+  const T* xb = static_cast<const T*>(p.x) + mdl * p.x_sn + bb * p.x_sb;
+  const T* wb = static_cast<const T*>(p.wp) + static_cast<int64_t>(mdl) * p.co * p.kh * p.kw * p.ci32;
+
+  // LDS offset (elements, tap (0,0), channel fk) of each A-fragment pixel
+  int aoff[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int px = wave * FM * 16 + i * 16 + fr;
+    const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+    const bool ok = pr < p.tr;
+    aoff[i] = ok ? ((pr * p.sh) * p.ic + pc * p.sw) * cip + fk : fk;
+  }
+  // B-fragment weight rows (output channel per j) and their validity
+  const T* wrow[kFN];
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) {
+    const int co = co0 + j * 16 + fr;
+    wrow[j] = (co < p.co) ? wb + static_cast<int64_t>(co) * p.kh * p.kw * p.ci32 + fk : nullptr;
+  }
+
+  f32x4 acc[FM][kFN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int taps = p.kh * p.kw;
+  for (int c0 = 0; c0 < p.ci32; c0 += p.cc) {
+    // ---- stage input channels [c0, c0+cc) of the tile as [row][col][ci] ----
+    if (c0 > 0) __syncthreads();
+    const int plane = p.ir * p.ic;
+    const int tot = p.cc * plane;
+    for (int e = tid; e < tot; e += kConvThreads) {
+      const int c = e / plane;
+      const int rc = e - c * plane;
+      const int r = rc / p.ic;
+      const int col = rc - r * p.ic;
+      const int hi = hi0 + r, wi = wi0 + col, ch = c0 + c;
+      T v = from_f32<T>(0.f);
+      if (ch < p.ci && hi >= 0 && hi < p.h && wi >= 0 && wi < p.w)
+        v = xb[(static_cast<int64_t>(ch) * p.h + hi) * p.w + wi];
+      xs[rc * cip + c] = v;
+    }
+    __syncthreads();
+
+    const int ksteps = taps * (p.cc / 32);
+    // B fragments for K-step 0 of this chunk
+    auto bload = [&](int ks, uint4* dst) {
+      const int tap = ks / (p.cc / 32);
+      const int cs = ks - tap * (p.cc / 32);
+      const int64_t koff = static_cast<int64_t>(tap) * p.ci32 + c0 + cs * 32;
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        if (sizeof(T) == 2) {
+          dst[2 * j] = wrow[j] ? *reinterpret_cast<const uint4*>(wrow[j] + koff) : make_uint4(0, 0, 0, 0);
+        } else {
+          dst[2 * j] = wrow[j] ? *reinterpret_cast<const uint4*>(wrow[j] + koff) : make_uint4(0, 0, 0, 0);
+          dst[2 * j + 1] = wrow[j] ? *reinterpret_cast<const uint4*>(wrow[j] + koff + 4) : make_uint4(0, 0, 0, 0);
+        }
+      }
+    };
+    uint4 bcur[2 * kFN], bnxt[2 * kFN];
+    bload(0, bcur);
+    for (int ks = 0; ks < ksteps; ++ks) {
+      if (ks + 1 < ksteps) bload(ks + 1, bnxt);
+      const int tap = ks / (p.cc / 32);
+      const int cs = ks - tap * (p.cc / 32);
+      const int r = tap / p.kw, s = tap - (tap / p.kw) * p.kw;
+      const int toff = ((r * p.dh) * p.ic + s * p.dw) * cip + cs * 32;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xs[aoff[i] + toff]);
+#pragma unroll
+          for (int j = 0; j < kFN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, *reinterpret_cast<const bf16x8*>(&bcur[2 * j]),
+                                                                 acc[i][j], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const float* ap = reinterpret_cast<const float*>(&xs[aoff[i] + toff]);
+          const f32x4 a0 = *reinterpret_cast<const f32x4*>(ap);
+          const f32x4 a1 = *reinterpret_cast<const f32x4*>(ap + 4);
+#pragma unroll
+          for (int j = 0; j < kFN; ++j) {
+            const f32x4 b0 = *reinterpret_cast<const f32x4*>(&bcur[2 * j]);
+            const f32x4 b1 = *reinterpret_cast<const f32x4*>(&bcur[2 * j + 1]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[q], b0[q], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[q], b1[q], acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+      if (ks + 1 < ksteps) {
+#pragma unroll
+        for (int q = 0; q < 2 * kFN; ++q) bcur[q] = bnxt[q];
+      }
+    }
+  }
+
+  // ---- epilogue 1: bias + folded BN, into LDS as [co][pixel] (type T) ----
+  __syncthreads();
+  constexpr int CPITCH = TPIX + 8;
+  T* cs = xs;  // reuse the input tile buffer
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) {
+    const int col = j * 16 + fr;          // output channel within the tile
+    const int co = co0 + col;
+    float alpha = 1.f, beta = 0.f;
+    if (co < p.co) {
+      const int64_t pi = static_cast<int64_t>(mdl) * p.co + co;
+      const float bv = p.bias ? ldp(p.bias, p.pdt, pi) : 0.f;
+      if (p.bn_mean) {
+        const float inv = 1.0f / sqrtf(ldp(p.bn_var, p.pdt, pi) + p.bn_eps);
+        alpha = p.bn_w ? inv * ldp(p.bn_w, p.pdt, pi) : inv;
+        beta = (p.bn_b ? ldp(p.bn_b, p.pdt, pi) : 0.f) - ldp(p.bn_mean, p.pdt, pi) * alpha;
+        beta += bv * alpha;   // (acc + bias) * alpha + beta
+      } else {
+        beta = bv;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int px = wave * FM * 16 + i * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cs[col * CPITCH + px + e] = from_f32<T>(acc[i][j][e] * alpha + beta);
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue 2: residual + activation, coalesced NCHW stores ----
+  T* yb = static_cast<T*>(p.y) + mdl * p.y_sn + bb * p.y_sb;
+  const T* rb = p.res ? static_cast<const T*>(p.res) + mdl * p.r_sn + bb * p.r_sb : nullptr;
+  const int how = p.ho * p.wo;
+  constexpr int VE = 16 / sizeof(T);
+  if (p.vec_out) {
+    // tc % VE == 0, wo0 % VE == 0, rows of y / res 16-byte aligned
+    const int chunks = 64 * (TPIX / VE);
+    for (int e = tid; e < chunks; e += kConvThreads) {
+      const int col = e / (TPIX / VE);
+      const int px = (e - col * (TPIX / VE)) * VE;
+      const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+      const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
+      if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
+      const int64_t off = static_cast<int64_t>(co) * how + oh * p.wo + ow;
+      float v[VE];
+      const T* src = &cs[col * CPITCH + px];
+#pragma unroll
+      for (int q = 0; q < VE; ++q) v[q] = to_f32(src[q]);
+      if (rb) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(rb + off);
+        const T* rr = reinterpret_cast<const T*>(&rv);
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = to_f32(from_f32<T>(v[q] + to_f32(rr[q])));
+      }
+      uint4 ov;
+      T* oo = reinterpret_cast<T*>(&ov);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) oo[q] = from_f32<T>(p.act == WC_ACT_RELU ? fmaxf(v[q], 0.f) : v[q]);
+      *reinterpret_cast<uint4*>(yb + off) = ov;
+    }
+  } else {
+    for (int e = tid; e < 64 * TPIX; e += kConvThreads) {
+      const int col = e / TPIX;
+      const int px = e - col * TPIX;
+      const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+      const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
+      if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
+      const int64_t off = static_cast<int64_t>(co) * how + oh * p.wo + ow;
+      float v = to_f32(cs[col * CPITCH + px]);
+      if (rb) v = to_f32(from_f32<T>(v + to_f32(rb[off])));
+      if (p.act == WC_ACT_RELU) v = fmaxf(v, 0.f);
+      yb[off] = from_f32<T>(v);
+    }
+  }
+}
+
+// packed[i][co][r][s][c] = c < ci ? w[i*co_n + co][c][r][s] : 0
+template <typename T>
+__global__ __launch_bounds__(256) void conv_pack_kernel(const T* __restrict__ w, T* __restrict__ out,
+                                                        int64_t total, int ci, int ci32, int taps) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= total) return;
+  const int c = static_cast<int>(e % ci32);
+  const int64_t rest = e / ci32;                 // (i*co + co) * taps + tap
+  const int tap = static_cast<int>(rest % taps);
+  const int64_t oc = rest / taps;                // i*co + co
+  out[e] = c < ci ? w[(oc * ci + c) * taps + tap] : from_f32<T>(0.f);
+}
+
+template <typename K>
+int32_t launch_big_lds(K kernel, const ConvParams& p, dim3 grid, size_t lds, hipStream_t st) {
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_conv2d: LDS of %zu bytes refused: %s", lds,
+                       hipGetErrorString(e));
+  }
+  kernel<<<grid, kConvThreads, lds, st>>>(p);
+  return check_launch("wc_conv2d");
+}
+
+constexpr size_t kConvLdsBudget = 152 * 1024;
+
+inline int round32(int v) { return (v + 31) & ~31; }
+
+// Tile / chunk plan; false if even the smallest tile does not fit in LDS.
+template <typename T>
+bool conv_plan(ConvParams& p) {
+  constexpr int TPIX = 4 * ConvTraits<T>::kFM * 16;
+  constexpr int PAD = ConvTraits<T>::kPad;
+  p.ci32 = round32(p.ci);
+  p.tc = p.wo < TPIX ? p.wo : TPIX;
+  p.tr = TPIX / p.tc;
+  if (p.tr > p.ho) p.tr = p.ho;
+  for (;;) {
+    p.ir = (p.tr - 1) * p.sh + (p.kh - 1) * p.dh + 1;
+    p.ic = (p.tc - 1) * p.sw + (p.kw - 1) * p.dw + 1;
+    const size_t epi = static_cast<size_t>(64) * (TPIX + 8) * sizeof(T);
+    for (p.cc = p.ci32; p.cc >= 32; p.cc -= 32) {
+      if (p.ci32 % p.cc) continue;
+      const size_t in = static_cast<size_t>(p.ir) * p.ic * (p.cc + PAD) * sizeof(T);
+      if ((in > epi ? in : epi) <= kConvLdsBudget) return true;
+    }
+    if (p.tr > 1) {
+      p.tr = (p.tr + 1) / 2;
+    } else if (p.tc > 16) {
+      p.tc = (p.tc + 1) / 2;
+    } else {
+      return false;
+    }
+  }
+}
+
+}  // namespace
+}  // namespace wc
+
+using namespace wc;
+
+extern "C" int32_t wc_conv_pack_weights(const void* w, int64_t n, int64_t c_out, int64_t c_in, int64_t kh,
+                                        int64_t kw, int32_t dtype, void* out, void* stream) {
+  clear_error();
+  WC_REQUIRE(n >= 0 && c_out >= 0 && c_in > 0 && kh > 0 && kw > 0, WC_ERR_SHAPE, "wc_conv_pack_weights: bad sizes");
+  if (n == 0 || c_out == 0) return WC_OK;
+  WC_REQUIRE(w && out, WC_ERR_NULL, "wc_conv_pack_weights: null pointer");
+  const int ci32 = round32(static_cast<int>(c_in));
+  const int64_t total = n * c_out * kh * kw * ci32;
+  const dim3 grid(static_cast<uint32_t>(cdiv(total, 256)));
+  hipStream_t st = as_stream(stream);
+  if (dtype == WC_F32)
+    conv_pack_kernel<float><<<grid, 256, 0, st>>>(static_cast<const float*>(w), static_cast<float*>(out), total,
+                                                  (int)c_in, ci32, (int)(kh * kw));
+  else if (dtype == WC_BF16)
+    conv_pack_kernel<bf16><<<grid, 256, 0, st>>>(static_cast<const bf16*>(w), static_cast<bf16*>(out), total,
+                                                 (int)c_in, ci32, (int)(kh * kw));
+  else
+    return set_error(WC_ERR_DTYPE, "wc_conv_pack_weights: unsupported dtype %s", dtype_name(dtype));
+  return check_launch("wc_conv_pack_weights");
+}
+
+extern "C" int64_t wc_conv_packed_weight_elems(int64_t n, int64_t c_out, int64_t c_in, int64_t kh, int64_t kw) {
+  return n * c_out * kh * kw * round32(static_cast<int>(c_in));
+}
+
+extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
+  clear_error();
+  WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_conv2d: null args");
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "wc_conv2d: unsupported dtype %s",
+             dtype_name(a->dtype));
+  WC_REQUIRE(a->param_dtype == WC_F32 || a->param_dtype == a->dtype, WC_ERR_DTYPE,
+             "wc_conv2d: parameter dtype %s", dtype_name(a->param_dtype));
+  WC_REQUIRE(a->n >= 0 && a->batch >= 0 && a->c_in > 0 && a->c_out >= 0 && a->h > 0 && a->w > 0 &&
+                 a->kh > 0 && a->kw > 0 && a->stride_h > 0 && a->stride_w > 0 && a->pad_h >= 0 &&
+                 a->pad_w >= 0 && a->dil_h > 0 && a->dil_w > 0,
+             WC_ERR_SHAPE, "wc_conv2d: bad sizes");
+  const int64_t ho = (a->h + 2 * a->pad_h - a->dil_h * (a->kh - 1) - 1) / a->stride_h + 1;
+  const int64_t wo = (a->w + 2 * a->pad_w - a->dil_w * (a->kw - 1) - 1) / a->stride_w + 1;
+  WC_REQUIRE(ho == a->h_out && wo == a->w_out, WC_ERR_SHAPE,
+             "wc_conv2d: output %lldx%lld does not match the geometry (%lldx%lld)", (long long)a->h_out,
+             (long long)a->w_out, (long long)ho, (long long)wo);
+  if (a->n == 0 || a->batch == 0 || a->c_out == 0 || ho <= 0 || wo <= 0) return WC_OK;
+  WC_REQUIRE(a->x && a->packed_weight && a->y, WC_ERR_NULL, "wc_conv2d: null pointer");
+  WC_REQUIRE(a->c_in * a->h * a->w < 0x7fffffffll && a->c_out * ho * wo < 0x7fffffffll &&
+                 a->n * a->c_out < 0x7fffffffll,
+             WC_ERR_LIMIT, "wc_conv2d: sizes too large");
+  ConvParams p;
+  p.n = (int)a->n;
+  p.batch = (int)a->batch;
+  p.ci = (int)a->c_in;
+  p.co = (int)a->c_out;
+  p.h = (int)a->h;
+  p.w = (int)a->w;
+  p.kh = (int)a->kh;
+  p.kw = (int)a->kw;
+  p.sh = (int)a->stride_h;
+  p.sw = (int)a->stride_w;
+  p.ph = (int)a->pad_h;
+  p.pw = (int)a->pad_w;
+  p.dh = (int)a->dil_h;
+  p.dw = (int)a->dil_w;
+  p.ho = (int)ho;
+  p.wo = (int)wo;
+  p.act = a->act;
+  p.x = a->x;
+  p.x_sn = a->x_stride_n;
+  p.x_sb = a->x_stride_b;
+  p.wp = a->packed_weight;
+  p.bias = a->bias;
+  p.bn_w = a->bn_weight;
+  p.bn_b = a->bn_bias;
+  p.bn_mean = a->bn_mean;
+  p.bn_var = a->bn_var;
+  p.bn_eps = a->bn_eps;
+  p.pdt = a->param_dtype;
+  WC_REQUIRE(!p.bn_mean || p.bn_var, WC_ERR_NULL, "wc_conv2d: BN mean without variance");
+  p.res = a->residual;
+  p.r_sn = a->r_stride_n;
+  p.r_sb = a->r_stride_b;
+  p.y = a->y;
+  p.y_sn = a->y_stride_n;
+  p.y_sb = a->y_stride_b;
+  const bool f32 = a->dtype == WC_F32;
+  if (!(f32 ? conv_plan<float>(p) : conv_plan<bf16>(p)))
+    return set_error(WC_ERR_LIMIT, "wc_conv2d: tile does not fit in LDS");
+  p.tiles_r = static_cast<int>(cdiv(p.ho, p.tr));
+  p.tiles_c = static_cast<int>(cdiv(p.wo, p.tc));
+  p.tiles_co = static_cast<int>(cdiv(p.co, 64));
+  const int es = f32 ? 4 : 2;
+  const int ve = 16 / es;
+  const bool yal = aligned(p.y, 16) && (p.y_sn * es) % 16 == 0 && (p.y_sb * es) % 16 == 0;
+  const bool ral = !p.res || (aligned(p.res, 16) && (p.r_sn * es) % 16 == 0 && (p.r_sb * es) % 16 == 0);
+  p.vec_out = (yal && ral && p.tc % ve == 0 && p.wo % ve == 0) ? 1 : 0;
+  WC_REQUIRE(aligned(p.wp, 16), WC_ERR_ALIGN, "wc_conv2d: packed weights not 16-byte aligned");
+  const int64_t nblk = static_cast<int64_t>(p.n) * p.batch * p.tiles_r * p.tiles_c * p.tiles_co;
+  WC_REQUIRE(nblk < 0x7fffffffll, WC_ERR_LIMIT, "wc_conv2d: too many tiles");
+  p.remap = (nblk % 8 == 0) ? 1 : 0;
+  const size_t in = static_cast<size_t>(p.ir) * p.ic * (p.cc + (f32 ? 4 : 8)) * es;
+  const size_t epi = static_cast<size_t>(64) * (4 * (f32 ? 4 : 8) * 16 + 8) * es;
+  const size_t lds = in > epi ? in : epi;
+  const dim3 grid(static_cast<uint32_t>(nblk));
+  hipStream_t st = as_stream(stream);
+  if (f32) return launch_big_lds(conv_kernel<float>, p, grid, lds, st);
+  return launch_big_lds(conv_kernel<bf16>, p, grid, lds, st);
+}

@@ -73,6 +73,23 @@ class _GemmArgs(ctypes.Structure):
     ]
 
 
+class _ConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("param_dtype", ctypes.c_int32), ("act", ctypes.c_int32),
+        ("n", ctypes.c_int64), ("batch", ctypes.c_int64), ("c_in", ctypes.c_int64), ("c_out", ctypes.c_int64),
+        ("h", ctypes.c_int64), ("w", ctypes.c_int64), ("kh", ctypes.c_int64), ("kw", ctypes.c_int64),
+        ("stride_h", ctypes.c_int64), ("stride_w", ctypes.c_int64), ("pad_h", ctypes.c_int64),
+        ("pad_w", ctypes.c_int64), ("dil_h", ctypes.c_int64), ("dil_w", ctypes.c_int64),
+        ("h_out", ctypes.c_int64), ("w_out", ctypes.c_int64),
+        ("x", ctypes.c_void_p), ("x_stride_n", ctypes.c_int64), ("x_stride_b", ctypes.c_int64),
+        ("packed_weight", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("bn_weight", ctypes.c_void_p), ("bn_bias", ctypes.c_void_p), ("bn_mean", ctypes.c_void_p),
+        ("bn_var", ctypes.c_void_p), ("bn_eps", ctypes.c_float),
+        ("residual", ctypes.c_void_p), ("r_stride_n", ctypes.c_int64), ("r_stride_b", ctypes.c_int64),
+        ("y", ctypes.c_void_p), ("y_stride_n", ctypes.c_int64), ("y_stride_b", ctypes.c_int64),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -93,6 +110,9 @@ SIGNATURES = {
     "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_recurrence": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_grouped_gemm": (_I32, [ctypes.POINTER(_GemmArgs), _P]),
+    "wc_conv_pack_weights": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P]),
+    "wc_conv_packed_weight_elems": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "wc_conv2d": (_I32, [ctypes.POINTER(_ConvArgs), _P]),
 }
 
 
@@ -259,6 +279,43 @@ def rnn_phase(a: _RnnArgs, phase: str, like: Tensor) -> None:
     """Run one phase ('input_projection' or 'recurrence') of a prepared rnn_args struct."""
     fn = getattr(lib(), f"wc_rnn_{phase}")
     _check(fn(ctypes.byref(a), stream_of(like)), f"wc_rnn_{phase}")
+
+
+def conv_pack_weights(w: Tensor, n: int, c_out: int, c_in: int, kh: int, kw: int) -> Tensor:
+    elems = int(lib().wc_conv_packed_weight_elems(n, c_out, c_in, kh, kw))
+    out = torch.empty(max(elems, 8), dtype=w.dtype, device=w.device)
+    _check(lib().wc_conv_pack_weights(w.data_ptr(), n, c_out, c_in, kh, kw, dtype_code(w.dtype, "conv"),
+                                      out.data_ptr(), stream_of(w)), "wc_conv_pack_weights")
+    return out
+
+
+def conv2d(*, x: Tensor, packed_w: Tensor, n: int, c_in: int, c_out: int, kernel, stride, padding, dilation,
+           y: Tensor, bias: Optional[Tensor] = None, bn=None, residual: Optional[Tensor] = None,
+           relu: bool = False) -> None:
+    """x / y / residual are [n, b, C, H, W] with dense [C, H, W] blocks; bn = (weight, bias,
+    running_mean, running_var, eps) or None."""
+    a = _ConvArgs()
+    a.dtype = dtype_code(x.dtype, "conv")
+    params = [t for t in (bias, *(bn[:4] if bn else ())) if t is not None]
+    a.param_dtype = dtype_code(params[0].dtype, "conv") if params else a.dtype
+    a.act = ACT_RELU if relu else ACT_NONE
+    a.n, a.batch, a.c_in, a.c_out = n, x.shape[1], c_in, c_out
+    a.h, a.w = x.shape[3], x.shape[4]
+    a.kh, a.kw = kernel
+    a.stride_h, a.stride_w = stride
+    a.pad_h, a.pad_w = padding
+    a.dil_h, a.dil_w = dilation
+    a.h_out, a.w_out = y.shape[3], y.shape[4]
+    a.x, a.x_stride_n, a.x_stride_b = x.data_ptr(), x.stride(0), x.stride(1)
+    a.packed_weight = packed_w.data_ptr()
+    a.bias = ptr(bias)
+    if bn is not None:
+        a.bn_weight, a.bn_bias, a.bn_mean, a.bn_var = ptr(bn[0]), ptr(bn[1]), ptr(bn[2]), ptr(bn[3])
+        a.bn_eps = float(bn[4])
+    if residual is not None:
+        a.residual, a.r_stride_n, a.r_stride_b = residual.data_ptr(), residual.stride(0), residual.stride(1)
+    a.y, a.y_stride_n, a.y_stride_b = y.data_ptr(), y.stride(0), y.stride(1)
+    _check(lib().wc_conv2d(ctypes.byref(a), stream_of(x)), "wc_conv2d")
 
 
 def exported_symbols() -> List[str]:

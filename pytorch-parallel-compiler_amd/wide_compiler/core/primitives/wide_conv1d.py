@@ -73,10 +73,12 @@ class WideConv1d(nn.Module):
         w = w.reshape(self.n * self.out_channels, self.in_channels, 1, self.kernel_size)
         return w, (None if b is None else b.reshape(-1))
 
-    def forward(self, x: Tensor) -> Tensor:
+    def forward(self, x: Tensor, residual: Optional[Tensor] = None) -> Tensor:
+        """x [N, B, C_in, L] -> [N, B, C_out, L'] (optional fused residual of the output's shape)."""
         if x.dim() != 4:
             raise RuntimeError(f"WideConv1d: expected [N, B, C, L], got {list(x.shape)}")
-        return conv_forward(self, x.unsqueeze(3), one_d=True).squeeze(3)
+        r = None if residual is None else residual.unsqueeze(3)
+        return conv_forward(self, x.unsqueeze(3), one_d=True, residual=r).squeeze(3)
 
     @classmethod
     def from_modules(cls, modules: List[nn.Conv1d], strategy: Optional[Conv1dStrategy] = None) -> "WideConv1d":

@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import warnings
 from enum import Enum
-from typing import List, Tuple, Union
+from typing import List, Optional, Tuple, Union
 
 import torch
 from torch import Tensor, nn
@@ -86,10 +86,13 @@ class WideConv2d(nn.Module):
     def strategy(self) -> ConvStrategy:
         return self._strategy
 
-    def forward(self, x: Tensor) -> Tensor:
+    def forward(self, x: Tensor, residual: Optional[Tensor] = None, out: Optional[Tensor] = None) -> Tensor:
+        """x [N, B, C_in, H, W] -> [N, B, C_out, H', W'].  ``residual`` (same shape as the
+        output) is added in the epilogue; TracedWideModel passes it when it has fused a
+        following ``+``."""
         if x.dim() != 5:
             raise RuntimeError(f"WideConv2d: expected [N, B, C, H, W], got {list(x.shape)}")
-        return conv_forward(self, x)
+        return conv_forward(self, x, residual=residual, out=out)
 
     @classmethod
     def from_modules(cls, modules: List[nn.Conv2d],

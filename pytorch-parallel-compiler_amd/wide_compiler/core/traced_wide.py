@@ -377,10 +377,11 @@ class TracedWideModel(nn.Module):
                       for k, v in self._node_kwargs.get(name, {}).items()}
             if name in self._residual_of:
                 kwargs["residual"] = values[self._residual_of[name]]
-            if name == out_name and isinstance(op, WideLinear) and not kwargs and len(args) == 1 \
-                    and isinstance(args[0], Tensor) and args[0].dim() >= 3:
-                packed_out, values[name] = self._linear_into_packed(op, args[0])
-                continue
+            if name == out_name and len(args) == 1 and isinstance(args[0], Tensor):
+                direct = self._into_packed(op, args[0], kwargs)
+                if direct is not None:
+                    packed_out, values[name] = direct
+                    continue
             if kwargs:
                 values[name] = op(*args, **kwargs)
             elif len(args) == 1:
@@ -395,17 +396,27 @@ class TracedWideModel(nn.Module):
             out = out[0]
         return self._to_packed(out)
 
-    def _linear_into_packed(self, op: WideLinear, x: Tensor) -> Tuple[Tensor, Tensor]:
-        """Run the final WideLinear writing straight into the packed [B, N*C, *S] layout;
-        returns (packed, N-first view of it)."""
-        n, b = x.shape[0], x.shape[1]
-        mid = tuple(x.shape[2:-1])
-        o = op.out_features
-        nf_shape = (n, b, *mid, o)            # the N-first result
-        c = nf_shape[2]
+    def _into_packed(self, op: nn.Module, x: Tensor, kwargs: Dict[str, Any]) -> Optional[Tuple[Tensor, Tensor]]:
+        """Run the output stage writing straight into the packed [B, N*C, *S] layout when it
+        is a WideLinear or WideConv2d; returns (packed, N-first view of it) or None."""
+        if isinstance(op, WideLinear) and not kwargs and x.dim() >= 3:
+            nf_shape = (x.shape[0], x.shape[1], *x.shape[2:-1], op.out_features)
+        elif isinstance(op, WideConv2d) and set(kwargs) <= {"residual"} and x.dim() == 5:
+            kh, kw = op.kernel_size
+            ho = (x.shape[3] + 2 * op.padding[0] - op.dilation[0] * (kh - 1) - 1) // op.stride[0] + 1
+            wo = (x.shape[4] + 2 * op.padding[1] - op.dilation[1] * (kw - 1) - 1) // op.stride[1] + 1
+            if ho <= 0 or wo <= 0:
+                return None
+            nf_shape = (x.shape[0], x.shape[1], op.out_channels, ho, wo)
+        else:
+            return None
+        n, b, c = nf_shape[0], nf_shape[1], nf_shape[2]
         packed = torch.empty((b, n * c, *nf_shape[3:]), dtype=x.dtype, device=x.device)
         view = packed.view(b, n, *nf_shape[2:]).movedim(1, 0)
-        op.forward_into(x, view, relu=op.fused_activation == "relu")
+        if isinstance(op, WideLinear):
+            op.forward_into(x, view, relu=op.fused_activation == "relu")
+        else:
+            op(x, out=view, **kwargs)
         return packed, view
 
     def _to_packed(self, out: Tensor) -> Tensor:

@@ -1,0 +1,188 @@
+"""GPU parity of the implicit-GEMM grouped convolution and the traced ResBlock against the oracle."""
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import wide_ref
+from tests._util import TOL_BF16, TOL_F32, gen, rel_err, tol
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def _rand(shape, g, dtype=torch.float32):
+    return torch.randn(shape, generator=g).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,b,ci,co,hw,k,stride,pad,dil", [
+    (4, 2, 64, 64, (32, 32), 3, 1, 1, 1),
+    (3, 2, 3, 16, (17, 13), 3, 1, 1, 1),
+    (2, 1, 40, 72, (9, 11), 3, 2, 1, 1),
+    (2, 3, 8, 8, (12, 12), 5, 1, 2, 2),
+    (5, 1, 16, 130, (6, 7), 1, 1, 0, 1),
+    (2, 2, 96, 24, (5, 70), (3, 1), (1, 2), (1, 0), 1),
+])
+def test_conv2d(hip, dtype, n, b, ci, co, hw, k, stride, pad, dil):
+    import wide_compiler as wc
+    g = gen(200)
+    torch.manual_seed(200)
+    mods = [nn.Conv2d(ci, co, k, stride=stride, padding=pad, dilation=dil) for _ in range(n)]
+    wide = wc.WideConv2d.from_modules(mods).to(DEV, dtype)
+    x = _rand((n, b, ci, *hw), g, dtype)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    cw = wide.grouped_conv.weight.detach().cpu()
+    cb = wide.grouped_conv.bias.detach().cpu()
+    exact = wide_ref.conv2d(x.double(), cw.double(), cb.double(), n, stride=wide.stride, padding=wide.padding,
+                            dilation=wide.dilation)
+    assert y.shape == exact.shape
+    assert rel_err(y, exact) <= tol(dtype)
+    if dtype == torch.bfloat16:
+        assert rel_err(y, wide_ref.conv2d(x, cw, cb, n, stride=wide.stride, padding=wide.padding,
+                                          dilation=wide.dilation)) <= TOL_BF16
+
+
+def test_conv2d_weight_update_invalidates_packing(hip):
+    import wide_compiler as wc
+    g = gen(201)
+    wide = wc.WideConv2d(3, 8, 8, 3, padding=1).to(DEV)
+    x = _rand((3, 2, 8, 6, 6), g).to(DEV)
+    with torch.no_grad():
+        wide(x)
+        wide.grouped_conv.weight.mul_(2.0)
+        y = wide(x).cpu()
+    exact = wide_ref.conv2d(x.cpu().double(), wide.grouped_conv.weight.detach().cpu().double(),
+                            wide.grouped_conv.bias.detach().cpu().double(), 3, padding=(1, 1))
+    assert rel_err(y, exact) <= TOL_F32
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [4, 12])     # SEQUENTIAL / GROUPED state layouts
+@pytest.mark.parametrize("stride,pad,dil", [(1, 1, 1), (2, 1, 2)])
+def test_conv1d(hip, dtype, n, stride, pad, dil):
+    import wide_compiler as wc
+    g = gen(202)
+    torch.manual_seed(202)
+    mods = [nn.Conv1d(64, 48, 3, stride=stride, padding=pad, dilation=dil) for _ in range(n)]
+    wide = wc.WideConv1d.from_modules(mods).to(DEV, dtype)
+    x = _rand((n, 8, 64, 256), g, dtype)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    w, bias = wide._filters()
+    w = w.detach().cpu().reshape(n * 48, 64, 3)
+    exact = wide_ref.conv1d(x.double(), w.double(), bias.detach().cpu().double(), n, stride=stride, padding=pad,
+                            dilation=dil)
+    assert rel_err(y, exact) <= tol(dtype)
+
+
+def _bn_modules(n, c, seed):
+    torch.manual_seed(seed)
+    mods = [nn.BatchNorm2d(c).eval() for _ in range(n)]
+    for m in mods:
+        with torch.no_grad():
+            m.running_mean.normal_(0, 0.2)
+            m.running_var.uniform_(0.5, 2.0)
+            m.weight.normal_(1.0, 0.1)
+            m.bias.normal_(0.0, 0.1)
+    return mods
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_conv_fused_bn_residual_relu(hip, dtype):
+    import wide_compiler as wc
+    g = gen(203)
+    n, b, c = 3, 2, 32
+    torch.manual_seed(203)
+    conv = wc.WideConv2d.from_modules([nn.Conv2d(c, c, 3, padding=1) for _ in range(n)]).to(DEV, dtype)
+    bn = wc.WideBatchNorm2d.from_modules(_bn_modules(n, c, 204)).to(DEV, dtype).eval()
+    conv.fused_bn = bn
+    conv.fused_activation = "relu"
+    x = _rand((n, b, c, 10, 12), g, dtype)
+    r = _rand((n, b, c, 10, 12), g, dtype)
+    with torch.no_grad():
+        y = conv(x.to(DEV), residual=r.to(DEV)).cpu()
+    op = bn.op
+    d = lambda t: t.detach().cpu().double()  # noqa: E731
+    ref = wide_ref.conv2d(x.double(), d(conv.grouped_conv.weight), d(conv.grouped_conv.bias), n, padding=(1, 1))
+    ref = wide_ref.batchnorm_eval(ref, d(op.weight), d(op.bias), d(op.running_mean), d(op.running_var), op.eps, n)
+    ref = F.relu(ref + r.double())
+    assert rel_err(y, ref) <= tol(dtype)
+
+
+class ResBlock(nn.Module):
+    """cli.py:84-97."""
+
+    def __init__(self, channels=64):
+        super().__init__()
+        self.conv1 = nn.Conv2d(channels, channels, 3, padding=1)
+        self.bn1 = nn.BatchNorm2d(channels)
+        self.conv2 = nn.Conv2d(channels, channels, 3, padding=1)
+        self.bn2 = nn.BatchNorm2d(channels)
+
+    def forward(self, x):
+        identity = x
+        out = F.relu(self.bn1(self.conv1(x)))
+        out = self.bn2(self.conv2(out))
+        return F.relu(out + identity)
+
+
+def _resblocks(n, c, dtype, seed=300):
+    mods = []
+    for i in range(n):
+        torch.manual_seed(seed + i)
+        m = ResBlock(c)
+        with torch.no_grad():
+            for bnm in (m.bn1, m.bn2):
+                bnm.weight.normal_(1.0, 0.1)
+                bnm.bias.normal_(0.0, 0.1)
+        mods.append(m.to(dtype).eval())
+    return mods
+
+
+def _params(mods):
+    from tests.test_oracle import resblock_params
+    return resblock_params(mods)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_traced_resblock_fuses_and_matches(hip, dtype):
+    import wide_compiler as wc
+    n, b, c, hw = 6, 2, 16, 8
+    mods = _resblocks(n, c, dtype)
+    g = gen(205)
+    ins = [_rand((b, c, hw, hw), g, dtype) for _ in range(n)]
+    wide = wc.compile([m.to(DEV) for m in mods], ins[0].to(DEV)).eval()
+    s = wide.summary()
+    assert s.count("fused into") == 5, s   # bn1, relu, bn2, add, relu -> conv1 / conv2 epilogues
+    packed = wide_ref.pack_inputs(ins)
+    with torch.no_grad():
+        y = wide(packed.to(DEV)).cpu()
+    p = {k: (v.double() if torch.is_tensor(v) else v) for k, v in _params([m.cpu() for m in mods]).items()}
+    exact = wide_ref.resblock_wide(packed.double(), n, p)
+    assert rel_err(y, exact) <= tol(dtype)
+    with torch.no_grad():
+        outs = wc.unpack(y, n)
+        for k in (0, n - 1):
+            assert rel_err(outs[k], mods[k](ins[k]).float()) <= tol(dtype)
+
+
+def test_resblock_config_n100(hip):
+    """The ResBlock configuration at full size: N=100, B=8, 64 channels, 32x32, bf16.
+    Checked model-by-model (the wide path has no cross-model terms) on three models."""
+    import wide_compiler as wc
+    n, b, c, hw = 100, 8, 64, 32
+    mods = _resblocks(n, c, torch.bfloat16)
+    g = gen(206)
+    x = torch.randn(b, n * c, hw, hw, generator=g).to(torch.bfloat16)
+    wide = wc.compile([m.to(DEV) for m in mods], x[:, :c].to(DEV)).eval()
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    assert y.shape == x.shape
+    for k in (0, 41, 99):
+        pk = {kk: (v.double() if torch.is_tensor(v) else v) for kk, v in _params([mods[k].cpu()]).items()}
+        exact = wide_ref.resblock_wide(x[:, k * c:(k + 1) * c].double(), 1, pk)
+        assert rel_err(y[:, k * c:(k + 1) * c], exact) <= TOL_BF16
