@@ -1,21 +1,22 @@
 """
-Wide-forward throughput of the MI355X build on one GPU.
+Wide-forward throughput of the MI355X build on one GPU.  Prints ONE JSON line.
 
-Workload (the configuration the headline metric is quoted on): WideGRU over N=32
-nn.GRU(64 -> 128, batch_first) models, x [32, 4, 32, 64] ~ N(0, 1) fp32, h0 = 0.  One
-step = one wide forward (input-projection GEMM + persistent recurrence) over that batch,
-inputs resident in HBM.  Prints ONE JSON line.
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--mode graph|eager]
+                  [--no-cpu] [--cpu-seconds S]
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode graph|eager] [--no-cpu]
+Default workload (the configuration the headline metric is quoted on): WideGRU over N=32
+nn.GRU(64 -> 128, batch_first) models, x [32, 4, 32, 64] ~ N(0, 1) fp32, h0 = 0.  The other
+configurations are selectable with --config (mlp, resblock, attention, seq).
 
-* value: samples/s = N*B*K / wall time of K steps (torch.cuda.synchronize on both sides).
+* step  = one wide forward over one batch, inputs already resident in HBM.
+* value = samples/s = N*B*K / wall time of K steps, bracketed by torch.cuda.synchronize().
   --mode graph (default) replays the forward as one captured HIP graph per step; eager
-  calls the module from Python each step (both are reported).
-* roofline: the recurrence kernel (dominant) -- algorithmic flops per launch
-  2*N*B*T*3H*H over its average duration, timed with HIP events on the launch stream;
-  peak = MI355X dense fp32 MFMA 157.3 TFLOP/s.
-* cpu_baseline: the oracle (op-for-op CPU restatement of the reference wide path, torch CPU
-  ops) on the host cores, over a bounded number of full forwards.
+  calls the module from Python; both rates are reported.
+* roofline = the dominant kernel: algorithmic flops (or bytes) per launch divided by its
+  average duration, timed with HIP events on the stream it is launched on; peaks are MI355X
+  datasheet values (dense MFMA fp32 157.3 TFLOP/s, bf16 2516.6 TFLOP/s; HBM 8 TB/s).
+* cpu_baseline = the oracle (op-for-op CPU restatement of the reference wide path, torch CPU
+  ops) on the host cores over a bounded sample, scaled to samples/s.
 """
 
 from __future__ import annotations
@@ -25,39 +26,185 @@ import json
 import os
 import sys
 import time
+from typing import Callable, Dict, Optional
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "pytorch-parallel-compiler_amd"))
 sys.path.insert(0, ROOT)
 
 METRIC = "wide fwd samples/sec (N×B) at 1 MI355X; % of MFMA / HBM roofline"
-PEAK_FP32_MFMA = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "rnn_recurrence_gru_n32.traffic.json")
+PEAK = {"fp32_mfma": 157.3e12, "bf16_mfma": 2516.6e12, "hbm": 8.0e12}
 
 
-def _cpu_baseline(work, seconds: float):
+def _rel(a, b) -> float:
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    return ((a - b).abs().max() / b.abs().max()).item()
+
+
+def _event_time(fn: Callable[[], None], k: int, w: int) -> float:
+    """Average seconds per call of fn (a kernel launch on torch's current stream)."""
     import torch
+    for _ in range(w):
+        fn()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(k):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / k * 1e-3
+
+
+def _cpu_loop(fn: Callable[[], None], seconds: float, min_iters: int = 2):
+    fn()  # warm-up
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        iters += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and iters >= min_iters) or iters >= 100000:
+            return iters, el
+
+
+# ---------------------------------------------------------------------------------------
+# configurations
+# ---------------------------------------------------------------------------------------
+
+def cfg_gru(dev, steps, warmup) -> Dict:
+    import torch
+    import wide_compiler as wc
+    from wide_compiler import _hip, workloads
     from oracle import wide_ref
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    work = workloads.gru_n32()
+    n, b = work.n, work.batch
+    x_cpu = work.inputs["x"]
+    _, _, t, i = x_cpu.shape
+    h = work.models[0].hidden_size
+    wide = wc.WideGRU.from_modules(work.models).to(dev).eval()
+    x = x_cpu.to(dev)
+
+    def parity():
+        with torch.inference_mode():
+            out, _ = wide(x)
+        p = [getattr(wide, k).detach().cpu().double() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+        ref, _ = wide_ref.gru(x_cpu.double(), *p)
+        return _rel(out, ref)
+
+    def kernels():
+        o = torch.empty((n, b, t, h), device=dev)
+        hn = torch.empty((n, b, h), device=dev)
+        a, ws = _hip.rnn_args(cell=_hip.CELL_GRU, x=x, w_ih=wide.weight_ih, w_hh=wide.weight_hh, b_ih=wide.bias_ih,
+                              b_hh=wide.bias_hh, h0=None, c0=None, out=o, h_n=hn, c_n=None)
+        kt = {ph: _event_time(lambda ph=ph: _hip.rnn_phase(a, ph, x), steps, warmup)
+              for ph in ("input_projection", "recurrence")}
+        return kt, ws
+
+    def roofline():
+        kt, _ = kernels()
+        flops = 2.0 * n * b * t * 3 * h * h
+        return {"bound": "mfma", "kernel": "rnn_seq_kernel (GRU recurrence, fp32)", "flops_per_launch": flops,
+                "sec": kt["recurrence"], "peak": PEAK["fp32_mfma"],
+                "other_kernels_us": {"input_projection_gemm": kt["input_projection"] * 1e6}}
+
     mods = work.models
-    p = [torch.stack([getattr(m, k).detach().float() for m in mods])
-         for k in ("weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0")]
-    x = work.inputs["x"]
-    with torch.inference_mode():
-        for _ in range(2):
-            wide_ref.gru(x, *p)
-        iters, t0 = 0, time.perf_counter()
-        while True:
-            wide_ref.gru(x, *p)
-            iters += 1
-            el = time.perf_counter() - t0
-            if (el >= seconds and iters >= 3) or iters >= 100000:
-                break
-    return {"value": work.n * work.batch * iters / el, "unit": "samples/s", "cores": threads, "kind": "port",
-            "sample": f"{iters} full forwards of the same workload (oracle GRU restatement, torch CPU, "
-                      f"fp32, {threads} threads), {el:.1f} s"}
+    p32 = [torch.stack([getattr(m, k).detach().float() for m in mods])
+           for k in ("weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0")]
+
+    def cpu_run():
+        wide_ref.gru(x_cpu, *p32)
+
+    return {"name": work.name, "n": n, "batch": b, "dtype": "fp32", "step": lambda: wide(x), "parity": parity,
+            "roofline": roofline, "cpu": cpu_run, "cpu_samples": n * b, "cpu_sample": "full workload",
+            "extra": {"seq_len": t, "input_size": i, "hidden": h}}
+
+
+def cfg_mlp(dev, steps, warmup) -> Dict:
+    import torch
+    import wide_compiler as wc
+    from wide_compiler import workloads
+    from oracle import wide_ref
+
+    work = workloads.mlp_n100()
+    n, b = work.n, work.batch
+    xs = work.inputs["per_model"]
+    packed_cpu = wide_ref.pack_inputs(xs)
+    models = [m.to(dev) for m in work.models]
+    wide = wc.compile(models, xs[0].to(dev)).eval()
+    packed = packed_cpu.to(dev)
+    st = lambda k: torch.stack([getattr(getattr(m, k.split('.')[0]), k.split('.')[1]).detach().cpu().float()  # noqa
+                                for m in models])
+    w1, b1, w2, b2 = st("fc1.weight"), st("fc1.bias"), st("fc2.weight"), st("fc2.bias")
+
+    def parity():
+        with torch.inference_mode():
+            y = wide(packed)
+        return _rel(y, wide_ref.mlp_wide(packed_cpu.double(), n, w1.double(), b1.double(), w2.double(),
+                                         b2.double()))
+
+    def roofline():
+        fc1 = wide.stages["fc1"]
+        xn = packed.view(b, n, 64).movedim(1, 0)
+        sec = _event_time(lambda: fc1(xn), steps, warmup)
+        byts = 4.0 * (n * 128 * 64 + n * 128 + n * b * 64 + n * b * 128)
+        return {"bound": "hbm", "kernel": "gemm_kernel (fc1 + bias + ReLU, fp32)", "bytes_per_launch": byts,
+                "sec": sec, "peak": PEAK["hbm"]}
+
+    def cpu_run():
+        wide_ref.mlp_wide(packed_cpu, n, w1, b1, w2, b2)
+
+    return {"name": work.name, "n": n, "batch": b, "dtype": "fp32", "step": lambda: wide(packed),
+            "parity": parity, "roofline": roofline, "cpu": cpu_run, "cpu_samples": n * b,
+            "cpu_sample": "full workload", "extra": {"layers": "Linear(64,128)-ReLU-Linear(128,64)"}}
+
+
+def cfg_resblock(dev, steps, warmup) -> Dict:
+    import torch
+    import wide_compiler as wc
+    from wide_compiler import workloads
+    from oracle import wide_ref
+
+    work = workloads.resblock_n100()
+    n, b, c, hw = work.n, work.batch, 64, 32
+    x_cpu = work.inputs["packed"]
+    models = [m.to(dev) for m in work.models]
+    wide = wc.compile(models, x_cpu[:, :c].to(dev)).eval()
+    x = x_cpu.to(dev)
+
+    def parity():
+        with torch.inference_mode():
+            y = wide(x).cpu()
+        errs = []
+        for k in (0, n // 2, n - 1):
+            pk = workloads.resblock_params([models[k]], torch.float64)
+            errs.append(_rel(y[:, k * c:(k + 1) * c],
+                             wide_ref.resblock_wide(x_cpu[:, k * c:(k + 1) * c].double(), 1, pk)))
+        return max(errs)
+
+    def roofline():
+        conv1 = wide.stages["conv1"]
+        xn = x.view(b, n, c, hw, hw).movedim(1, 0)
+        sec = _event_time(lambda: conv1(xn), steps, warmup)
+        flops = 2.0 * n * b * hw * hw * c * c * 9
+        return {"bound": "mfma", "kernel": "conv_kernel (conv3x3 + BN + ReLU, bf16)", "flops_per_launch": flops,
+                "sec": sec, "peak": PEAK["bf16_mfma"]}
+
+    n_cpu = 4
+    pk_cpu = workloads.resblock_params([m for m in models[:n_cpu]], torch.bfloat16)
+    x_sub = x_cpu[:, :n_cpu * c].contiguous()
+
+    def cpu_run():
+        wide_ref.resblock_wide(x_sub, n_cpu, pk_cpu)
+
+    return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": lambda: wide(x), "parity": parity,
+            "roofline": roofline, "cpu": cpu_run, "cpu_samples": n_cpu * b,
+            "cpu_sample": f"{n_cpu} of the {n} models (the wide path has no cross-model terms), bf16",
+            "extra": {"channels": c, "hw": hw}}
+
+
+CONFIGS = {"gru": cfg_gru, "mlp": cfg_mlp, "resblock": cfg_resblock}
 
 
 def main() -> int:
@@ -65,6 +212,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="gru")
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -75,28 +223,12 @@ def main() -> int:
         return 2
 
     import torch
-    import wide_compiler as wc
-    from wide_compiler import _hip, workloads
 
     dev = torch.device("cuda", 0)
-    work = workloads.gru_n32()
-    n, b = work.n, work.batch
-    x_cpu = work.inputs["x"]
-    _, _, t, i = x_cpu.shape
-    h = work.models[0].hidden_size
-    wide = wc.WideGRU.from_modules(work.models).to(dev).eval()
-    x = x_cpu.to(dev)
-
-    # ---- parity of the measured path against the oracle (float64) ----
-    from oracle import wide_ref
-    with torch.inference_mode():
-        out, _ = wide(x)
-    p64 = [getattr(wide, k).detach().cpu().double() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
-    ref, _ = wide_ref.gru(x_cpu.double(), *p64)
-    parity = ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item()
-
-    def step():
-        return wide(x)
+    cfg = CONFIGS[args.config](dev, args.steps, args.warmup)
+    n, b = cfg["n"], cfg["batch"]
+    step = cfg["step"]
+    parity = cfg["parity"]()
 
     def timed(fn, k, w):
         with torch.inference_mode():
@@ -122,40 +254,45 @@ def main() -> int:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 static_out = step()
+            eager_out = step()
         graph_s = timed(graph.replay, args.steps, args.warmup)
         with torch.inference_mode():
             torch.cuda.synchronize()
-            g_err = ((static_out[0].cpu().double() - ref).abs().max() / ref.abs().max()).item()
-        parity = max(parity, g_err)
+            go = static_out[0] if isinstance(static_out, tuple) else static_out
+            eo = eager_out[0] if isinstance(eager_out, tuple) else eager_out
+            if not torch.equal(go, eo):
+                print("bench.py: graph replay differs from the eager forward", file=sys.stderr)
+                return 3
     wall = graph_s if graph_s is not None else eager_s
 
-    # ---- per-kernel durations with HIP events on the launch stream ----
     with torch.inference_mode():
-        o = torch.empty((n, b, t, h), device=dev)
-        hn = torch.empty((n, b, h), device=dev)
-        a, ws = _hip.rnn_args(cell=_hip.CELL_GRU, x=x, w_ih=wide.weight_ih, w_hh=wide.weight_hh,
-                              b_ih=wide.bias_ih, b_hh=wide.bias_hh, h0=None, c0=None, out=o, h_n=hn, c_n=None)
-        kt = {}
-        for phase in ("input_projection", "recurrence"):
-            for _ in range(args.warmup):
-                _hip.rnn_phase(a, phase, x)
-            st = torch.cuda.current_stream()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(st)
-            for _ in range(args.steps):
-                _hip.rnn_phase(a, phase, x)
-            e1.record(st)
-            e1.synchronize()
-            kt[phase] = e0.elapsed_time(e1) / args.steps * 1e-3  # seconds per launch
-    flops_rec = 2.0 * n * b * t * 3 * h * h
-    flops_proj = 2.0 * n * b * t * 3 * h * i
-    achieved = flops_rec / kt["recurrence"]
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+        rf = cfg["roofline"]()
+    if "flops_per_launch" in rf:
+        achieved = rf["flops_per_launch"] / rf["sec"]
+        unit, scale = "TFLOP/s", 1e12
+    else:
+        achieved = rf["bytes_per_launch"] / rf["sec"]
+        unit, scale = "GB/s", 1e9
+    roofline = {"bound": rf["bound"], "achieved": achieved / scale, "peak": rf["peak"] / scale, "unit": unit,
+                "frac": achieved / rf["peak"], "traffic": None, "kernel": rf["kernel"],
+                "us_per_launch": rf["sec"] * 1e6}
+    for key in ("flops_per_launch", "bytes_per_launch", "other_kernels_us"):
+        if key in rf:
+            roofline[key] = rf[key]
+    traffic_file = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            roofline["traffic"] = json.load(f).get("bytes_per_launch")
 
-    cpu = None if args.no_cpu else _cpu_baseline(work, args.cpu_seconds)
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        torch.set_num_threads(threads)
+        with torch.inference_mode():
+            iters, el = _cpu_loop(cfg["cpu"], args.cpu_seconds)
+        cpu = {"value": cfg["cpu_samples"] * iters / el, "unit": "samples/s", "cores": threads, "kind": "port",
+               "sample": f"{iters} forwards of the oracle ({cfg['cpu_sample']}; torch CPU ops, {threads} threads) "
+                         f"in {el:.1f} s"}
 
     line = {
         "metric": METRIC,
@@ -168,17 +305,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic (seeded torch.nn default init, x ~ N(0,1))",
-        "config": {"workload": work.name, "n_models": n, "batch": b, "seq_len": t, "input_size": i,
-                   "hidden": h, "mode": args.mode},
-        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
-                     "kernel": "rnn_seq_kernel (recurrence)", "flops_per_launch": flops_rec,
-                     "us_per_launch": kt["recurrence"] * 1e6},
-        "kernels_us": {"input_projection_gemm": kt["input_projection"] * 1e6,
-                       "recurrence": kt["recurrence"] * 1e6,
-                       "input_projection_tflops": flops_proj / kt["input_projection"] / 1e12},
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded torch.nn default init, inputs ~ N(0,1))",
+        "config": {"workload": cfg["name"], "n_models": n, "batch": b, "mode": args.mode, **cfg["extra"]},
+        "roofline": roofline,
         "eager_samples_per_s": n * b * args.steps / eager_s,
         "graph_samples_per_s": None if graph_s is None else n * b * args.steps / graph_s,
         "parity_rel_err_vs_oracle": parity,

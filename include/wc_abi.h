@@ -262,6 +262,31 @@ typedef struct wc_conv_args {
 
 int32_t wc_conv2d(const wc_conv_args* args, void* stream);
 
+/*
+ * Fused multi-head attention core -- replaces the view/permute/reshape to
+ * [N*B, H, T, Dh], F.scaled_dot_product_attention and the permute back of
+ * WideAttention._forward_fused (wide_compiler/core/primitives/wide_attention.py:
+ * 215-231):  O = softmax(Q K^T * scale [+ causal mask]) V  per (n*b, head).
+ * Q/K/V/O rows live at base + nb*stride_nb + s*stride_s + head*head_dim, i.e. the
+ * [N*B, S, heads*head_dim] layout of the projection outputs, read in place.
+ * head_dim in {16, 32, 64, 128}; dtype WC_F32 or WC_BF16; fp32 softmax / accumulation.
+ */
+typedef struct wc_attn_args {
+  int32_t dtype, causal;
+  int64_t nb, heads, sq, skv, head_dim;
+  float scale;
+  const void* q;
+  int64_t q_stride_nb, q_stride_s;
+  const void* k;
+  int64_t k_stride_nb, k_stride_s;
+  const void* v;
+  int64_t v_stride_nb, v_stride_s;
+  void* o;
+  int64_t o_stride_nb, o_stride_s;
+} wc_attn_args;
+
+int32_t wc_attention(const wc_attn_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

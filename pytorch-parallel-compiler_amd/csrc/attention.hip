@@ -1,0 +1,353 @@
+// Fused multi-head attention (softmax(Q K^T * scale) V per (model, batch, head))
+// on MFMA with an online (flash-style) softmax over key tiles.
+//
+// Layout: Q, K, V, O are read / written in place in the [N*B, S, heads*Dh]
+// layout the projection GEMMs produce (head h = columns [h*Dh, (h+1)*Dh)), so no
+// head-major copies are made.
+//
+// Per workgroup: one (model*batch, head) pair and a tile of 128 queries, four
+// waves of 32 queries each.  For every tile of 64 keys:
+//   S^T = K Q^T          (MFMA; the output layout puts 4 consecutive keys of
+//                         one query in each lane)
+//   online softmax       column-wise over keys: running max m and sum l per query
+//   O^T += V^T P^T       (MFMA; P^T is consumed straight from the S^T registers:
+//                         the 32-key reduction step takes keys {4g..4g+3,
+//                         16+4g..16+4g+3} from lane group g, and V^T is read from
+//                         LDS in that same key order, so P never goes through LDS)
+// K tiles are staged in LDS row-major, V tiles transposed (V^T [Dh][keys]); the
+// next tile is fetched into registers while the current one is processed.
+// Scores are scaled by log2(e)/sqrt(Dh) so the exponentials are v_exp_f32 (2^x).
+#include "wc_common.h"
+
+namespace wc {
+namespace {
+
+struct AttnParams {
+  int nb, heads, sq, skv, causal, q_tiles;
+  float scale_log2;
+  const void* q;
+  int64_t q_sb, q_ss;
+  const void* k;
+  int64_t k_sb, k_ss;
+  const void* v;
+  int64_t v_sb, v_ss;
+  void* o;
+  int64_t o_sb, o_ss;
+};
+
+constexpr int kAttnThreads = 256;
+constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
+constexpr int kBK = 64;    // keys per tile
+
+__device__ __forceinline__ float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
+__device__ __forceinline__ float xor_sum(float v, int m) { return v + __shfl_xor(v, m, 64); }
+
+template <typename T, int DH>
+__global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int DHP = DH < 32 ? 32 : DH;       // head dim padded to the 32-wide S^T k-step
+  constexpr int KP = DHP + (BF ? 8 : 4);       // K tile pitch (elements)
+  constexpr int VP = kBK + (BF ? 8 : 4);       // V^T tile pitch (elements)
+  constexpr int DT = DH / 16;                  // 16-row tiles of O^T
+  constexpr int NKS = DHP / 32;                // 32-wide head-dim steps of S^T = K Q^T
+  extern __shared__ float4 smem4[];
+  T* const ks0 = reinterpret_cast<T*>(smem4);   // [2][kBK * KP]  K tiles
+  T* const vt0 = ks0 + 2 * kBK * KP;            // [2][DH * VP]   V^T tiles
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int fr = lane & 15, g = lane >> 4;
+  const int qt = blockIdx.x % p.q_tiles;
+  const int bh = blockIdx.x / p.q_tiles;
+  const int nb = bh / p.heads, h = bh - (bh / p.heads) * p.heads;
+  const T* qb = static_cast<const T*>(p.q) + nb * p.q_sb + h * DH;
+  const T* kb = static_cast<const T*>(p.k) + nb * p.k_sb + h * DH;
+  const T* vb = static_cast<const T*>(p.v) + nb * p.v_sb + h * DH;
+  T* ob = static_cast<T*>(p.o) + nb * p.o_sb + h * DH;
+  const int q0 = qt * kBQ + wave * 32;           // first query of this wave
+
+  // ---- Q^T fragments (B operand of S^T = K Q^T), kept in registers ----
+  // lane supplies Q[q = q0 + nt*16 + fr][d = s*32 + g*8 .. +8] (fp32: two 16-byte halves)
+  uint4 qf[2][NKS][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int q = q0 + nt * 16 + fr;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const T* src = qb + q * p.q_ss + s * 32 + g * 8;
+      const bool ok = q < p.sq && s * 32 + g * 8 < DH;   // head-dim padding reads as zero
+      qf[nt][s][0] = ok ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+      qf[nt][s][1] = (!BF && ok) ? *reinterpret_cast<const uint4*>(src + (BF ? 0 : 4)) : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // ---- staging of one K / V tile: each thread moves one 16-byte row piece of each ----
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int PIECES = kBK * DH / VE;          // 16-byte pieces per tile
+  uint4 kreg[(PIECES + kAttnThreads - 1) / kAttnThreads], vreg[(PIECES + kAttnThreads - 1) / kAttnThreads];
+  constexpr int PPT = (PIECES + kAttnThreads - 1) / kAttnThreads;
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int e = tid + u * kAttnThreads;
+      const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
+      const bool ok = e < PIECES && k0 + key < p.skv;
+      kreg[u] = ok ? *reinterpret_cast<const uint4*>(kb + (k0 + key) * p.k_ss + c) : make_uint4(0, 0, 0, 0);
+      vreg[u] = ok ? *reinterpret_cast<const uint4*>(vb + (k0 + key) * p.v_ss + c) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int e = tid + u * kAttnThreads;
+      if (e >= PIECES) continue;
+      const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
+      *reinterpret_cast<uint4*>(&ks0[buf * kBK * KP + key * KP + c]) = kreg[u];
+      const T* vv = reinterpret_cast<const T*>(&vreg[u]);
+#pragma unroll
+      for (int q = 0; q < VE; ++q) vt0[buf * DH * VP + (c + q) * VP + key] = vv[q];
+    }
+  };
+
+  f32x4 acc_o[DT][2];
+#pragma unroll
+  for (int i = 0; i < DT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc_o[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+
+  int kend = p.skv;
+  if (p.causal) {
+    const int qlast = qt * kBQ + kBQ - 1;
+    kend = qlast + 1 < p.skv ? qlast + 1 : p.skv;
+  }
+  const int ntiles = (kend + kBK - 1) / kBK;
+  if (DHP != DH) {
+    // zero the padded head-dim columns of both K buffers once (stash never writes them)
+    for (int e = tid; e < 2 * kBK * (DHP - DH); e += kAttnThreads) {
+      const int row = e / (DHP - DH), c = DH + (e - row * (DHP - DH));
+      ks0[row * KP + c] = from_f32<T>(0.f);
+    }
+  }
+  fetch(0);
+  stash(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int buf = kt & 1;
+    const int k0 = kt * kBK;
+    if (kt + 1 < ntiles) fetch(k0 + kBK);
+    const T* kt_s = ks0 + buf * kBK * KP;
+    const T* vt_s = vt0 + buf * DH * VP;
+
+    // ---- S^T = K Q^T : [64 keys x 32 queries] per wave ----
+    f32x4 sacc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const T* krow = kt_s + (mt * 16 + fr) * KP + g * 8;
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) {
+        if constexpr (BF) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(krow + s * 32);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                a, *reinterpret_cast<const bf16x8*>(&qf[nt][s][0]), sacc[mt][nt], 0, 0, 0);
+        } else {
+          const f32x4 a0 = *reinterpret_cast<const f32x4*>(krow + s * 32);
+          const f32x4 a1 = *reinterpret_cast<const f32x4*>(krow + s * 32 + 4);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            const f32x4 b0 = *reinterpret_cast<const f32x4*>(&qf[nt][s][0]);
+            const f32x4 b1 = *reinterpret_cast<const f32x4*>(&qf[nt][s][1]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[j], b0[j], sacc[mt][nt], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[j], b1[j], sacc[mt][nt], 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    // ---- online softmax over keys (rows of S^T), per query column ----
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int q = q0 + nt * 16 + fr;
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + mt * 16 + g * 4 + e;
+          float sv = sacc[mt][nt][e] * p.scale_log2;
+          if (key >= p.skv || (p.causal && key > q)) sv = -INFINITY;
+          sacc[mt][nt][e] = sv;
+          tmax = fmaxf(tmax, sv);
+        }
+      tmax = xor_max(xor_max(tmax, 16), 32);
+      const float m_new = fmaxf(m_run[nt], tmax);
+      // rows with no valid key so far keep m = -inf; use 0 as the exponent base then
+      const float base = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run[nt] - base);
+      float tsum = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pv = exp2f(sacc[mt][nt][e] - base);
+          sacc[mt][nt][e] = pv;
+          tsum += pv;
+        }
+      tsum = xor_sum(xor_sum(tsum, 16), 32);
+      l_run[nt] = l_run[nt] * alpha + tsum;
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc_o[dt][nt] *= alpha;
+    }
+
+    // ---- O^T += V^T P^T ----
+    if constexpr (BF) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {           // 32-key steps
+        bf16x8 bp[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            bp[nt][e] = static_cast<bf16>(sacc[2 * s][nt][e]);
+            bp[nt][4 + e] = static_cast<bf16>(sacc[2 * s + 1][nt][e]);
+          }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const T* vrow = vt_s + (dt * 16 + fr) * VP + s * 32 + g * 4;
+          bf16x8 a;
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 16);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            a[e] = lo[e];
+            a[4 + e] = hi[e];
+          }
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            acc_o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[nt], acc_o[dt][nt], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)          // 16-key tiles, 4 k-slots each
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(vt_s + (dt * 16 + fr) * VP + mt * 16 + g * 4);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc_o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], sacc[mt][nt][j], acc_o[dt][nt], 0, 0, 0);
+        }
+    }
+
+    if (kt + 1 < ntiles) {
+      // buffer buf^1 was last read in the previous iteration, before its closing barrier
+      stash(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // ---- O = (O^T / l)^T : lane holds O[q][d = dt*16 + g*4 + e] ----
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int q = q0 + nt * 16 + fr;
+    if (q >= p.sq) continue;
+    const float inv = l_run[nt] > 0.f ? 1.0f / l_run[nt] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      T* dst = ob + q * p.o_ss + dt * 16 + g * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc_o[dt][nt][e] * inv);
+    }
+  }
+}
+
+template <typename T, int DH>
+int32_t launch_attn_dh(const AttnParams& p, dim3 grid, hipStream_t st) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr size_t lds = sizeof(T) * 2 * (static_cast<size_t>(kBK) * ((DH < 32 ? 32 : DH) + (BF ? 8 : 4)) +
+                                          static_cast<size_t>(DH) * (kBK + (BF ? 8 : 4)));
+  auto kernel = attn_kernel<T, DH>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_attention: LDS of %zu bytes refused: %s", lds,
+                       hipGetErrorString(e));
+  }
+  kernel<<<grid, kAttnThreads, lds, st>>>(p);
+  return check_launch("wc_attention");
+}
+
+template <typename T>
+int32_t launch_attn(const AttnParams& p, int dh, hipStream_t st) {
+  const int64_t blocks = static_cast<int64_t>(p.nb) * p.heads * p.q_tiles;
+  if (blocks >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_attention: too many tiles");
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  switch (dh) {
+    case 16: return launch_attn_dh<T, 16>(p, grid, st);
+    case 32: return launch_attn_dh<T, 32>(p, grid, st);
+    case 64: return launch_attn_dh<T, 64>(p, grid, st);
+    case 128: return launch_attn_dh<T, 128>(p, grid, st);
+    default: return set_error(WC_ERR_LIMIT, "wc_attention: head dim %d unsupported (16, 32, 64, 128)", dh);
+  }
+}
+
+}  // namespace
+}  // namespace wc
+
+using namespace wc;
+
+extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
+  clear_error();
+  WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_attention: null args");
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "wc_attention: unsupported dtype %s",
+             dtype_name(a->dtype));
+  WC_REQUIRE(a->nb >= 0 && a->heads > 0 && a->sq >= 0 && a->skv >= 0 && a->head_dim > 0, WC_ERR_SHAPE,
+             "wc_attention: bad sizes");
+  if (a->nb == 0 || a->sq == 0) return WC_OK;
+  WC_REQUIRE(a->skv > 0, WC_ERR_SHAPE, "wc_attention: no keys");
+  WC_REQUIRE(a->q && a->k && a->v && a->o, WC_ERR_NULL, "wc_attention: null pointer");
+  const int es = dtype_size(a->dtype);
+  const bool al = aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 16) &&
+                  (a->q_stride_nb * es) % 16 == 0 && (a->q_stride_s * es) % 16 == 0 &&
+                  (a->k_stride_nb * es) % 16 == 0 && (a->k_stride_s * es) % 16 == 0 &&
+                  (a->v_stride_nb * es) % 16 == 0 && (a->v_stride_s * es) % 16 == 0;
+  WC_REQUIRE(al, WC_ERR_ALIGN, "wc_attention: q/k/v rows must be 16-byte aligned");
+  WC_REQUIRE(a->sq < 0x7fffffffll && a->skv < 0x7fffffffll && a->nb < 0x7fffffffll, WC_ERR_LIMIT,
+             "wc_attention: sizes too large");
+  AttnParams p;
+  p.nb = (int)a->nb;
+  p.heads = (int)a->heads;
+  p.sq = (int)a->sq;
+  p.skv = (int)a->skv;
+  p.causal = a->causal ? 1 : 0;
+  p.q_tiles = static_cast<int>(cdiv(a->sq, kBQ));
+  p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.q = a->q;
+  p.q_sb = a->q_stride_nb;
+  p.q_ss = a->q_stride_s;
+  p.k = a->k;
+  p.k_sb = a->k_stride_nb;
+  p.k_ss = a->k_stride_s;
+  p.v = a->v;
+  p.v_sb = a->v_stride_nb;
+  p.v_ss = a->v_stride_s;
+  p.o = a->o;
+  p.o_sb = a->o_stride_nb;
+  p.o_ss = a->o_stride_s;
+  if (a->dtype == WC_BF16) return launch_attn<bf16>(p, (int)a->head_dim, as_stream(stream));
+  return launch_attn<float>(p, (int)a->head_dim, as_stream(stream));
+}

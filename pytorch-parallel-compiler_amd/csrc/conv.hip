@@ -31,6 +31,7 @@ struct ConvParams {
   int ir, ic;               // input tile rows / cols
   int tiles_r, tiles_c, tiles_co;
   int remap, act, vec_out;
+  FastDiv fd_plane, fd_ic;  // ir*ic and ic
   const void* x;
   int64_t x_sn, x_sb;
   const void* wp;           // packed weights [n][co][kh][kw][ci32]
@@ -55,12 +56,14 @@ __device__ __forceinline__ float ldp(const void* p, int dt, int64_t i) {
 }
 
 template <typename T> struct ConvTraits;
+// Tile sizes keep one workgroup's LDS near 50 KB so three workgroups share a CU
+// and hide each other's global-memory latency.
 template <> struct ConvTraits<bf16> {
-  static constexpr int kFM = 8;    // 128 pixels per wave
+  static constexpr int kFM = 4;    // 64 pixels per wave, 256 per tile
   static constexpr int kPad = 8;   // channel pitch padding (elements)
 };
 template <> struct ConvTraits<float> {
-  static constexpr int kFM = 4;    // 64 pixels per wave
+  static constexpr int kFM = 2;    // 32 pixels per wave, 128 per tile
   static constexpr int kPad = 4;
 };
 
@@ -122,19 +125,46 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
   const int taps = p.kh * p.kw;
   for (int c0 = 0; c0 < p.ci32; c0 += p.cc) {
     // ---- stage input channels [c0, c0+cc) of the tile as [row][col][ci] ----
+    // unit = (group of 8 channels, tile pixel): 8 loads (consecutive lanes read
+    // consecutive pixels of one channel plane -> coalesced), one 16-byte LDS store.
     if (c0 > 0) __syncthreads();
-    const int plane = p.ir * p.ic;
-    const int tot = p.cc * plane;
-    for (int e = tid; e < tot; e += kConvThreads) {
-      const int c = e / plane;
-      const int rc = e - c * plane;
-      const int r = rc / p.ic;
-      const int col = rc - r * p.ic;
-      const int hi = hi0 + r, wi = wi0 + col, ch = c0 + c;
-      T v = from_f32<T>(0.f);
-      if (ch < p.ci && hi >= 0 && hi < p.h && wi >= 0 && wi < p.w)
-        v = xb[(static_cast<int64_t>(ch) * p.h + hi) * p.w + wi];
-      xs[rc * cip + c] = v;
+    {
+      const int plane = p.ir * p.ic;
+      const int units = (p.cc >> 3) * plane;
+      constexpr int U = 8;   // units per thread in flight: all loads issued before the stores
+      for (int e0 = tid; e0 < units; e0 += U * kConvThreads) {
+        T v[U][8];
+        int dst[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int e = e0 + u * kConvThreads;
+          dst[u] = -1;
+          if (e < units) {
+            const int cg = static_cast<int>(fdiv(static_cast<uint32_t>(e), p.fd_plane));
+            const int rc = e - cg * plane;
+            const int r = static_cast<int>(fdiv(static_cast<uint32_t>(rc), p.fd_ic));
+            const int col = rc - r * p.ic;
+            const int hi = hi0 + r, wi = wi0 + col, ch0 = c0 + cg * 8;
+            const bool in = hi >= 0 && hi < p.h && wi >= 0 && wi < p.w;
+            const T* src = xb + (static_cast<int64_t>(ch0) * p.h + hi) * p.w + wi;
+            const int64_t cstride = static_cast<int64_t>(p.h) * p.w;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+              v[u][q] = (in && ch0 + q < p.ci) ? src[q * cstride] : from_f32<T>(0.f);
+            dst[u] = rc * cip + cg * 8;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (dst[u] < 0) continue;
+          if constexpr (sizeof(T) == 2) {
+            *reinterpret_cast<uint4*>(&xs[dst[u]]) = *reinterpret_cast<const uint4*>(v[u]);
+          } else {
+            *reinterpret_cast<uint4*>(&xs[dst[u]]) = *reinterpret_cast<const uint4*>(v[u]);
+            *reinterpret_cast<uint4*>(&xs[dst[u] + 4]) = *reinterpret_cast<const uint4*>(v[u] + 4);
+          }
+        }
+      }
     }
     __syncthreads();
 
@@ -233,30 +263,46 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
   const int how = p.ho * p.wo;
   constexpr int VE = 16 / sizeof(T);
   if (p.vec_out) {
-    // tc % VE == 0, wo0 % VE == 0, rows of y / res 16-byte aligned
+    // tc % VE == 0, wo0 % VE == 0, rows of y / res 16-byte aligned; EB chunks per
+    // thread are handled together so their residual loads are in flight at once
+    constexpr int EB = 4;
     const int chunks = 64 * (TPIX / VE);
-    for (int e = tid; e < chunks; e += kConvThreads) {
-      const int col = e / (TPIX / VE);
-      const int px = (e - col * (TPIX / VE)) * VE;
-      const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
-      const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
-      if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
-      const int64_t off = static_cast<int64_t>(co) * how + oh * p.wo + ow;
-      float v[VE];
-      const T* src = &cs[col * CPITCH + px];
+    for (int e0 = tid; e0 < chunks; e0 += EB * kConvThreads) {
+      int64_t off[EB];
+      int lds_at[EB];
+      uint4 rv[EB];
 #pragma unroll
-      for (int q = 0; q < VE; ++q) v[q] = to_f32(src[q]);
-      if (rb) {
-        const uint4 rv = *reinterpret_cast<const uint4*>(rb + off);
-        const T* rr = reinterpret_cast<const T*>(&rv);
-#pragma unroll
-        for (int q = 0; q < VE; ++q) v[q] = to_f32(from_f32<T>(v[q] + to_f32(rr[q])));
+      for (int u = 0; u < EB; ++u) {
+        const int e = e0 + u * kConvThreads;
+        off[u] = -1;
+        if (e >= chunks) continue;
+        const int col = e / (TPIX / VE);
+        const int px = (e - col * (TPIX / VE)) * VE;
+        const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+        const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
+        if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
+        off[u] = static_cast<int64_t>(co) * how + oh * p.wo + ow;
+        lds_at[u] = col * CPITCH + px;
+        if (rb) rv[u] = *reinterpret_cast<const uint4*>(rb + off[u]);
       }
-      uint4 ov;
-      T* oo = reinterpret_cast<T*>(&ov);
 #pragma unroll
-      for (int q = 0; q < VE; ++q) oo[q] = from_f32<T>(p.act == WC_ACT_RELU ? fmaxf(v[q], 0.f) : v[q]);
-      *reinterpret_cast<uint4*>(yb + off) = ov;
+      for (int u = 0; u < EB; ++u) {
+        if (off[u] < 0) continue;
+        float v[VE];
+        const T* src = &cs[lds_at[u]];
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = to_f32(src[q]);
+        if (rb) {
+          const T* rr = reinterpret_cast<const T*>(&rv[u]);
+#pragma unroll
+          for (int q = 0; q < VE; ++q) v[q] = to_f32(from_f32<T>(v[q] + to_f32(rr[q])));
+        }
+        uint4 ov;
+        T* oo = reinterpret_cast<T*>(&ov);
+#pragma unroll
+        for (int q = 0; q < VE; ++q) oo[q] = from_f32<T>(p.act == WC_ACT_RELU ? fmaxf(v[q], 0.f) : v[q]);
+        *reinterpret_cast<uint4*>(yb + off[u]) = ov;
+      }
     }
   } else {
     for (int e = tid; e < 64 * TPIX; e += kConvThreads) {
@@ -422,6 +468,8 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   const bool f32 = a->dtype == WC_F32;
   if (!(f32 ? conv_plan<float>(p) : conv_plan<bf16>(p)))
     return set_error(WC_ERR_LIMIT, "wc_conv2d: tile does not fit in LDS");
+  p.fd_plane = make_fastdiv(static_cast<uint32_t>(p.ir * p.ic));
+  p.fd_ic = make_fastdiv(static_cast<uint32_t>(p.ic));
   p.tiles_r = static_cast<int>(cdiv(p.ho, p.tr));
   p.tiles_c = static_cast<int>(cdiv(p.wo, p.tc));
   p.tiles_co = static_cast<int>(cdiv(p.co, 64));

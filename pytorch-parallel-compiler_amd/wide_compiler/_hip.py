@@ -90,6 +90,18 @@ class _ConvArgs(ctypes.Structure):
     ]
 
 
+class _AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
+        ("nb", ctypes.c_int64), ("heads", ctypes.c_int64), ("sq", ctypes.c_int64), ("skv", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64), ("scale", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("q_stride_nb", ctypes.c_int64), ("q_stride_s", ctypes.c_int64),
+        ("k", ctypes.c_void_p), ("k_stride_nb", ctypes.c_int64), ("k_stride_s", ctypes.c_int64),
+        ("v", ctypes.c_void_p), ("v_stride_nb", ctypes.c_int64), ("v_stride_s", ctypes.c_int64),
+        ("o", ctypes.c_void_p), ("o_stride_nb", ctypes.c_int64), ("o_stride_s", ctypes.c_int64),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -113,6 +125,7 @@ SIGNATURES = {
     "wc_conv_pack_weights": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P]),
     "wc_conv_packed_weight_elems": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "wc_conv2d": (_I32, [ctypes.POINTER(_ConvArgs), _P]),
+    "wc_attention": (_I32, [ctypes.POINTER(_AttnArgs), _P]),
 }
 
 
@@ -316,6 +329,22 @@ def conv2d(*, x: Tensor, packed_w: Tensor, n: int, c_in: int, c_out: int, kernel
         a.residual, a.r_stride_n, a.r_stride_b = residual.data_ptr(), residual.stride(0), residual.stride(1)
     a.y, a.y_stride_n, a.y_stride_b = y.data_ptr(), y.stride(0), y.stride(1)
     _check(lib().wc_conv2d(ctypes.byref(a), stream_of(x)), "wc_conv2d")
+
+
+def attention(*, q: Tensor, k: Tensor, v: Tensor, o: Tensor, nb: int, heads: int, sq: int, skv: int,
+              head_dim: int, q_strides, k_strides, v_strides, o_strides, scale: float, causal: bool) -> None:
+    """q/k/v/o are base pointers (views) of [nb, S, heads*head_dim]-shaped data with the given
+    (stride_nb, stride_s) element strides."""
+    a = _AttnArgs()
+    a.dtype = dtype_code(q.dtype, "attention")
+    a.causal = 1 if causal else 0
+    a.nb, a.heads, a.sq, a.skv, a.head_dim = nb, heads, sq, skv, head_dim
+    a.scale = float(scale)
+    a.q, (a.q_stride_nb, a.q_stride_s) = q.data_ptr(), q_strides
+    a.k, (a.k_stride_nb, a.k_stride_s) = k.data_ptr(), k_strides
+    a.v, (a.v_stride_nb, a.v_stride_s) = v.data_ptr(), v_strides
+    a.o, (a.o_stride_nb, a.o_stride_s) = o.data_ptr(), o_strides
+    _check(lib().wc_attention(ctypes.byref(a), stream_of(q)), "wc_attention")
 
 
 def exported_symbols() -> List[str]:

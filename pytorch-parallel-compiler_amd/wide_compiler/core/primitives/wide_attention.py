@@ -7,6 +7,12 @@ WideAttention: N independent nn.MultiheadAttention modules
 
 Parameters keep the reference layout: q_weight [N, D, D], kv_weight [N, 2D, D],
 out_weight [N, D, D], q_bias [N, D], kv_bias [N, 2D], out_bias [N, D].
+
+Execution (every strategy): the Q and K/V projections are grouped MFMA GEMMs with the bias
+in the epilogue (one K|V GEMM over kv_weight when key is value), the attention core is the
+fused flash-style kernel wc_attention reading Q/K/V in place in the projections' [N*B, S,
+heads*Dh] layout, and the output projection is a third grouped GEMM.  Inference only:
+dropout in training mode and explicit attention masks raise (``is_causal`` is supported).
 """
 
 from __future__ import annotations
@@ -74,7 +80,66 @@ class WideAttention(nn.Module):
     def forward(self, query: Tensor, key: Optional[Tensor] = None, value: Optional[Tensor] = None,
                 attn_mask: Optional[Tensor] = None, is_causal: bool = False,
                 need_weights: bool = False) -> Union[Tensor, Tuple[Tensor, None]]:
-        raise NotImplementedError("WideAttention: the attention kernel is not built yet")
+        mha_mode = key is not None
+        if key is None:
+            key = query
+        if value is None:
+            value = key
+        out = self._attend(query, key, value, attn_mask, is_causal)
+        return (out, None) if mha_mode else out
+
+    def _project(self, x: Tensor, w: Tensor, w_sn: int, bias: Optional[Tensor], b_sn: int, o: int) -> Tensor:
+        """[N, B, T, D] @ W[n]^T + b -> [N, B, T, o] via the grouped GEMM (x read in place)."""
+        from .._layout import rows_or_contiguous
+        x, r = rows_or_contiguous(x)
+        out = torch.empty((*x.shape[:-1], o), dtype=x.dtype, device=x.device)
+        m = r.rows
+        _hip.grouped_gemm(n=self.n, m=m, o=o, k=self.d_model, a=x, a_sn=r.stride_n, a_so=r.stride_outer,
+                          a_si=r.stride_inner, a_rows_inner=r.rows_inner, w=w, w_sn=w_sn, c=out,
+                          c_sn=m * o, c_so=0, c_si=o, c_rows_inner=max(m, 1), bias=bias, bias_sn=b_sn)
+        return out
+
+    def _attend(self, query: Tensor, key: Tensor, value: Tensor, attn_mask: Optional[Tensor],
+                is_causal: bool) -> Tensor:
+        what = "WideAttention"
+        n, d, hh, dh = self.n, self.d_model, self.n_heads, self.d_head
+        params = (self.q_weight, self.kv_weight, self.out_weight, self.q_bias, self.kv_bias, self.out_bias)
+        _hip.require_device(what, query, key, value, *params)
+        _hip.require_forward_only(what, query, key, value, *params)
+        if attn_mask is not None:
+            raise NotImplementedError(f"{what}: explicit attention masks are not supported (is_causal is)")
+        if self.training and self.dropout > 0:
+            raise RuntimeError(f"{what}: attention dropout in training mode is not supported (forward-only "
+                               "inference kernels); call .eval()")
+        for name, t in (("query", query), ("key", key), ("value", value)):
+            if t.dim() != 4 or t.shape[0] != n or t.shape[3] != d:
+                raise RuntimeError(f"{what}: {name} must be [N={n}, B, T, {d}], got {list(t.shape)}")
+            if t.dtype != self.q_weight.dtype:
+                raise RuntimeError(f"{what}: {name} dtype {t.dtype} != weight dtype {self.q_weight.dtype}")
+        b, tq, tkv = query.shape[1], query.shape[2], key.shape[2]
+        if key.shape[1] != b or value.shape[1] != b or value.shape[2] != tkv:
+            raise RuntimeError(f"{what}: key/value must be [N, B={b}, Tkv, D] with matching Tkv")
+        kvw = self.kv_weight if self.kv_weight.is_contiguous() else self.kv_weight.contiguous()
+        qw = self.q_weight if self.q_weight.is_contiguous() else self.q_weight.contiguous()
+        ow = self.out_weight if self.out_weight.is_contiguous() else self.out_weight.contiguous()
+        kvb = self.kv_bias
+        q = self._project(query, qw, d * d, self.q_bias, d, d)
+        if key is value:
+            kv = self._project(key, kvw, 2 * d * d, kvb, 2 * d, 2 * d)       # [N, B, Tkv, 2D]: K | V
+            k_t, v_t = kv, kv[..., d:]
+            k_strides = (tkv * 2 * d, 2 * d)
+            v_strides = k_strides
+        else:
+            k_t = self._project(key, kvw, 2 * d * d, kvb, 2 * d, d)
+            v_t = self._project(value, kvw[:, d:], 2 * d * d, None if kvb is None else kvb[:, d:], 2 * d, d)
+            k_strides = (tkv * d, d)
+            v_strides = (tkv * d, d)
+        attn = torch.empty((n, b, tq, d), dtype=query.dtype, device=query.device)
+        if tq > 0 and tkv > 0:
+            _hip.attention(q=q, k=k_t, v=v_t, o=attn, nb=n * b, heads=hh, sq=tq, skv=tkv, head_dim=dh,
+                           q_strides=(tq * d, d), k_strides=k_strides, v_strides=v_strides, o_strides=(tq * d, d),
+                           scale=dh ** -0.5, causal=is_causal)
+        return self._project(attn, ow, d * d, self.out_bias, d, d)
 
     @classmethod
     def from_modules(cls, modules: List[nn.MultiheadAttention],

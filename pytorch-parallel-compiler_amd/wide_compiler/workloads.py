@@ -65,3 +65,51 @@ def gru_n32(n: int = 32, batch: int = 4, steps: int = 32, in_size: int = 64, hid
         models.append(nn.GRU(in_size, hidden, batch_first=True))
     x = torch.randn(n, batch, steps, in_size, generator=_gen())
     return Workload(f"WideGRU N={n} B={batch} T={steps} {in_size}->{hidden} fp32", n, batch, models, {"x": x})
+
+
+class ResBlock(nn.Module):
+    """conv3x3 - BN - ReLU - conv3x3 - BN - (+x) - ReLU: the reference CLI's ResBlock (cli.py:84-97)."""
+
+    def __init__(self, channels: int = 64):
+        super().__init__()
+        self.conv1 = nn.Conv2d(channels, channels, 3, padding=1)
+        self.bn1 = nn.BatchNorm2d(channels)
+        self.conv2 = nn.Conv2d(channels, channels, 3, padding=1)
+        self.bn2 = nn.BatchNorm2d(channels)
+
+    def forward(self, x):
+        identity = x
+        out = F.relu(self.bn1(self.conv1(x)))
+        out = self.bn2(self.conv2(out))
+        return F.relu(out + identity)
+
+
+def resblock_n100(n: int = 100, batch: int = 8, channels: int = 64, hw: int = 32) -> Workload:
+    """N=100 ResBlock(64) in eval mode, everything bf16.  BatchNorm running mean 0 / var 1 (the
+    nn defaults), affine weight ~ N(1, 0.1) and bias ~ N(0, 0.1) (the configuration text gives
+    both as "~N(1, 0.1)"; a zero-centred shift keeps the residual path balanced, recorded as a
+    choice of this build).  Input [8, 6400, 32, 32] ~ N(0, 1), channel-packed."""
+    models = []
+    for i in range(n):
+        torch.manual_seed(SEED + i)
+        m = ResBlock(channels)
+        with torch.no_grad():
+            for bn in (m.bn1, m.bn2):
+                bn.weight.normal_(1.0, 0.1)
+                bn.bias.normal_(0.0, 0.1)
+        models.append(m.to(torch.bfloat16).eval())
+    x = torch.randn(batch, n * channels, hw, hw, generator=_gen()).to(torch.bfloat16)
+    return Workload(f"TracedWideModel ResBlock(64) N={n} B={batch} 32x32 bf16", n, batch, models, {"packed": x})
+
+
+def resblock_params(models: List[nn.Module], dtype: torch.dtype) -> Dict[str, object]:
+    """The reference wide layout of a list of ResBlocks (grouped conv filters, flat BN params)."""
+    p: Dict[str, object] = {}
+    for name in ("conv1", "conv2"):
+        p[f"{name}.weight"] = torch.cat([getattr(m, name).weight.detach().cpu() for m in models]).to(dtype)
+        p[f"{name}.bias"] = torch.cat([getattr(m, name).bias.detach().cpu() for m in models]).to(dtype)
+    for name in ("bn1", "bn2"):
+        for k in ("weight", "bias", "running_mean", "running_var"):
+            p[f"{name}.{k}"] = torch.cat([getattr(getattr(m, name), k).detach().cpu() for m in models]).to(dtype)
+        p[f"{name}.eps"] = getattr(models[0], name).eps
+    return p

@@ -1,0 +1,109 @@
+"""GPU parity of WideAttention (grouped projections + fused attention kernel) against the oracle."""
+
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import wide_ref
+from tests._util import TOL_BF16, TOL_F32, gen, rel_err, tol
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def _mha(n, d, h, seed, dtype, random_bias=True):
+    mods = []
+    for i in range(n):
+        torch.manual_seed(seed + i)
+        m = nn.MultiheadAttention(d, h, batch_first=True)
+        if random_bias:
+            with torch.no_grad():
+                m.in_proj_bias.normal_(0, 0.1)
+                m.out_proj.bias.normal_(0, 0.1)
+        mods.append(m.to(dtype).eval())
+    return mods
+
+
+def _oracle(wide, q, k, v, causal, double=True):
+    c = (lambda t: None if t is None else t.detach().cpu().double()) if double else \
+        (lambda t: None if t is None else t.detach().cpu())
+    f = (lambda t: t.double()) if double else (lambda t: t)
+    return wide_ref.attention(f(q), f(k), f(v), c(wide.q_weight), c(wide.kv_weight), c(wide.out_weight),
+                              c(wide.q_bias), c(wide.kv_bias), c(wide.out_bias), wide.n_heads, is_causal=causal)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,b,t,d,h", [(3, 2, 64, 64, 2), (2, 2, 50, 128, 4), (2, 1, 200, 256, 2),
+                                       (4, 3, 17, 32, 1), (2, 2, 130, 256, 8)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_self_attention(hip, dtype, n, b, t, d, h, causal):
+    import wide_compiler as wc
+    g = gen(400)
+    wide = wc.WideAttention.from_modules(_mha(n, d, h, 400, torch.float32)).to(DEV, dtype).eval()
+    x = torch.randn(n, b, t, d, generator=g).to(dtype)
+    with torch.no_grad():
+        y = wide(x.to(DEV), is_causal=causal).cpu()
+    exact = _oracle(wide, x, x, x, causal)
+    assert rel_err(y, exact) <= tol(dtype)
+    if dtype == torch.bfloat16:
+        assert rel_err(y, _oracle(wide, x, x, x, causal, double=False)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_cross_attention_mha_mode(hip, dtype):
+    import wide_compiler as wc
+    g = gen(401)
+    n, b, tq, tkv, d, h = 3, 2, 40, 77, 64, 4
+    wide = wc.WideAttention.from_modules(_mha(n, d, h, 401, torch.float32)).to(DEV, dtype).eval()
+    q = torch.randn(n, b, tq, d, generator=g).to(dtype)
+    k = torch.randn(n, b, tkv, d, generator=g).to(dtype)
+    v = torch.randn(n, b, tkv, d, generator=g).to(dtype)
+    with torch.no_grad():
+        out, w = wide(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert w is None
+    assert rel_err(out.cpu(), _oracle(wide, q, k, v, False)) <= tol(dtype)
+
+
+def test_attention_matches_nn_mha_per_model(hip):
+    """Against torch.nn.MultiheadAttention itself (batch_first), the reference's bench model."""
+    import wide_compiler as wc
+    g = gen(402)
+    n, b, t, d, h = 3, 2, 33, 64, 4
+    mods = _mha(n, d, h, 402, torch.float32)
+    wide = wc.WideAttention.from_modules(mods).to(DEV).eval()
+    x = torch.randn(n, b, t, d, generator=g)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+        for k in range(n):
+            e, _ = mods[k](x[k], x[k], x[k], need_weights=False)
+            assert rel_err(y[k], e) <= TOL_F32
+
+
+def test_attention_mask_and_dropout_raise(hip):
+    import wide_compiler as wc
+    wide = wc.WideAttention(2, 32, 2, dropout=0.1).to(DEV)
+    x = torch.zeros(2, 1, 4, 32, device=DEV)
+    with torch.no_grad():
+        with pytest.raises(RuntimeError, match="dropout"):
+            wide.train()(x)
+        with pytest.raises(NotImplementedError, match="mask"):
+            wide.eval()(x, attn_mask=torch.zeros(4, 4, device=DEV))
+
+
+def test_attention_config_n16(hip):
+    """The attention configuration at full size: N=16 MHA(256, 8 heads), B=8, S=512, bf16;
+    checked model-by-model on three models (no cross-model terms in the wide path)."""
+    import wide_compiler as wc
+    g = gen(403)
+    n, b, t, d, h = 16, 8, 512, 256, 8
+    wide = wc.WideAttention.from_modules(_mha(n, d, h, 403, torch.float32, random_bias=False)).to(DEV, torch.bfloat16)
+    x = torch.randn(n, b, t, d, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        y = wide.eval()(x.to(DEV)).cpu()
+    for k in (0, 7, 15):
+        c = lambda w: None if w is None else w.detach().cpu()[k:k + 1].double()  # noqa: E731
+        exact = wide_ref.attention(x[k:k + 1].double(), x[k:k + 1].double(), x[k:k + 1].double(),
+                                   c(wide.q_weight), c(wide.kv_weight), c(wide.out_weight), c(wide.q_bias),
+                                   c(wide.kv_bias), c(wide.out_bias), h)
+        assert rel_err(y[k:k + 1], exact) <= TOL_BF16
