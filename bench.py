@@ -204,7 +204,133 @@ def cfg_resblock(dev, steps, warmup) -> Dict:
             "extra": {"channels": c, "hw": hw}}
 
 
-CONFIGS = {"gru": cfg_gru, "mlp": cfg_mlp, "resblock": cfg_resblock}
+def cfg_attention(dev, steps, warmup) -> Dict:
+    import torch
+    import wide_compiler as wc
+    from wide_compiler import _hip, workloads
+    from oracle import wide_ref
+
+    work = workloads.attention_n16()
+    n, b = work.n, work.batch
+    x_cpu = work.inputs["x"]
+    _, _, s, d = x_cpu.shape
+    hh = work.models[0].num_heads
+    dh = d // hh
+    wide = wc.WideAttention.from_modules([m.to(dev) for m in work.models]).eval()
+    x = x_cpu.to(dev)
+    prm = lambda w, k: getattr(w, k).detach().cpu()  # noqa: E731
+
+    def parity():
+        with torch.inference_mode():
+            y = wide(x).cpu()
+        errs = []
+        for k in (0, n - 1):
+            c = lambda t: t[k:k + 1].double()  # noqa: E731
+            xs = c(x_cpu)
+            ref = wide_ref.attention(xs, xs, xs, *(c(prm(wide, a)) for a in
+                                     ("q_weight", "kv_weight", "out_weight", "q_bias", "kv_bias", "out_bias")), hh)
+            errs.append(_rel(y[k:k + 1], ref))
+        return max(errs)
+
+    def roofline():
+        kv = torch.empty((n, b, s, 2 * d), device=dev, dtype=x.dtype)
+        q = torch.empty((n, b, s, d), device=dev, dtype=x.dtype)
+        o = torch.empty_like(q)
+        x.view(-1)  # contiguous input
+        attn = lambda: _hip.attention(q=q, k=kv, v=kv[..., d:], o=o, nb=n * b, heads=hh, sq=s, skv=s,  # noqa
+                                      head_dim=dh, q_strides=(s * d, d), k_strides=(s * 2 * d, 2 * d),
+                                      v_strides=(s * 2 * d, 2 * d), o_strides=(s * d, d), scale=dh ** -0.5,
+                                      causal=False)
+        with torch.inference_mode():
+            q.copy_(wide._project(x, wide.q_weight, d * d, wide.q_bias, d, d))
+            kv.copy_(wide._project(x, wide.kv_weight, 2 * d * d, wide.kv_bias, 2 * d, 2 * d))
+        t_attn = _event_time(attn, steps, warmup)
+        t_kv = _event_time(lambda: wide._project(x, wide.kv_weight, 2 * d * d, wide.kv_bias, 2 * d, 2 * d),
+                           steps, warmup)
+        t_q = _event_time(lambda: wide._project(x, wide.q_weight, d * d, wide.q_bias, d, d), steps, warmup)
+        flops = 4.0 * n * b * hh * s * s * dh
+        return {"bound": "mfma", "kernel": "attn_kernel (fused softmax(QK^T)V, bf16, head_dim 32)",
+                "flops_per_launch": flops, "sec": t_attn, "peak": PEAK["bf16_mfma"],
+                "other_kernels_us": {"kv_projection_gemm": t_kv * 1e6, "q_projection_gemm": t_q * 1e6,
+                                     "out_projection_gemm": t_q * 1e6}}
+
+    n_cpu = 1
+    xs_cpu = x_cpu[:n_cpu].contiguous()
+    pc = [prm(wide, a)[:n_cpu].contiguous() for a in
+          ("q_weight", "kv_weight", "out_weight", "q_bias", "kv_bias", "out_bias")]
+
+    def cpu_run():
+        wide_ref.attention(xs_cpu, xs_cpu, xs_cpu, *pc, hh)
+
+    return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": lambda: wide(x), "parity": parity,
+            "roofline": roofline, "cpu": cpu_run, "cpu_samples": n_cpu * b,
+            "cpu_sample": f"{n_cpu} of the {n} models (the wide path has no cross-model terms), bf16",
+            "extra": {"seq_len": s, "embed": d, "heads": hh}}
+
+
+def cfg_seq(dev, steps, warmup) -> Dict:
+    import torch
+    from wide_compiler import _hip, workloads
+    from oracle import wide_ref
+
+    work = workloads.seq_n64()
+    n, b = work.n, work.batch
+    ids_cpu = work.inputs["ids"]
+    _, _, t = ids_cpu.shape
+    wide = workloads.WideSeqModel([m.to(dev) for m in work.models]).eval()
+    ids = ids_cpu.to(dev)
+    hdim, v = wide.lstm.hidden_size, wide.fc.out_features
+    logits = torch.empty((n, b, t, v), device=dev, dtype=torch.bfloat16)
+
+    def parity():
+        with torch.inference_mode():
+            y = wide(ids)
+        errs = []
+        for k in (0, n - 1):
+            p = {kk: (vv.double() if torch.is_tensor(vv) else vv)
+                 for kk, vv in workloads.seq_params([work.models[k]]).items()}
+            errs.append(_rel(y[k:k + 1], wide_ref.seq_model(ids_cpu[k:k + 1], p)))
+        return max(errs)
+
+    def roofline():
+        with torch.inference_mode():
+            x = wide.ln(wide.emb(ids, per_model=True))
+            hs, _ = wide.lstm(x)
+            lstm = wide.lstm
+            a, ws = _hip.rnn_args(cell=_hip.CELL_LSTM, x=x, w_ih=lstm.weight_ih, w_hh=lstm.weight_hh,
+                                  b_ih=lstm.bias_ih, b_hh=lstm.bias_hh, h0=None, c0=None, out=hs,
+                                  h_n=None, c_n=None)
+            t_fc = _event_time(lambda: wide.fc.forward_into(hs, logits), steps // 10 + 1, 2)
+            t_rec = _event_time(lambda: _hip.rnn_phase(a, "recurrence", x), 3, 1)
+            t_proj = _event_time(lambda: _hip.rnn_phase(a, "input_projection", x), 5, 1)
+            t_emb = _event_time(lambda: wide.emb(ids, per_model=True), 10, 2)
+            t_ln = _event_time(lambda: wide.ln(x), 10, 2)
+        flops = 2.0 * n * b * t * hdim * v
+        return {"bound": "mfma", "kernel": "gemm_kernel (vocab projection 512 -> 8192 + bias, bf16)",
+                "flops_per_launch": flops, "sec": t_fc, "peak": PEAK["bf16_mfma"],
+                "other_kernels_us": {"lstm_recurrence_128_steps": t_rec * 1e6,
+                                     "lstm_input_projection_gemm": t_proj * 1e6,
+                                     "embedding_gather": t_emb * 1e6, "layernorm": t_ln * 1e6}}
+
+    n_cpu = 1
+    p_cpu = {kk: (vv.float() if torch.is_tensor(vv) and vv.is_floating_point() else vv)
+             for kk, vv in workloads.seq_params(work.models[:n_cpu]).items()}
+    p_cpu = {kk: (vv.to(torch.bfloat16) if torch.is_tensor(vv) and vv.is_floating_point() else vv)
+             for kk, vv in p_cpu.items()}
+    ids_sub = ids_cpu[:n_cpu, :4].contiguous()
+
+    def cpu_run():
+        wide_ref.seq_model(ids_sub, p_cpu)
+
+    return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": lambda: wide(ids),
+            "parity": parity, "roofline": roofline, "cpu": cpu_run, "cpu_samples": n_cpu * 4,
+            "cpu_sample": f"{n_cpu} of the {n} models, 4 of the {b} sequences (no cross-model or cross-sequence "
+                          f"terms), bf16",
+            "extra": {"seq_len": t, "vocab": v, "embed": 256, "hidden": hdim}}
+
+
+CONFIGS = {"gru": cfg_gru, "mlp": cfg_mlp, "resblock": cfg_resblock, "attention": cfg_attention,
+           "seq": cfg_seq}
 
 
 def main() -> int:

@@ -171,7 +171,8 @@ typedef struct wc_rnn_args {
   int64_t workspace_bytes;
 } wc_rnn_args;
 
-/* Bytes of workspace wc_rnn_forward needs for these sizes (n*batch*steps*G*4). */
+/* Bytes of workspace wc_rnn_forward needs for these sizes:
+ * fp32 input projection n*batch*steps*G*4 + fp32 cell state n*batch*hidden*4. */
 int64_t wc_rnn_workspace_bytes(const wc_rnn_args* args);
 
 /* Runs wc_rnn_input_projection, then wc_rnn_recurrence. */
@@ -182,8 +183,10 @@ int32_t wc_rnn_forward(const wc_rnn_args* args, void* stream);
  * before the reference's time loop (wide_gru.py:168-170, wide_lstm.py:190-193). */
 int32_t wc_rnn_input_projection(const wc_rnn_args* args, void* stream);
 
-/* Phase 2: the time loop (wide_gru.py:181-211, wide_lstm.py:205-232) as one
- * persistent kernel reading gates_x from the workspace; x and w_ih are not read. */
+/* Phase 2: the time loop (wide_gru.py:181-211, wide_lstm.py:205-232) reading
+ * gates_x from the workspace; x and w_ih are not read.  When one model's W_hh fits
+ * a workgroup's registers this is one persistent launch; otherwise one launch per
+ * step (an MFMA gate GEMM fused with the cell update; hidden % 32 == 0). */
 int32_t wc_rnn_recurrence(const wc_rnn_args* args, void* stream);
 
 /*

@@ -311,6 +311,144 @@ int32_t launch_rec(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStr
 inline int round4(int v) { return (v + 3) & ~3; }
 inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
+// ---------------------------------------------------------------------------
+// Streamed recurrence for hidden sizes whose W_hh does not fit one workgroup:
+// one launch per time step.  Workgroup = (model, block of UB units); it forms
+// the gate pre-activations of its units for all batch rows as an MFMA GEMM
+//   G[b][r] = sum_k h_{t-1}[b][k] W_hh[row(r)][k],   row(r) = (r / UB)*H + u0 + r % UB
+// with A = h_{t-1} (batch rows, read from the previous step's output) and
+// B = the W_hh rows (K-contiguous, streamed from L2 / MALL), stages G in LDS,
+// then applies the cell update for its (batch row, unit) pairs.  The cell
+// state is carried in an fp32 workspace.
+// ---------------------------------------------------------------------------
+struct StepParams {
+  int n, batch, steps, hid, t, ublocks;
+  const void* hprev;          // h_{t-1}: [n][batch] rows of `hid` elements (null: zeros)
+  int64_t hp_sn, hp_sb;
+  const float* gx;            // [n, batch, steps, G] fp32 (incl. b_ih)
+  const void* w_hh;           // [n, G, hid]
+  const void* b_hh;           // [n, G] or null
+  float* cst;                 // [n, batch, hid] fp32 cell state (LSTM)
+  const void* c0;             // initial cell state or null (read at t == 0)
+  void* out;                  // [n, batch, steps, hid]
+  void* hn;
+  void* cn;
+};
+
+constexpr int kStepThreads = 256;
+
+template <typename T, int CELL>
+struct StepCfg {
+  static constexpr int GATES = CELL == WC_CELL_GRU ? 3 : 4;
+  static constexpr int NTW = CELL == WC_CELL_GRU ? 3 : 2;   // 16-row tiles per wave
+  static constexpr int R = 4 * 16 * NTW;                     // gate rows per workgroup
+  static constexpr int UB = R / GATES;                       // units per workgroup (64 / 32)
+};
+
+template <typename T, int CELL>
+__global__ __launch_bounds__(kStepThreads) void rnn_step_kernel(StepParams p) {
+  using C = StepCfg<T, CELL>;
+  constexpr int GATES = C::GATES, NTW = C::NTW, R = C::R, UB = C::UB;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int RP = R + 4;                                   // LDS pitch of the gate tile
+  __shared__ float gs[16 * RP];
+
+  const int H = p.hid, G = GATES * H;
+  const int mdl = blockIdx.x / p.ublocks;
+  const int ub = blockIdx.x - mdl * p.ublocks;
+  const int u0 = ub * UB;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int fr = lane & 15, g = lane >> 4;
+  const T* wb = static_cast<const T*>(p.w_hh) + static_cast<int64_t>(mdl) * G * H;
+
+  for (int b0 = 0; b0 < p.batch; b0 += 16) {
+    // ---- G = h_{t-1} W^T over 16 batch rows x R gate rows ----
+    f32x4 acc[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int brow = b0 + fr;
+    const T* arow = (p.hprev && brow < p.batch)
+                        ? static_cast<const T*>(p.hprev) + mdl * p.hp_sn + brow * p.hp_sb + g * 8
+                        : nullptr;
+    const T* wrow[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int r = (wave * NTW + j) * 16 + fr;
+      const int q = r / UB, u = u0 + (r - q * UB);
+      wrow[j] = (u < H) ? wb + static_cast<int64_t>(q * H + u) * H + g * 8 : nullptr;
+    }
+    if (p.hprev) {
+      for (int k0 = 0; k0 < H; k0 += 32) {
+        if constexpr (BF) {
+          const bf16x8 a = arow ? *reinterpret_cast<const bf16x8*>(arow + k0) : bf16x8{};
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            const bf16x8 bv = wrow[j] ? *reinterpret_cast<const bf16x8*>(wrow[j] + k0) : bf16x8{};
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
+          }
+        } else {
+          const f32x4 a0 = arow ? *reinterpret_cast<const f32x4*>(arow + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+          const f32x4 a1 = arow ? *reinterpret_cast<const f32x4*>(arow + k0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            const f32x4 b0v = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const f32x4 b1v = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], b0v[e], acc[j], 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], b1v[e], acc[j], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // lane holds G[b = (lane>>4)*4 + e][r = tile*16 + fr]
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int r = (wave * NTW + j) * 16 + fr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gs[(g * 4 + e) * RP + r] = acc[j][e];
+    }
+    __syncthreads();
+
+    // ---- cell update for (batch row, unit) pairs ----
+    for (int e = tid; e < 16 * UB; e += kStepThreads) {
+      const int bl = e / UB, ul = e - bl * UB;
+      const int b = b0 + bl, u = u0 + ul;
+      if (b >= p.batch || u >= H) continue;
+      const int64_t nb = static_cast<int64_t>(mdl) * p.batch + b;
+      const float* gxr = p.gx + (nb * p.steps + p.t) * G + u;
+      const float* ghr = gs + bl * RP + ul;
+      float gh[GATES];
+#pragma unroll
+      for (int q = 0; q < GATES; ++q)
+        gh[q] = ghr[q * UB] + (p.b_hh ? ldf<T>(p.b_hh, static_cast<int64_t>(mdl) * G + q * H + u) : 0.f);
+      float hnew, cnew = 0.f;
+      if (CELL == WC_CELL_GRU) {
+        const float hprev = p.hprev ? ldf<T>(p.hprev, mdl * p.hp_sn + b * p.hp_sb + u) : 0.f;
+        const float rg = sigmoid_f(gxr[0] + gh[0]);
+        const float zg = sigmoid_f(gxr[H] + gh[1]);
+        const float nn = tanh_f(gxr[2 * H] + rg * gh[2]);
+        hnew = (1.0f - zg) * nn + zg * hprev;
+      } else {
+        const float cprev = p.t == 0 ? (p.c0 ? ldf<T>(p.c0, nb * H + u) : 0.f) : p.cst[nb * H + u];
+        const float ig = sigmoid_f(gxr[0] + gh[0]);
+        const float fg = sigmoid_f(gxr[H] + gh[1]);
+        const float gg = tanh_f(gxr[2 * H] + gh[2]);
+        const float og = sigmoid_f(gxr[3 * H] + gh[3]);
+        cnew = fg * cprev + ig * gg;
+        hnew = og * tanh_f(cnew);
+        p.cst[nb * H + u] = cnew;
+      }
+      static_cast<T*>(p.out)[(nb * p.steps + p.t) * H + u] = from_f32<T>(hnew);
+      if (p.t == p.steps - 1) {
+        if (p.hn) static_cast<T*>(p.hn)[nb * H + u] = from_f32<T>(hnew);
+        if (CELL == WC_CELL_LSTM && p.cn) static_cast<T*>(p.cn)[nb * H + u] = from_f32<T>(cnew);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 }  // namespace wc
 
@@ -338,7 +476,46 @@ static bool rnn_plan(int gates, int hid, RnnParams& p) {
 
 static int64_t rnn_ws_bytes(const wc_rnn_args* a) {
   const int64_t gates = a->cell == WC_CELL_GRU ? 3 : 4;
-  return a->n * a->batch * a->steps * gates * a->hidden * static_cast<int64_t>(sizeof(float));
+  // fp32 input projection [n, batch, steps, G] + fp32 cell state [n, batch, hidden]
+  return (a->n * a->batch * a->steps * gates * a->hidden + a->n * a->batch * a->hidden) *
+         static_cast<int64_t>(sizeof(float));
+}
+
+template <typename T, int CELL>
+static int32_t streamed_recurrence(const wc_rnn_args* a, const RnnParams& rp, hipStream_t st) {
+  using C = StepCfg<T, CELL>;
+  StepParams p;
+  p.n = rp.n;
+  p.batch = rp.batch;
+  p.steps = rp.steps;
+  p.hid = rp.hid;
+  p.ublocks = (rp.hid + C::UB - 1) / C::UB;
+  p.gx = static_cast<const float*>(a->workspace);
+  p.w_hh = a->w_hh;
+  p.b_hh = a->b_hh;
+  p.cst = static_cast<float*>(a->workspace) +
+          static_cast<int64_t>(rp.n) * rp.batch * rp.steps * C::GATES * rp.hid;
+  p.c0 = a->c0;
+  p.out = a->out;
+  p.hn = a->h_n;
+  p.cn = a->c_n;
+  const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(rp.n) * p.ublocks));
+  for (int t = 0; t < rp.steps; ++t) {
+    p.t = t;
+    if (t == 0) {
+      p.hprev = a->h0;
+      p.hp_sn = static_cast<int64_t>(rp.batch) * rp.hid;
+      p.hp_sb = rp.hid;
+    } else {
+      p.hprev = static_cast<const T*>(a->out) + static_cast<int64_t>(t - 1) * rp.hid;
+      p.hp_sn = static_cast<int64_t>(rp.batch) * rp.steps * rp.hid;
+      p.hp_sb = static_cast<int64_t>(rp.steps) * rp.hid;
+    }
+    rnn_step_kernel<T, CELL><<<grid, kStepThreads, 0, st>>>(p);
+    int32_t rc = check_launch("wc_rnn_recurrence(step)");
+    if (rc) return rc;
+  }
+  return WC_OK;
 }
 
 extern "C" int64_t wc_rnn_workspace_bytes(const wc_rnn_args* a) {
@@ -414,11 +591,20 @@ extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
   if (rc) return rc;
   if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
   WC_REQUIRE(a->w_hh && a->out, WC_ERR_NULL, "wc_rnn_recurrence: null pointer");
-  if (!rnn_plan(gates, p.hid, p))
-    return set_error(WC_ERR_LIMIT,
-                     "wc_rnn_recurrence: hidden=%d exceeds the register-resident recurrent kernel "
-                     "(W_hh of one model must fit the register file of one workgroup)",
-                     p.hid);
+  if (!rnn_plan(gates, p.hid, p)) {
+    // W_hh of one model does not fit a workgroup's registers: one launch per step
+    const int es = dtype_size(a->dtype);
+    WC_REQUIRE(aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && p.hid % 32 == 0 &&
+                   (!a->h0 || aligned(a->h0, 16)) && aligned(a->out, 16),
+               WC_ERR_ALIGN, "wc_rnn_recurrence: hidden=%d needs hidden %% 32 == 0 and 16-byte aligned "
+               "W_hh / h0 / out for the streamed recurrence", p.hid);
+    hipStream_t st = as_stream(stream);
+    if (a->dtype == WC_F32)
+      return a->cell == WC_CELL_GRU ? streamed_recurrence<float, WC_CELL_GRU>(a, p, st)
+                                    : streamed_recurrence<float, WC_CELL_LSTM>(a, p, st);
+    return a->cell == WC_CELL_GRU ? streamed_recurrence<bf16, WC_CELL_GRU>(a, p, st)
+                                  : streamed_recurrence<bf16, WC_CELL_LSTM>(a, p, st);
+  }
   const int nwg = p.n * p.batch;
   p.remap = (nwg % 8 == 0) ? 1 : 0;
   p.gx = static_cast<const float*>(a->workspace);
@@ -457,12 +643,6 @@ extern "C" int32_t wc_rnn_forward(const wc_rnn_args* a, void* stream) {
   int32_t rc = rnn_check(a, "wc_rnn_forward", p, gates);
   if (rc) return rc;
   if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
-  // refuse sizes the recurrence cannot take before launching the projection
-  if (!rnn_plan(gates, p.hid, p))
-    return set_error(WC_ERR_LIMIT,
-                     "wc_rnn_forward: hidden=%d exceeds the register-resident recurrent kernel "
-                     "(W_hh of one model must fit the register file of one workgroup)",
-                     p.hid);
   rc = wc_rnn_input_projection(a, stream);
   if (rc) return rc;
   return wc_rnn_recurrence(a, stream);

@@ -10,7 +10,7 @@ feed both the HIP path (after ``.to('cuda')``) and the CPU oracle.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, List
+from typing import Dict, List, Optional
 
 import torch
 import torch.nn as nn
@@ -113,3 +113,83 @@ def resblock_params(models: List[nn.Module], dtype: torch.dtype) -> Dict[str, ob
             p[f"{name}.{k}"] = torch.cat([getattr(getattr(m, name), k).detach().cpu() for m in models]).to(dtype)
         p[f"{name}.eps"] = getattr(models[0], name).eps
     return p
+
+
+def attention_n16(n: int = 16, batch: int = 8, seq: int = 512, embed: int = 256, heads: int = 8) -> Workload:
+    """N=16 nn.MultiheadAttention(256, 8 heads, batch_first; xavier-uniform in-projection, the nn
+    default), bf16; self-attention input x [16, 8, 512, 256] ~ N(0, 1), no mask."""
+    models = []
+    for i in range(n):
+        torch.manual_seed(SEED + i)
+        models.append(nn.MultiheadAttention(embed, heads, batch_first=True).to(torch.bfloat16).eval())
+    x = torch.randn(n, batch, seq, embed, generator=_gen()).to(torch.bfloat16)
+    return Workload(f"WideAttention MHA(256, 8 heads) N={n} B={batch} S={seq} bf16", n, batch, models, {"x": x})
+
+
+class SeqModel(nn.Module):
+    """Embedding(8192, 256) - LayerNorm(256) - LSTM(256 -> 512, batch_first) - Linear(512 -> 8192):
+    one small token model; ids [B, T] -> logits [B, T, 8192]."""
+
+    def __init__(self, vocab: int = 8192, dim: int = 256, hidden: int = 512):
+        super().__init__()
+        self.emb = nn.Embedding(vocab, dim)          # init ~ N(0, 1) (the nn default)
+        self.ln = nn.LayerNorm(dim)
+        self.lstm = nn.LSTM(dim, hidden, batch_first=True)
+        self.fc = nn.Linear(hidden, vocab)
+
+    def forward(self, ids):
+        h, _ = self.lstm(self.ln(self.emb(ids)))
+        return self.fc(h)
+
+
+class WideSeqModel(nn.Module):
+    """N SeqModels fused primitive by primitive: per-model embedding gather (each model reads
+    its own ids), N-first LayerNorm, WideLSTM, WideLinear over the vocabulary.  The wide
+    primitives are the reference's (wide_embedding.py, wide_layernorm.py, wide_lstm.py,
+    wide_linear.py); the composition is not traced because the LSTM returns a tuple."""
+
+    def __init__(self, models: List[SeqModel]):
+        super().__init__()
+        from .core.primitives import WideEmbedding, WideLayerNorm, WideLinear, WideLSTM
+        self.n = len(models)
+        self.emb = WideEmbedding.from_modules([m.emb for m in models])
+        self.ln = WideLayerNorm.from_modules([m.ln for m in models])
+        self.lstm = WideLSTM.from_modules([m.lstm for m in models])
+        self.fc = WideLinear.from_modules([m.fc for m in models])
+
+    def forward(self, ids: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """ids [N, B, T] (model i uses row i) -> logits [N, B, T, V]."""
+        x = self.ln(self.emb(ids, per_model=True))
+        h, _ = self.lstm(x)
+        return self.fc.forward_into(h, out)
+
+
+def seq_n64(n: int = 64, batch: int = 16, steps: int = 128, vocab: int = 8192, dim: int = 256,
+            hidden: int = 512) -> Workload:
+    """N=64 SeqModels, weights bf16 (fp32 accumulate, fp32 cell state in the kernels);
+    ids [64, 16, 128] uniform int64 in [0, 8192)."""
+    models = []
+    for i in range(n):
+        torch.manual_seed(SEED + i)
+        models.append(SeqModel(vocab, dim, hidden).to(torch.bfloat16).eval())
+    ids = torch.randint(0, vocab, (n, batch, steps), generator=_gen(), dtype=torch.int64)
+    return Workload(f"Emb-LN-LSTM-Linear N={n} B={batch} T={steps} V={vocab} {dim}->{hidden} bf16",
+                    n, batch, models, {"ids": ids})
+
+
+def seq_params(models: List[SeqModel]) -> Dict[str, object]:
+    """The wide parameter layout of a list of SeqModels, as the oracle's seq_model takes it
+    (LSTM weights in the compact per-model form [N, 4H, I] / [N, 4H, H])."""
+    st = lambda ts: torch.stack([t.detach().cpu() for t in ts])  # noqa: E731
+    return {
+        "emb.weight": st([m.emb.weight for m in models]),
+        "ln.weight": torch.cat([m.ln.weight.detach().cpu() for m in models]),
+        "ln.bias": torch.cat([m.ln.bias.detach().cpu() for m in models]),
+        "ln.eps": models[0].ln.eps,
+        "lstm.weight_ih": st([m.lstm.weight_ih_l0 for m in models]),
+        "lstm.weight_hh": st([m.lstm.weight_hh_l0 for m in models]),
+        "lstm.bias_ih": st([m.lstm.bias_ih_l0 for m in models]),
+        "lstm.bias_hh": st([m.lstm.bias_hh_l0 for m in models]),
+        "fc.weight": st([m.fc.weight for m in models]),
+        "fc.bias": st([m.fc.bias for m in models]),
+    }

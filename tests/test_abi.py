@@ -54,7 +54,8 @@ def test_rnn_limit_and_workspace_checks(hip):
     a = hip._RnnArgs()
     a.cell, a.dtype = hip.CELL_LSTM, hip.F32
     a.n, a.batch, a.steps, a.input_size, a.hidden = 2, 3, 4, 8, 16
-    assert hip.lib().wc_rnn_workspace_bytes(ctypes.byref(a)) == 2 * 3 * 4 * 64 * 4
+    # fp32 gates_x [n, batch, steps, 4H] + fp32 cell state [n, batch, H]
+    assert hip.lib().wc_rnn_workspace_bytes(ctypes.byref(a)) == (2 * 3 * 4 * 64 + 2 * 3 * 16) * 4
     a.x = a.w_ih = a.w_hh = a.out = 16  # never dereferenced: rejected before any launch
     a.workspace, a.workspace_bytes = 16, 8
     assert hip.lib().wc_rnn_forward(ctypes.byref(a), None) == -6

@@ -323,6 +323,25 @@ def test_resblock_wide_vs_per_model():
 
 
 # ----------------------------------------------------------------------------- planted mistakes
+def test_seq_model_wide_vs_per_model():
+    """The composed sequence model (per-model ids) against each torch.nn SeqModel in float64."""
+    from wide_compiler.workloads import SeqModel, seq_params
+    n, b, t, v, d, h = 3, 2, 5, 40, 16, 24
+    mods = []
+    for i in range(n):
+        torch.manual_seed(400 + i)
+        m = SeqModel(v, d, h).double()
+        with torch.no_grad():
+            m.ln.weight.normal_(1.0, 0.2)
+            m.ln.bias.normal_(0.0, 0.2)
+        mods.append(m)
+    ids = torch.randint(0, v, (n, b, t), generator=gen(401))
+    got = wide_ref.seq_model(ids, seq_params(mods))
+    with torch.no_grad():
+        for i in range(n):
+            assert rel_err(got[i], mods[i](ids[i])) <= 1e-12
+
+
 def test_planted_gru_gate_swap_is_caught():
     """Swapping r and z in a copy of the oracle's GRU must fail the nn.GRU pin."""
     def gru_swapped(x, wih, whh, bih, bhh):
