@@ -43,15 +43,22 @@ def _rel(a, b) -> float:
 
 
 def _event_time(fn: Callable[[], None], k: int, w: int) -> float:
-    """Average seconds per call of fn (a kernel launch on torch's current stream)."""
+    """Average seconds per call of fn (kernel launches on torch's current stream): k calls are
+    captured back to back into one HIP graph, so host dispatch does not enter the figure, and
+    the replay is bracketed by HIP events recorded on the stream the graph runs on."""
     import torch
-    for _ in range(w):
+    for _ in range(max(w, 1)):
         fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(k):
+            fn()
+    graph.replay()                      # warm replay
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for _ in range(k):
-        fn()
+    graph.replay()
     e1.record(st)
     e1.synchronize()
     return e0.elapsed_time(e1) / k * 1e-3
@@ -342,6 +349,9 @@ def main() -> int:
     ap.add_argument("--mode", choices=("graph", "eager"), default="graph")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (the reference kernel whose "
+                         "FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -351,6 +361,15 @@ def main() -> int:
     import torch
 
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        nbytes = args.copy_calibration << 20
+        src = torch.ones(nbytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 5}))
+        return 0
     cfg = CONFIGS[args.config](dev, args.steps, args.warmup)
     n, b = cfg["n"], cfg["batch"]
     step = cfg["step"]

@@ -1,0 +1,203 @@
+"""Write the golden fixtures of tests/golden/ (float64, small shapes).
+
+Expected outputs come from per-model torch.nn modules, run one model at a time.  These are
+the modules the wide path replaces and the reference validates against.  The wide path
+and the oracle therefore never produce their own expected values.  Each fixture is one
+.npz holding:
+  * m{i}.{name}  -- model i's state_dict entries
+  * in.{name}    -- inputs
+  * out.{name}   -- expected outputs
+  * meta         -- a JSON string: module constructor arguments and the torch version
+
+Run from the repository root:  python tests/golden/make_golden.py
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "..", "..", "pytorch-parallel-compiler_amd"))
+
+from wide_compiler.workloads import MLP, ResBlock, SeqModel  # noqa: E402
+
+SEED = 7100
+
+
+def _seed(i):
+    torch.manual_seed(SEED + i)
+
+
+def _gen(i=0):
+    g = torch.Generator()
+    g.manual_seed(SEED + 1000 + i)
+    return g
+
+
+def _perturb(m):
+    """Non-default affine / running statistics so the norms are not identities."""
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, (nn.BatchNorm2d, nn.LayerNorm)):
+                mod.weight.normal_(1.0, 0.2)
+                mod.bias.normal_(0.0, 0.2)
+            if isinstance(mod, nn.BatchNorm2d):
+                mod.running_mean.normal_(0.0, 0.3)
+                mod.running_var.uniform_(0.5, 2.0)
+            if isinstance(mod, nn.MultiheadAttention):
+                mod.in_proj_bias.normal_(0.0, 0.1)
+                mod.out_proj.bias.normal_(0.0, 0.1)
+            if isinstance(mod, (nn.GRU, nn.LSTM)):
+                for name, p in mod.named_parameters():
+                    if "bias" in name:
+                        p.normal_(0.0, 0.1)
+    return m
+
+
+def _save(name, mods, inputs, outputs, meta):
+    arrs = {}
+    for i, m in enumerate(mods):
+        for k, v in m.state_dict().items():
+            arrs[f"m{i}.{k}"] = v.detach().cpu().numpy()
+    for k, v in inputs.items():
+        arrs[f"in.{k}"] = v.detach().cpu().numpy()
+    for k, v in outputs.items():
+        arrs[f"out.{k}"] = v.detach().cpu().numpy()
+    meta = dict(meta, torch=torch.__version__, n=len(mods))
+    arrs["meta"] = np.array(json.dumps(meta))
+    np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **arrs)
+
+
+def main():
+    torch.set_default_dtype(torch.float64)
+    with torch.no_grad():
+        # Linear: N=3, x [3, 4, 5] -> [3, 4, 7]
+        mods = []
+        for i in range(3):
+            _seed(i)
+            mods.append(nn.Linear(5, 7))
+        x = torch.randn(3, 4, 5, generator=_gen(0))
+        _save("linear", mods, {"x": x}, {"y": torch.stack([m(x[i]) for i, m in enumerate(mods)])},
+              {"in_features": 5, "out_features": 7})
+
+        # Conv2d: N=2, stride 2, pad 1, dilation 1, x [2, 2, 3, 7, 6]
+        mods = []
+        for i in range(2):
+            _seed(10 + i)
+            mods.append(nn.Conv2d(3, 4, 3, stride=2, padding=1))
+        x = torch.randn(2, 2, 3, 7, 6, generator=_gen(1))
+        _save("conv2d", mods, {"x": x}, {"y": torch.stack([m(x[i]) for i, m in enumerate(mods)])},
+              {"in": 3, "out": 4, "k": 3, "stride": 2, "padding": 1})
+
+        # Conv1d: N=2, dilation 2, pad 2, x [2, 3, 4, 11]
+        mods = []
+        for i in range(2):
+            _seed(20 + i)
+            mods.append(nn.Conv1d(4, 5, 3, padding=2, dilation=2))
+        x = torch.randn(2, 3, 4, 11, generator=_gen(2))
+        _save("conv1d", mods, {"x": x}, {"y": torch.stack([m(x[i]) for i, m in enumerate(mods)])},
+              {"in": 4, "out": 5, "k": 3, "padding": 2, "dilation": 2})
+
+        # BatchNorm2d eval: N=2, x [2, 3, 4, 5, 5]
+        mods = []
+        for i in range(2):
+            _seed(30 + i)
+            mods.append(_perturb(nn.BatchNorm2d(4)).eval())
+        x = torch.randn(2, 3, 4, 5, 5, generator=_gen(3))
+        _save("batchnorm2d", mods, {"x": x}, {"y": torch.stack([m(x[i]) for i, m in enumerate(mods)])},
+              {"c": 4})
+
+        # LayerNorm: N=3, x [3, 2, 5, 8]
+        mods = []
+        for i in range(3):
+            _seed(40 + i)
+            mods.append(_perturb(nn.LayerNorm(8)))
+        x = torch.randn(3, 2, 5, 8, generator=_gen(4))
+        _save("layernorm", mods, {"x": x}, {"y": torch.stack([m(x[i]) for i, m in enumerate(mods)])},
+              {"d": 8})
+
+        # Embedding: N=3, vocab 11, dim 6; shared ids [2, 5] and per-model ids [3, 2, 5]
+        mods = []
+        for i in range(3):
+            _seed(50 + i)
+            mods.append(nn.Embedding(11, 6))
+        ids = torch.randint(0, 11, (2, 5), generator=_gen(5))
+        pm = torch.randint(0, 11, (3, 2, 5), generator=_gen(6))
+        _save("embedding", mods, {"ids": ids, "ids_per_model": pm},
+              {"shared": torch.stack([m(ids) for m in mods]),
+               "per_model": torch.stack([m(pm[i]) for i, m in enumerate(mods)])}, {"vocab": 11, "dim": 6})
+
+        # GRU: N=2, x [2, 3, 4, 5], hidden 6, with h0
+        mods = []
+        for i in range(2):
+            _seed(60 + i)
+            mods.append(_perturb(nn.GRU(5, 6, batch_first=True)))
+        x = torch.randn(2, 3, 4, 5, generator=_gen(7))
+        h0 = torch.randn(2, 3, 6, generator=_gen(8))
+        outs = [m(x[i], h0[i:i + 1]) for i, m in enumerate(mods)]
+        _save("gru", mods, {"x": x, "h0": h0},
+              {"out": torch.stack([o for o, _ in outs]), "h_n": torch.stack([h[0] for _, h in outs])},
+              {"input_size": 5, "hidden": 6})
+
+        # LSTM: N=2, x [2, 3, 4, 5], hidden 6, with (h0, c0)
+        mods = []
+        for i in range(2):
+            _seed(70 + i)
+            mods.append(_perturb(nn.LSTM(5, 6, batch_first=True)))
+        x = torch.randn(2, 3, 4, 5, generator=_gen(9))
+        h0 = torch.randn(2, 3, 6, generator=_gen(10))
+        c0 = torch.randn(2, 3, 6, generator=_gen(11))
+        outs = [m(x[i], (h0[i:i + 1], c0[i:i + 1])) for i, m in enumerate(mods)]
+        _save("lstm", mods, {"x": x, "h0": h0, "c0": c0},
+              {"out": torch.stack([o for o, _ in outs]), "h_n": torch.stack([h[0][0] for _, h in outs]),
+               "c_n": torch.stack([h[1][0] for _, h in outs])}, {"input_size": 5, "hidden": 6})
+
+        # MultiheadAttention: N=2, embed 8, 2 heads, self-attention x [2, 2, 5, 8]
+        mods = []
+        for i in range(2):
+            _seed(80 + i)
+            mods.append(_perturb(nn.MultiheadAttention(8, 2, batch_first=True)).eval())
+        x = torch.randn(2, 2, 5, 8, generator=_gen(12))
+        _save("attention", mods, {"x": x},
+              {"y": torch.stack([m(x[i], x[i], x[i], need_weights=False)[0] for i, m in enumerate(mods)])},
+              {"embed": 8, "heads": 2})
+
+        # MLP (Linear-ReLU-Linear): N=3, packed input [4, 3*64]
+        mods = []
+        for i in range(3):
+            _seed(90 + i)
+            mods.append(MLP())
+        xs = torch.randn(3, 4, 64, generator=_gen(13))
+        packed = xs.transpose(0, 1).reshape(4, 3 * 64)
+        y = torch.stack([m(xs[i]) for i, m in enumerate(mods)], dim=1).reshape(4, 3 * 64)
+        _save("mlp", mods, {"packed": packed}, {"packed": y}, {})
+
+        # ResBlock(4): N=2, packed input [2, 2*4, 5, 6]
+        mods = []
+        for i in range(2):
+            _seed(100 + i)
+            mods.append(_perturb(ResBlock(4)).eval())
+        xs = torch.randn(2, 2, 4, 5, 6, generator=_gen(14))
+        packed = xs.transpose(0, 1).reshape(2, 8, 5, 6)
+        y = torch.stack([m(xs[i]) for i, m in enumerate(mods)], dim=1).reshape(2, 8, 5, 6)
+        _save("resblock", mods, {"packed": packed}, {"packed": y}, {"channels": 4})
+
+        # Sequence model: N=2, vocab 16, dim 8, hidden 12, ids [2, 3, 4]
+        mods = []
+        for i in range(2):
+            _seed(110 + i)
+            mods.append(_perturb(SeqModel(16, 8, 12)).eval())
+        ids = torch.randint(0, 16, (2, 3, 4), generator=_gen(15))
+        _save("seq_model", mods, {"ids": ids}, {"logits": torch.stack([m(ids[i]) for i, m in enumerate(mods)])},
+              {"vocab": 16, "dim": 8, "hidden": 12})
+
+
+if __name__ == "__main__":
+    main()

@@ -80,3 +80,22 @@ def test_empty_problems_are_noops(hip):
     assert lib.wc_swap01(None, 0, 5, 0, 0, 16, None, None) == 0
     assert lib.wc_pack_rows(None, None, 0, 3, 8, None, None) == 0
     assert lib.wc_layernorm(None, 0, 0, None, None, None, 0, 0, 0, 4, 8, 1e-5, 0, 0, None) == 0
+
+
+def test_package_never_imports_the_oracle():
+    """The product path has no route to the CPU restatement: no package source names it."""
+    import pathlib
+    pkg = pathlib.Path(__file__).resolve().parents[1] / "pytorch-parallel-compiler_amd" / "wide_compiler"
+    offenders = [str(p) for p in pkg.rglob("*.py")
+                 if re.search(r"^\s*(from|import)\s+oracle\b", p.read_text(), re.M)]
+    assert not offenders, offenders
+
+
+def test_cpu_tensors_raise_without_touching_a_device():
+    """Every primitive refuses CPU tensors (no CPU fallback)."""
+    import torch
+    import wide_compiler as wc
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        wc.WideLinear(2, 4, 3)(torch.zeros(2, 5, 4))
+    with pytest.raises(RuntimeError, match="ROCm device tensors only"):
+        wc.WideLayerNorm(2, 4)(torch.zeros(2, 3, 4))
