@@ -226,6 +226,206 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile bf16 kernel.  A workgroup of WM x WN waves computes a
+// (WM*FM*16) x (WN*FN*16) tile; K advances in tiles of 64 staged through a
+// double-buffered LDS ring (each thread moves 16-byte chunks global ->
+// registers -> LDS; the next tile's loads are in flight during the current
+// tile's 2 x FM x FN MFMAs).  The epilogue goes through LDS as well: each wave
+// parks a 16-row strip of its fp32 accumulators, reads it back row-major and
+// applies bias / residual / ReLU with 8- or 16-byte stores along rows.
+// ---------------------------------------------------------------------------
+constexpr int kBigBK = 64;
+constexpr int kBigPitch = kBigBK + 8;          // bf16 elements per LDS row (144 bytes)
+
+template <int WM, int WN, int FM, int FN>
+struct BigCfg {
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int BM = WM * FM * 16, BN = WN * FN * 16;
+  static constexpr int CH = (BM + BN) * (kBigBK / 8);        // 16-byte chunks per stage
+  static constexpr int CPT = CH / NT;                       // chunks per thread
+  static constexpr int STAGE = (BM + BN) * kBigPitch;       // bf16 elements per stage
+  static constexpr int EPI_PITCH = FN * 16 + 4;             // floats per epilogue row
+  static constexpr size_t LDS_MAIN = 2 * STAGE * sizeof(bf16);
+  static constexpr size_t LDS_EPI = static_cast<size_t>(WM * WN) * 16 * EPI_PITCH * sizeof(float);
+  static constexpr size_t LDS = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
+  static_assert(CH % NT == 0, "chunks must divide evenly");
+};
+
+template <typename TC, typename TB, int WM, int WN, int FM, int FN>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmParams p) {
+  using C = BigCfg<WM, WN, FM, FN>;
+  constexpr int NT = C::NT, BM = C::BM, BN = C::BN, CPT = C::CPT;
+  extern __shared__ __attribute__((aligned(16))) bf16 big_smem[];
+
+  const int tiles_per_model = p.tiles_m * p.tiles_o;
+  const int nblk = p.n * tiles_per_model;
+  int bid = blockIdx.x;
+  if (p.remap) bid = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
+  const int mdl = bid / tiles_per_model;
+  const int rem = bid - mdl * tiles_per_model;
+  const int to = rem / p.tiles_m;
+  const int tm = rem - to * p.tiles_m;
+  const int m0 = tm * BM, o0 = to * BN;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave / WN, wn = wave - (wave / WN) * WN;
+
+  const bf16* abase = static_cast<const bf16*>(p.a) + static_cast<int64_t>(mdl) * p.a_sn;
+  const bf16* wbase = static_cast<const bf16*>(p.w) + static_cast<int64_t>(mdl) * p.w_sn;
+
+  // staging: chunk c = tid + q*NT; rows [0, BM) are A, [BM, BM+BN) are W
+  const bf16* src[CPT];
+  int dst[CPT];
+#pragma unroll
+  for (int q = 0; q < CPT; ++q) {
+    const int c = tid + q * NT;
+    const int r = c >> 3, kc = (c & 7) * 8;
+    dst[q] = r * kBigPitch + kc;
+    src[q] = nullptr;
+    if (r < BM) {
+      const int gm = m0 + r;
+      if (gm < p.m) {
+        const uint32_t outer = fdiv(static_cast<uint32_t>(gm), p.a_ri);
+        const uint32_t inner = gm - outer * p.a_ri.d;
+        src[q] = abase + static_cast<int64_t>(outer) * p.a_so + static_cast<int64_t>(inner) * p.a_si + kc;
+      }
+    } else {
+      const int go = o0 + (r - BM);
+      if (go < p.o) src[q] = wbase + static_cast<int64_t>(go) * p.k + kc;
+    }
+  }
+  uint4 stg[CPT];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      const int kk = k0 + (dst[q] % kBigPitch);
+      stg[q] = (src[q] && kk < p.k) ? *reinterpret_cast<const uint4*>(src[q] + k0) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&](int stage) {
+    bf16* base = big_smem + stage * C::STAGE;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) *reinterpret_cast<uint4*>(base + dst[q]) = stg[q];
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int ktiles = (p.k + kBigBK - 1) / kBigBK;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int stage = kt & 1;
+    if (kt + 1 < ktiles) fetch((kt + 1) * kBigBK);
+    const bf16* as = big_smem + stage * C::STAGE + (wm * FM * 16 + fr) * kBigPitch + fk;
+    const bf16* bs = big_smem + stage * C::STAGE + (BM + wn * FN * 16 + fr) * kBigPitch + fk;
+#pragma unroll
+    for (int kk = 0; kk < kBigBK; kk += 32) {
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(as + i * 16 * kBigPitch + kk);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(bs + j * 16 * kBigPitch + kk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < ktiles) stash(stage ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue through LDS: one 16-row strip of the wave's tile at a time ----
+  constexpr int EP = C::EPI_PITCH;
+  constexpr int COLS = FN * 16;
+  constexpr int LPR = COLS / 4;                  // lanes per row (4 columns each)
+  constexpr int RPI = 64 / LPR;                  // rows per read instruction
+  float* ep = reinterpret_cast<float*>(big_smem) + wave * 16 * EP;
+  const TB* bias = p.bias ? static_cast<const TB*>(p.bias) + static_cast<int64_t>(mdl) * p.b_sn : nullptr;
+  TC* cbase = static_cast<TC*>(p.c) + static_cast<int64_t>(mdl) * p.c_sn;
+  const TC* rbase = p.r ? static_cast<const TC*>(p.r) + static_cast<int64_t>(mdl) * p.r_sn : nullptr;
+  const int lc = (lane % LPR) * 4;               // this lane's 4 columns within the strip
+  const int col0 = o0 + wn * COLS + lc;
+  const bool vec4 = (p.o & 3) == 0;
+  float bv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) bv[e] = (bias && col0 + e < p.o) ? to_f32(bias[col0 + e]) : 0.f;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ep[((lane >> 4) * 4 + e) * EP + j * 16 + fr] = acc[i][j][e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0): this wave's strip is in LDS
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int rr = 0; rr < 16; rr += RPI) {
+      const int lr = rr + lane / LPR;
+      const int row = m0 + wm * FM * 16 + i * 16 + lr;
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(ep + lr * EP + lc);
+      if (row < p.m && col0 < p.o) {
+        const uint32_t outer = fdiv(static_cast<uint32_t>(row), p.c_ri);
+        const uint32_t inner = row - outer * p.c_ri.d;
+        const int64_t off = static_cast<int64_t>(outer) * p.c_so + static_cast<int64_t>(inner) * p.c_si + col0;
+        float v[4] = {v4[0] + bv[0], v4[1] + bv[1], v4[2] + bv[2], v4[3] + bv[3]};
+        if (rbase) {
+          const int64_t roff = static_cast<int64_t>(outer) * p.r_so + static_cast<int64_t>(inner) * p.r_si + col0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col0 + e < p.o) v[e] += to_f32(rbase[roff + e]);
+        }
+        if (p.act == WC_ACT_RELU)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = relu_f(v[e]);
+        if (vec4 && col0 + 3 < p.o) {
+          if constexpr (sizeof(TC) == 4) {
+            *reinterpret_cast<f32x4*>(cbase + off) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+            bf16x4 o4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = from_f32<bf16>(v[e]);
+            *reinterpret_cast<bf16x4*>(cbase + off) = o4;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col0 + e < p.o) cbase[off + e] = from_f32<TC>(v[e]);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+template <typename TC, typename TB, int WM, int WN, int FM, int FN>
+int32_t launch_big(GemmParams p, hipStream_t st) {
+  using C = BigCfg<WM, WN, FM, FN>;
+  p.tiles_m = static_cast<int>(cdiv(p.m, C::BM));
+  p.tiles_o = static_cast<int>(cdiv(p.o, C::BN));
+  const int64_t nblk = static_cast<int64_t>(p.n) * p.tiles_m * p.tiles_o;
+  if (nblk >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_grouped_gemm: too many tiles");
+  p.remap = (nblk % 8 == 0) ? 1 : 0;
+  auto kern = gemm_big_kernel<TC, TB, WM, WN, FM, FN>;
+  if (C::LDS > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(C::LDS));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_grouped_gemm: LDS of %zu bytes refused: %s", C::LDS,
+                       hipGetErrorString(e));
+  }
+  kern<<<dim3(static_cast<uint32_t>(nblk)), dim3(C::NT), C::LDS, st>>>(p);
+  return check_launch("wc_grouped_gemm");
+}
+
 template <typename TA, typename TC, typename TB, int TM, int TN, int WM, int WN>
 int32_t launch_cfg(GemmParams p, bool vec, hipStream_t st) {
   constexpr int BM = WM * TM, BN = WN * TN;
@@ -244,10 +444,17 @@ int32_t launch_cfg(GemmParams p, bool vec, hipStream_t st) {
 
 template <typename TA, typename TC, typename TB>
 int32_t launch_gemm_t(const GemmParams& p, bool vec, hipStream_t st) {
-  // small problems: 64x64 tiles keep more workgroups in flight
+  if constexpr (sizeof(TA) == 2) {
+    const int64_t tiles256 = static_cast<int64_t>(p.n) * cdiv(p.m, 256) * cdiv(p.o, 256);
+    if (vec && tiles256 >= 256) return launch_big<TC, TB, 2, 4, 8, 4>(p, st);
+  }
   const int64_t tiles128 = static_cast<int64_t>(p.n) * cdiv(p.m, 128) * cdiv(p.o, 128);
   if (tiles128 >= 512) return launch_cfg<TA, TC, TB, 64, 64, 2, 2>(p, vec, st);
-  return launch_cfg<TA, TC, TB, 32, 32, 2, 2>(p, vec, st);
+  const int64_t tiles64 = static_cast<int64_t>(p.n) * cdiv(p.m, 64) * cdiv(p.o, 64);
+  if (tiles64 >= 1024) return launch_cfg<TA, TC, TB, 32, 32, 2, 2>(p, vec, st);
+  // small problems are latency-bound: 16 x 16 wave tiles give each wave the
+  // fewest dependent MFMAs and the most workgroups in flight
+  return launch_cfg<TA, TC, TB, 16, 16, 2, 2>(p, vec, st);
 }
 
 }  // namespace

@@ -69,13 +69,14 @@ __device__ __forceinline__ float dpp(float v) {
                                                                0xF, true));
 }
 
-// sum over groups of LG adjacent lanes (8: half-row, 16: row), delivered to
-// every lane of the group
+// sum over groups of LG adjacent lanes (2, 4: part of a quad; 8: half-row;
+// 16: row), delivered to every lane of the group
 template <int LG>
 __device__ __forceinline__ float group_sum_dpp(float v) {
-  v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]
-  v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]
-  v += dpp<0x141>(v);   // row_half_mirror: lane i <- 7 - i within each 8 lanes
+  static_assert(LG == 2 || LG == 4 || LG == 8 || LG == 16, "group size");
+  v += dpp<0xB1>(v);                  // quad_perm [1,0,3,2]
+  if (LG >= 4) v += dpp<0x4E>(v);     // quad_perm [2,3,0,1]
+  if (LG >= 8) v += dpp<0x141>(v);    // row_half_mirror: lane i <- 7 - i within each 8 lanes
   if (LG == 16) v += dpp<0x140>(v);   // row_mirror: lane i <- 15 - i
   return v;
 }
@@ -282,30 +283,30 @@ int32_t launch_lds(K kernel, const RnnParams& p, dim3 grid, dim3 block, size_t l
   return check_launch("wc_rnn_recurrence");
 }
 
-template <typename T, int CELL, int LG, int UPG>
-int32_t launch_kl(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-  switch (p.kl) {
-    case 4: return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, 4>, p, grid, block, lds, st);
-    case 8: return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, 8>, p, grid, block, lds, st);
-    case 16: return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, 16>, p, grid, block, lds, st);
-    default: return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: %d columns per lane unsupported", p.kl);
-  }
+template <typename T, int CELL, int LG, int UPG, int KL>
+int32_t launch_one(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
+  return launch_lds(rnn_seq_kernel<T, CELL, LG, UPG, KL>, p, grid, block, lds, st);
 }
 
-template <typename T, int CELL, int LG>
-int32_t launch_upg(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-  switch (p.upg) {
-    case 1: return launch_kl<T, CELL, LG, 1>(p, grid, block, lds, st);
-    case 2: return launch_kl<T, CELL, LG, 2>(p, grid, block, lds, st);
-    case 4: return launch_kl<T, CELL, LG, 4>(p, grid, block, lds, st);
-    default: return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: %d units per group unsupported", p.upg);
-  }
-}
-
+// The (lanes per group, units per group, columns per lane) shapes rnn_plan may pick.
 template <typename T, int CELL>
 int32_t launch_rec(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-  if (p.lg == 8) return launch_upg<T, CELL, 8>(p, grid, block, lds, st);
-  return launch_upg<T, CELL, 16>(p, grid, block, lds, st);
+#define WC_RNN_SHAPE(LG, UPG, KL)                      \
+  if (p.lg == LG && p.upg == UPG && p.kl == KL) \
+    return launch_one<T, CELL, LG, UPG, KL>(p, grid, block, lds, st);
+  WC_RNN_SHAPE(16, 1, 4) WC_RNN_SHAPE(16, 2, 4) WC_RNN_SHAPE(16, 4, 4)
+  WC_RNN_SHAPE(16, 1, 8) WC_RNN_SHAPE(16, 2, 8) WC_RNN_SHAPE(16, 4, 8)
+  WC_RNN_SHAPE(16, 1, 16) WC_RNN_SHAPE(16, 2, 16) WC_RNN_SHAPE(16, 4, 16)
+  WC_RNN_SHAPE(8, 1, 4) WC_RNN_SHAPE(8, 2, 4) WC_RNN_SHAPE(8, 4, 4)
+  WC_RNN_SHAPE(8, 1, 8) WC_RNN_SHAPE(8, 2, 8) WC_RNN_SHAPE(8, 4, 8)
+  WC_RNN_SHAPE(8, 1, 16) WC_RNN_SHAPE(8, 2, 16) WC_RNN_SHAPE(8, 4, 16)
+  WC_RNN_SHAPE(4, 1, 8) WC_RNN_SHAPE(4, 2, 8)
+  WC_RNN_SHAPE(4, 1, 16) WC_RNN_SHAPE(4, 2, 16)
+  WC_RNN_SHAPE(4, 1, 32)
+  WC_RNN_SHAPE(2, 1, 32)
+#undef WC_RNN_SHAPE
+  return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: no kernel for %d lanes x %d units x %d columns", p.lg,
+                   p.upg, p.kl);
 }
 
 inline int round4(int v) { return (v + 3) & ~3; }
@@ -346,7 +347,7 @@ struct StepCfg {
 };
 
 template <typename T, int CELL>
-__global__ __launch_bounds__(kStepThreads) void rnn_step_kernel(StepParams p) {
+__global__ __launch_bounds__(kStepThreads, 4) void rnn_step_kernel(StepParams p) {
   using C = StepCfg<T, CELL>;
   constexpr int GATES = C::GATES, NTW = C::NTW, R = C::R, UB = C::UB;
   constexpr bool BF = sizeof(T) == 2;
@@ -377,26 +378,65 @@ __global__ __launch_bounds__(kStepThreads) void rnn_step_kernel(StepParams p) {
       const int q = r / UB, u = u0 + (r - q * UB);
       wrow[j] = (u < H) ? wb + static_cast<int64_t>(q * H + u) * H + g * 8 : nullptr;
     }
+    // K loop software-pipelined PD k-steps deep: the loads of k-step k + PD are
+    // issued as soon as k-step k has been consumed, so PD loads per operand are
+    // in flight behind the MFMAs (W_hh streams from L2 / MALL every step).
     if (p.hprev) {
-      for (int k0 = 0; k0 < H; k0 += 32) {
-        if constexpr (BF) {
-          const bf16x8 a = arow ? *reinterpret_cast<const bf16x8*>(arow + k0) : bf16x8{};
+      const int nk = H / 32;
+      if constexpr (BF) {
+        constexpr int PD = 4;
+        bf16x8 ra[PD], rb[PD][NTW];
+        auto ld = [&](bf16x8& a, bf16x8 (&b)[NTW], int k) {
+          const int k0 = k * 32;
+          a = arow ? *reinterpret_cast<const bf16x8*>(arow + k0) : bf16x8{};
 #pragma unroll
-          for (int j = 0; j < NTW; ++j) {
-            const bf16x8 bv = wrow[j] ? *reinterpret_cast<const bf16x8*>(wrow[j] + k0) : bf16x8{};
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bv, acc[j], 0, 0, 0);
+          for (int j = 0; j < NTW; ++j)
+            b[j] = wrow[j] ? *reinterpret_cast<const bf16x8*>(wrow[j] + k0) : bf16x8{};
+        };
+#pragma unroll
+        for (int s = 0; s < PD; ++s)
+          if (s < nk) ld(ra[s], rb[s], s);
+        for (int k0 = 0; k0 < nk; k0 += PD) {
+#pragma unroll
+          for (int s = 0; s < PD; ++s) {
+            if (k0 + s < nk) {
+#pragma unroll
+              for (int j = 0; j < NTW; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[s], rb[s][j], acc[j], 0, 0, 0);
+              if (k0 + s + PD < nk) ld(ra[s], rb[s], k0 + s + PD);
+            }
           }
-        } else {
-          const f32x4 a0 = arow ? *reinterpret_cast<const f32x4*>(arow + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
-          const f32x4 a1 = arow ? *reinterpret_cast<const f32x4*>(arow + k0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      } else {
+        constexpr int PD = 2;
+        f32x4 ra[PD][2], rb[PD][NTW][2];
+        const f32x4 z4 = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto ld = [&](f32x4 (&a)[2], f32x4 (&b)[NTW][2], int k) {
+          const int k0 = k * 32;
+          a[0] = arow ? *reinterpret_cast<const f32x4*>(arow + k0) : z4;
+          a[1] = arow ? *reinterpret_cast<const f32x4*>(arow + k0 + 4) : z4;
 #pragma unroll
           for (int j = 0; j < NTW; ++j) {
-            const f32x4 b0v = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
-            const f32x4 b1v = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+            b[j][0] = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0) : z4;
+            b[j][1] = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0 + 4) : z4;
+          }
+        };
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], b0v[e], acc[j], 0, 0, 0);
+        for (int s = 0; s < PD; ++s)
+          if (s < nk) ld(ra[s], rb[s], s);
+        for (int k0 = 0; k0 < nk; k0 += PD) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], b1v[e], acc[j], 0, 0, 0);
+          for (int s = 0; s < PD; ++s) {
+            if (k0 + s < nk) {
+#pragma unroll
+              for (int j = 0; j < NTW; ++j) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[s][e >> 2][e & 3], rb[s][j][e >> 2][e & 3],
+                                                                acc[j], 0, 0, 0);
+              }
+              if (k0 + s + PD < nk) ld(ra[s], rb[s], k0 + s + PD);
+            }
           }
         }
       }
@@ -456,22 +496,37 @@ using namespace wc;
 
 // Chooses the lane layout of the register-resident kernel; false when the
 // weights of one (model, batch row) do not fit the register file.
+// Pick the lane shape of the persistent kernel.  Per step every SIMD issues,
+// for each of its waves, the lane's GATES*UPG*KL FMAs, KL/4 LDS reads,
+// GATES*UPG*log2(LG) DPP adds and a roughly fixed cell update (~60 issue
+// slots with its transcendentals); the shape with the fewest slots on the
+// busiest SIMD wins.  Weight registers stay <= 176 per lane (no spills).
 static bool rnn_plan(int gates, int hid, RnnParams& p) {
-  for (int lg = 8; lg <= 16; lg <<= 1) {
-    const int kl = round4((hid + lg - 1) / lg);
-    if (kl > 16) continue;
-    for (int upg = 1; upg <= 4; upg <<= 1) {
-      const int threads = ((hid + upg - 1) / upg) * lg;
-      const int regs = gates * upg * kl;              // weight registers per lane
-      if (regs > 176) break;
-      if (round_up(threads, 64) > rnn_bound(gates, upg, kl)) continue;
+  static const int kShapes[][3] = {   // {LG, UPG, KL}: the instantiated kernels
+      {16, 1, 4}, {16, 2, 4}, {16, 4, 4}, {16, 1, 8}, {16, 2, 8}, {16, 4, 8}, {16, 1, 16}, {16, 2, 16},
+      {16, 4, 16}, {8, 1, 4}, {8, 2, 4}, {8, 4, 4}, {8, 1, 8}, {8, 2, 8}, {8, 4, 8}, {8, 1, 16},
+      {8, 2, 16}, {8, 4, 16}, {4, 1, 8}, {4, 2, 8}, {4, 1, 16}, {4, 2, 16}, {4, 1, 32}, {2, 1, 32}};
+  long best = -1;
+  for (const auto& sh : kShapes) {
+    const int lg = sh[0], upg = sh[1], kl = sh[2];
+    const int need = (hid + lg - 1) / lg;                    // columns per lane
+    if (kl < need || (kl > 4 && kl / 2 >= need)) continue;   // the tightest instantiated KL only
+    const int regs = gates * upg * kl;
+    if (regs > 176) continue;
+    const int threads = round_up(((hid + upg - 1) / upg) * lg, 64);
+    if (threads > rnn_bound(gates, upg, kl)) continue;
+    const int waves_per_simd = (threads / 64 + 3) / 4;
+    int lg2 = 0;
+    while ((1 << lg2) < lg) ++lg2;
+    const long cost = static_cast<long>(waves_per_simd) * (regs + kl / 4 + gates * upg * lg2 + 60);
+    if (best < 0 || cost < best) {
+      best = cost;
       p.lg = lg;
       p.kl = kl;
       p.upg = upg;
-      return true;
     }
   }
-  return false;
+  return best >= 0;
 }
 
 static int64_t rnn_ws_bytes(const wc_rnn_args* a) {
@@ -583,28 +638,8 @@ extern "C" int32_t wc_rnn_input_projection(const wc_rnn_args* a, void* stream) {
   return grouped_gemm(g, a->dtype, WC_F32, a->dtype, as_stream(stream));
 }
 
-extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
-  clear_error();
-  RnnParams p;
-  int gates = 0;
-  int32_t rc = rnn_check(a, "wc_rnn_recurrence", p, gates);
-  if (rc) return rc;
-  if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
-  WC_REQUIRE(a->w_hh && a->out, WC_ERR_NULL, "wc_rnn_recurrence: null pointer");
-  if (!rnn_plan(gates, p.hid, p)) {
-    // W_hh of one model does not fit a workgroup's registers: one launch per step
-    const int es = dtype_size(a->dtype);
-    WC_REQUIRE(aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && p.hid % 32 == 0 &&
-                   (!a->h0 || aligned(a->h0, 16)) && aligned(a->out, 16),
-               WC_ERR_ALIGN, "wc_rnn_recurrence: hidden=%d needs hidden %% 32 == 0 and 16-byte aligned "
-               "W_hh / h0 / out for the streamed recurrence", p.hid);
-    hipStream_t st = as_stream(stream);
-    if (a->dtype == WC_F32)
-      return a->cell == WC_CELL_GRU ? streamed_recurrence<float, WC_CELL_GRU>(a, p, st)
-                                    : streamed_recurrence<float, WC_CELL_LSTM>(a, p, st);
-    return a->cell == WC_CELL_GRU ? streamed_recurrence<bf16, WC_CELL_GRU>(a, p, st)
-                                  : streamed_recurrence<bf16, WC_CELL_LSTM>(a, p, st);
-  }
+// Launch the persistent kernel with the lane shape already in p (lg, kl, upg).
+static int32_t persistent_recurrence(const wc_rnn_args* a, RnnParams p, int gates, hipStream_t st) {
   const int nwg = p.n * p.batch;
   p.remap = (nwg % 8 == 0) ? 1 : 0;
   p.gx = static_cast<const float*>(a->workspace);
@@ -627,13 +662,37 @@ extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
   p.wvec = (aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && (p.kl * es) % 16 == 0) ? 1 : 0;
   const dim3 grid(nwg), block(threads);
   const size_t lds = fixed + per_step * static_cast<size_t>(p.xt);
-  hipStream_t st = as_stream(stream);
   if (a->dtype == WC_F32) {
     if (a->cell == WC_CELL_GRU) return launch_rec<float, WC_CELL_GRU>(p, grid, block, lds, st);
     return launch_rec<float, WC_CELL_LSTM>(p, grid, block, lds, st);
   }
   if (a->cell == WC_CELL_GRU) return launch_rec<bf16, WC_CELL_GRU>(p, grid, block, lds, st);
   return launch_rec<bf16, WC_CELL_LSTM>(p, grid, block, lds, st);
+}
+
+extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
+  clear_error();
+  RnnParams p;
+  int gates = 0;
+  int32_t rc = rnn_check(a, "wc_rnn_recurrence", p, gates);
+  if (rc) return rc;
+  if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
+  WC_REQUIRE(a->w_hh && a->out, WC_ERR_NULL, "wc_rnn_recurrence: null pointer");
+  if (!rnn_plan(gates, p.hid, p)) {
+    // W_hh of one model does not fit a workgroup's registers: one launch per step
+    const int es = dtype_size(a->dtype);
+    WC_REQUIRE(aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && p.hid % 32 == 0 &&
+                   (!a->h0 || aligned(a->h0, 16)) && aligned(a->out, 16),
+               WC_ERR_ALIGN, "wc_rnn_recurrence: hidden=%d needs hidden %% 32 == 0 and 16-byte aligned "
+               "W_hh / h0 / out for the streamed recurrence", p.hid);
+    hipStream_t st = as_stream(stream);
+    if (a->dtype == WC_F32)
+      return a->cell == WC_CELL_GRU ? streamed_recurrence<float, WC_CELL_GRU>(a, p, st)
+                                    : streamed_recurrence<float, WC_CELL_LSTM>(a, p, st);
+    return a->cell == WC_CELL_GRU ? streamed_recurrence<bf16, WC_CELL_GRU>(a, p, st)
+                                  : streamed_recurrence<bf16, WC_CELL_LSTM>(a, p, st);
+  }
+  return persistent_recurrence(a, p, gates, as_stream(stream));
 }
 
 extern "C" int32_t wc_rnn_forward(const wc_rnn_args* a, void* stream) {

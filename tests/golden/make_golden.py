@@ -159,15 +159,15 @@ def main():
               {"out": torch.stack([o for o, _ in outs]), "h_n": torch.stack([h[0][0] for _, h in outs]),
                "c_n": torch.stack([h[1][0] for _, h in outs])}, {"input_size": 5, "hidden": 6})
 
-        # MultiheadAttention: N=2, embed 8, 2 heads, self-attention x [2, 2, 5, 8]
+        # MultiheadAttention: N=2, embed 32, 2 heads (head dim 16), self-attention x [2, 2, 5, 32]
         mods = []
         for i in range(2):
             _seed(80 + i)
-            mods.append(_perturb(nn.MultiheadAttention(8, 2, batch_first=True)).eval())
-        x = torch.randn(2, 2, 5, 8, generator=_gen(12))
+            mods.append(_perturb(nn.MultiheadAttention(32, 2, batch_first=True)).eval())
+        x = torch.randn(2, 2, 5, 32, generator=_gen(12))
         _save("attention", mods, {"x": x},
               {"y": torch.stack([m(x[i], x[i], x[i], need_weights=False)[0] for i, m in enumerate(mods)])},
-              {"embed": 8, "heads": 2})
+              {"embed": 32, "heads": 2})
 
         # MLP (Linear-ReLU-Linear): N=3, packed input [4, 3*64]
         mods = []

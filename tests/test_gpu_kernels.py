@@ -183,6 +183,39 @@ def test_linear(hip, dtype, n, batch, i, o, bias):
         assert rel_err(y, wide_ref.linear(x, w, b)) <= TOL_BF16
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,o,k", [(300, 300, 264), (256, 260, 64), (257, 255, 72), (512, 256, 512)])
+@pytest.mark.parametrize("rows_inner", [None, 7])
+def test_grouped_gemm_large_tiles(hip, out_dtype, m, o, k, rows_inner):
+    """bf16 problems big enough (>= 256 tiles of 256 x 256) for the large-tile kernel: ragged
+    M / O / K, two-level row addressing, bias + residual + ReLU epilogue, bf16 or fp32 out."""
+    from wide_compiler import _hip
+    n = 128
+    g = gen(113)
+    a = _rand((n, m, k), g, torch.bfloat16)
+    w = (_rand((n, o, k), g) * k ** -0.5).to(torch.bfloat16)
+    bias = _rand((n, o), g, torch.bfloat16)
+    res = _rand((n, m, o), g, out_dtype)
+    ri = rows_inner or m
+    if rows_inner:
+        # rows m = outer * ri + inner live at outer * (ri + 3) * k + inner * k: a padded layout
+        outer = (m + ri - 1) // ri
+        a_store = torch.zeros((n, outer * (ri + 3), k), dtype=torch.bfloat16)
+        for r in range(m):
+            a_store[:, (r // ri) * (ri + 3) + r % ri] = a[:, r]
+        a_so = (ri + 3) * k
+    else:
+        a_store, a_so = a, 0
+    a_d, w_d, b_d, r_d = (t.to(DEV) for t in (a_store, w, bias, res))
+    c = torch.empty((n, m, o), dtype=out_dtype, device=DEV)
+    _hip.grouped_gemm(n=n, m=m, o=o, k=k, a=a_d, a_sn=a_store.shape[1] * k, a_so=a_so, a_si=k, a_rows_inner=ri,
+                      w=w_d, w_sn=o * k, c=c, c_sn=m * o, c_so=0, c_si=o, c_rows_inner=m, bias=b_d, bias_sn=o,
+                      residual=r_d, r_sn=m * o, r_so=0, r_si=o, relu=True)
+    exact = F.relu(torch.bmm(a.double(), w.double().transpose(1, 2).contiguous()) + bias.double().unsqueeze(1)
+                   + res.double())
+    assert rel_err(c.cpu(), exact) <= TOL_BF16
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_linear_strided_boundary_view_and_relu(hip, dtype):
     import wide_compiler as wc
