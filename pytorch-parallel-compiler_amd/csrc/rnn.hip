@@ -24,6 +24,8 @@
 // them across the group with log2(LG) DPP butterfly adds (no LDS traffic).
 // Lane k < UPG of the group then applies the cell update of unit g*UPG + k and
 // writes h into LDS; one barrier per step.
+#include <type_traits>
+
 #include "wc_gemm.h"
 
 namespace wc {
@@ -347,30 +349,28 @@ struct StepCfg {
 };
 
 template <typename T, int CELL>
-__global__ __launch_bounds__(kStepThreads, 4) void rnn_step_kernel(StepParams p) {
+__global__ __launch_bounds__(kStepThreads, CELL == WC_CELL_GRU ? 2 : 4) void rnn_step_kernel(StepParams p) {
   using C = StepCfg<T, CELL>;
   constexpr int GATES = C::GATES, NTW = C::NTW, R = C::R, UB = C::UB;
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int RP = R + 4;                                   // LDS pitch of the gate tile
-  __shared__ float gs[16 * RP];
+  constexpr int RP = R + 4;                       // LDS pitch of the gate tile (floats)
+  constexpr int VE = 16 / sizeof(T);              // elements per 16-byte chunk
+  constexpr int PAIRS = 16 * UB / kStepThreads;   // (batch row, unit) pairs per thread
+  static_assert(PAIRS * kStepThreads == 16 * UB, "pairs");
+  extern __shared__ __attribute__((aligned(16))) float step_smem[];
+  float* gs = step_smem;                                        // [16][RP] gate pre-activations
+  T* hs = reinterpret_cast<T*>(step_smem + 16 * RP);            // [16][H + VE] h_{t-1} rows
 
-  const int H = p.hid, G = GATES * H;
+  const int H = p.hid, G = GATES * H, HP = H + VE;
   const int mdl = blockIdx.x / p.ublocks;
   const int ub = blockIdx.x - mdl * p.ublocks;
   const int u0 = ub * UB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int fr = lane & 15, g = lane >> 4;
   const T* wb = static_cast<const T*>(p.w_hh) + static_cast<int64_t>(mdl) * G * H;
+  const int nk = H / 32;
 
   for (int b0 = 0; b0 < p.batch; b0 += 16) {
-    // ---- G = h_{t-1} W^T over 16 batch rows x R gate rows ----
-    f32x4 acc[NTW];
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int brow = b0 + fr;
-    const T* arow = (p.hprev && brow < p.batch)
-                        ? static_cast<const T*>(p.hprev) + mdl * p.hp_sn + brow * p.hp_sb + g * 8
-                        : nullptr;
     const T* wrow[NTW];
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
@@ -378,65 +378,80 @@ __global__ __launch_bounds__(kStepThreads, 4) void rnn_step_kernel(StepParams p)
       const int q = r / UB, u = u0 + (r - q * UB);
       wrow[j] = (u < H) ? wb + static_cast<int64_t>(q * H + u) * H + g * 8 : nullptr;
     }
-    // K loop software-pipelined PD k-steps deep: the loads of k-step k + PD are
-    // issued as soon as k-step k has been consumed, so PD loads per operand are
-    // in flight behind the MFMAs (W_hh streams from L2 / MALL every step).
+    // (1) W_hh ring: PD k-steps of B fragments in flight (streams from L2 / MALL)
+    constexpr int PD = BF ? 4 : 2;
+    constexpr int BR = BF ? 1 : 2;                  // 16-byte pieces per fragment
+    typedef typename std::conditional<BF, bf16x8, f32x4>::type frag_t;
+    frag_t rb[PD][NTW][BR];
+    auto ld = [&](frag_t (&b)[NTW][BR], int k) {
+#pragma unroll
+      for (int j = 0; j < NTW; ++j)
+#pragma unroll
+        for (int h2 = 0; h2 < BR; ++h2)
+          b[j][h2] = wrow[j] ? *reinterpret_cast<const frag_t*>(wrow[j] + k * 32 + h2 * 4) : frag_t{};
+    };
     if (p.hprev) {
-      const int nk = H / 32;
-      if constexpr (BF) {
-        constexpr int PD = 4;
-        bf16x8 ra[PD], rb[PD][NTW];
-        auto ld = [&](bf16x8& a, bf16x8 (&b)[NTW], int k) {
-          const int k0 = k * 32;
-          a = arow ? *reinterpret_cast<const bf16x8*>(arow + k0) : bf16x8{};
 #pragma unroll
-          for (int j = 0; j < NTW; ++j)
-            b[j] = wrow[j] ? *reinterpret_cast<const bf16x8*>(wrow[j] + k0) : bf16x8{};
-        };
+      for (int s = 0; s < PD; ++s)
+        if (s < nk) ld(rb[s], s);
+    }
+    // (2) the cell update's inputs, fetched now so they arrive during the K loop
+    float gxv[PAIRS][GATES], cprev[PAIRS];
 #pragma unroll
-        for (int s = 0; s < PD; ++s)
-          if (s < nk) ld(ra[s], rb[s], s);
-        for (int k0 = 0; k0 < nk; k0 += PD) {
+    for (int q = 0; q < PAIRS; ++q) {
+      const int e = tid + q * kStepThreads;
+      const int bl = e / UB, ul = e - (e / UB) * UB;
+      const int b = b0 + bl, u = u0 + ul;
+      const bool ok = b < p.batch && u < H;
+      const int64_t nb = static_cast<int64_t>(mdl) * p.batch + b;
+      const float* gxr = p.gx + (nb * p.steps + p.t) * G + u;
 #pragma unroll
-          for (int s = 0; s < PD; ++s) {
-            if (k0 + s < nk) {
+      for (int gi = 0; gi < GATES; ++gi) gxv[q][gi] = ok ? gxr[gi * H] : 0.f;
+      cprev[q] = 0.f;
+      if (CELL == WC_CELL_LSTM && ok)
+        cprev[q] = p.t == 0 ? (p.c0 ? ldf<T>(p.c0, nb * H + u) : 0.f) : p.cst[nb * H + u];
+    }
+    // (3) h_{t-1} rows of this batch tile -> LDS (read once per workgroup)
+    for (int c = tid; c < 16 * (H / VE); c += kStepThreads) {
+      const int row = c / (H / VE), col = (c - row * (H / VE)) * VE;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (p.hprev && b0 + row < p.batch)
+        v = *reinterpret_cast<const uint4*>(static_cast<const T*>(p.hprev) + mdl * p.hp_sn +
+                                             static_cast<int64_t>(b0 + row) * p.hp_sb + col);
+      *reinterpret_cast<uint4*>(hs + row * HP + col) = v;
+    }
+    __syncthreads();
+
+    // (4) G = h_{t-1} W^T: 16 batch rows x R gate rows, A fragments from LDS
+    f32x4 acc[NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (p.hprev) {
+      const T* arow = hs + fr * HP + g * 8;
+      for (int k0 = 0; k0 < nk; k0 += PD) {
+#pragma unroll
+        for (int s = 0; s < PD; ++s) {
+          if (k0 + s < nk) {
+            const int k = k0 + s;
+            if constexpr (BF) {
+              const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + k * 32);
 #pragma unroll
               for (int j = 0; j < NTW; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ra[s], rb[s][j], acc[j], 0, 0, 0);
-              if (k0 + s + PD < nk) ld(ra[s], rb[s], k0 + s + PD);
-            }
-          }
-        }
-      } else {
-        constexpr int PD = 2;
-        f32x4 ra[PD][2], rb[PD][NTW][2];
-        const f32x4 z4 = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto ld = [&](f32x4 (&a)[2], f32x4 (&b)[NTW][2], int k) {
-          const int k0 = k * 32;
-          a[0] = arow ? *reinterpret_cast<const f32x4*>(arow + k0) : z4;
-          a[1] = arow ? *reinterpret_cast<const f32x4*>(arow + k0 + 4) : z4;
-#pragma unroll
-          for (int j = 0; j < NTW; ++j) {
-            b[j][0] = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0) : z4;
-            b[j][1] = wrow[j] ? *reinterpret_cast<const f32x4*>(wrow[j] + k0 + 4) : z4;
-          }
-        };
-#pragma unroll
-        for (int s = 0; s < PD; ++s)
-          if (s < nk) ld(ra[s], rb[s], s);
-        for (int k0 = 0; k0 < nk; k0 += PD) {
-#pragma unroll
-          for (int s = 0; s < PD; ++s) {
-            if (k0 + s < nk) {
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, rb[s][j][0], acc[j], 0, 0, 0);
+            } else {
+              const f32x4 a0 = *reinterpret_cast<const f32x4*>(arow + k * 32);
+              const f32x4 a1 = *reinterpret_cast<const f32x4*>(arow + k * 32 + 4);
 #pragma unroll
               for (int j = 0; j < NTW; ++j) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                  acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ra[s][e >> 2][e & 3], rb[s][j][e >> 2][e & 3],
-                                                                acc[j], 0, 0, 0);
+                for (int e = 0; e < 4; ++e)
+                  acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], rb[s][j][0][e], acc[j], 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], rb[s][j][1][e], acc[j], 0, 0, 0);
               }
-              if (k0 + s + PD < nk) ld(ra[s], rb[s], k0 + s + PD);
             }
+            if (k + PD < nk) ld(rb[s], k + PD);
           }
         }
       }
@@ -450,32 +465,32 @@ __global__ __launch_bounds__(kStepThreads, 4) void rnn_step_kernel(StepParams p)
     }
     __syncthreads();
 
-    // ---- cell update for (batch row, unit) pairs ----
-    for (int e = tid; e < 16 * UB; e += kStepThreads) {
-      const int bl = e / UB, ul = e - bl * UB;
+    // (5) cell update for this thread's (batch row, unit) pairs
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) {
+      const int e = tid + q * kStepThreads;
+      const int bl = e / UB, ul = e - (e / UB) * UB;
       const int b = b0 + bl, u = u0 + ul;
       if (b >= p.batch || u >= H) continue;
       const int64_t nb = static_cast<int64_t>(mdl) * p.batch + b;
-      const float* gxr = p.gx + (nb * p.steps + p.t) * G + u;
       const float* ghr = gs + bl * RP + ul;
       float gh[GATES];
 #pragma unroll
-      for (int q = 0; q < GATES; ++q)
-        gh[q] = ghr[q * UB] + (p.b_hh ? ldf<T>(p.b_hh, static_cast<int64_t>(mdl) * G + q * H + u) : 0.f);
+      for (int gi = 0; gi < GATES; ++gi)
+        gh[gi] = ghr[gi * UB] + (p.b_hh ? ldf<T>(p.b_hh, static_cast<int64_t>(mdl) * G + gi * H + u) : 0.f);
       float hnew, cnew = 0.f;
       if (CELL == WC_CELL_GRU) {
-        const float hprev = p.hprev ? ldf<T>(p.hprev, mdl * p.hp_sn + b * p.hp_sb + u) : 0.f;
-        const float rg = sigmoid_f(gxr[0] + gh[0]);
-        const float zg = sigmoid_f(gxr[H] + gh[1]);
-        const float nn = tanh_f(gxr[2 * H] + rg * gh[2]);
+        const float hprev = to_f32(hs[bl * HP + u]);
+        const float rg = sigmoid_f(gxv[q][0] + gh[0]);
+        const float zg = sigmoid_f(gxv[q][1] + gh[1]);
+        const float nn = tanh_f(gxv[q][2] + rg * gh[2]);
         hnew = (1.0f - zg) * nn + zg * hprev;
       } else {
-        const float cprev = p.t == 0 ? (p.c0 ? ldf<T>(p.c0, nb * H + u) : 0.f) : p.cst[nb * H + u];
-        const float ig = sigmoid_f(gxr[0] + gh[0]);
-        const float fg = sigmoid_f(gxr[H] + gh[1]);
-        const float gg = tanh_f(gxr[2 * H] + gh[2]);
-        const float og = sigmoid_f(gxr[3 * H] + gh[3]);
-        cnew = fg * cprev + ig * gg;
+        const float ig = sigmoid_f(gxv[q][0] + gh[0]);
+        const float fg = sigmoid_f(gxv[q][1] + gh[1]);
+        const float gg = tanh_f(gxv[q][2] + gh[2]);
+        const float og = sigmoid_f(gxv[q][3] + gh[3]);
+        cnew = fg * cprev[q] + ig * gg;
         hnew = og * tanh_f(cnew);
         p.cst[nb * H + u] = cnew;
       }
@@ -487,6 +502,12 @@ __global__ __launch_bounds__(kStepThreads, 4) void rnn_step_kernel(StepParams p)
     }
     __syncthreads();
   }
+}
+
+template <typename T, int CELL>
+size_t step_lds_bytes(int hid) {
+  using C = StepCfg<T, CELL>;
+  return sizeof(float) * 16 * (C::R + 4) + sizeof(T) * 16 * static_cast<size_t>(hid + 16 / sizeof(T));
 }
 
 }  // namespace
@@ -555,6 +576,16 @@ static int32_t streamed_recurrence(const wc_rnn_args* a, const RnnParams& rp, hi
   p.hn = a->h_n;
   p.cn = a->c_n;
   const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(rp.n) * p.ublocks));
+  const size_t lds = step_lds_bytes<T, CELL>(rp.hid);
+  if (lds > 160 * 1024)
+    return set_error(WC_ERR_LIMIT, "wc_rnn_recurrence: hidden=%d exceeds the streamed kernel's LDS", rp.hid);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(rnn_step_kernel<T, CELL>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_rnn_recurrence: LDS of %zu bytes refused: %s", lds,
+                       hipGetErrorString(e));
+  }
   for (int t = 0; t < rp.steps; ++t) {
     p.t = t;
     if (t == 0) {
@@ -566,7 +597,7 @@ static int32_t streamed_recurrence(const wc_rnn_args* a, const RnnParams& rp, hi
       p.hp_sn = static_cast<int64_t>(rp.batch) * rp.steps * rp.hid;
       p.hp_sb = static_cast<int64_t>(rp.steps) * rp.hid;
     }
-    rnn_step_kernel<T, CELL><<<grid, kStepThreads, 0, st>>>(p);
+    rnn_step_kernel<T, CELL><<<grid, kStepThreads, lds, st>>>(p);
     int32_t rc = check_launch("wc_rnn_recurrence(step)");
     if (rc) return rc;
   }
