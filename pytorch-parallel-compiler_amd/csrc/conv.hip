@@ -67,6 +67,120 @@ template <> struct ConvTraits<float> {
   static constexpr int kPad = 4;
 };
 
+// Epilogue shared by the conv kernels (LDS free on entry): bias + folded eval
+// BatchNorm into LDS as [co][pixel] in the output type, then residual add +
+// ReLU during coalesced NCHW stores.
+// Per-lane folded bias / eval-BatchNorm affine of the 4 output channels
+// j * 16 + (lane & 15) the lane writes: y = acc * alpha + beta.
+__device__ __forceinline__ void conv_affine(const ConvParams& p, int mdl, int co0, float (&alpha)[kFN],
+                                            float (&beta)[kFN]) {
+  const int fr = threadIdx.x & 15;
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) {
+    const int co = co0 + j * 16 + fr;
+    alpha[j] = 1.f;
+    beta[j] = 0.f;
+    if (co < p.co) {
+      const int64_t pi = static_cast<int64_t>(mdl) * p.co + co;
+      const float bv = p.bias ? ldp(p.bias, p.pdt, pi) : 0.f;
+      if (p.bn_mean) {
+        const float inv = 1.0f / sqrtf(ldp(p.bn_var, p.pdt, pi) + p.bn_eps);
+        alpha[j] = p.bn_w ? inv * ldp(p.bn_w, p.pdt, pi) : inv;
+        beta[j] = (p.bn_b ? ldp(p.bn_b, p.pdt, pi) : 0.f) - ldp(p.bn_mean, p.pdt, pi) * alpha[j];
+        beta[j] += bv * alpha[j];   // (acc + bias) * alpha + beta
+      } else {
+        beta[j] = bv;
+      }
+    }
+  }
+}
+
+template <typename T, int FM>
+__device__ __forceinline__ void conv_epilogue(const ConvParams& p, const f32x4 (&acc)[FM][kFN], T* xs, int mdl,
+                                              int bb, int ho0, int wo0, int co0, const float (&alpha)[kFN],
+                                              const float (&beta)[kFN]) {
+  constexpr int TPIX = 4 * FM * 16;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int fr = lane & 15;
+  // ---- epilogue 1: bias + folded BN, into LDS as [co][pixel] (type T) ----
+  constexpr int CPITCH = TPIX + 8;
+  T* cs = xs;  // reuse the input tile buffer
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) {
+    const int col = j * 16 + fr;          // output channel within the tile
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int px = wave * FM * 16 + i * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cs[col * CPITCH + px + e] = from_f32<T>(acc[i][j][e] * alpha[j] + beta[j]);
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue 2: residual + activation, coalesced NCHW stores ----
+  T* yb = static_cast<T*>(p.y) + mdl * p.y_sn + bb * p.y_sb;
+  const T* rb = p.res ? static_cast<const T*>(p.res) + mdl * p.r_sn + bb * p.r_sb : nullptr;
+  const int how = p.ho * p.wo;
+  constexpr int VE = 16 / sizeof(T);
+  if (p.vec_out) {
+    // tc % VE == 0, wo0 % VE == 0, rows of y / res 16-byte aligned; EB chunks per
+    // thread are handled together so their residual loads are in flight at once
+    constexpr int EB = 4;
+    const int chunks = 64 * (TPIX / VE);
+    for (int e0 = tid; e0 < chunks; e0 += EB * kConvThreads) {
+      int64_t off[EB];
+      int lds_at[EB];
+      uint4 rv[EB];
+#pragma unroll
+      for (int u = 0; u < EB; ++u) {
+        const int e = e0 + u * kConvThreads;
+        off[u] = -1;
+        if (e >= chunks) continue;
+        const int col = e / (TPIX / VE);
+        const int px = (e - col * (TPIX / VE)) * VE;
+        const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+        const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
+        if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
+        off[u] = static_cast<int64_t>(co) * how + oh * p.wo + ow;
+        lds_at[u] = col * CPITCH + px;
+        if (rb) rv[u] = *reinterpret_cast<const uint4*>(rb + off[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < EB; ++u) {
+        if (off[u] < 0) continue;
+        float v[VE];
+        const T* src = &cs[lds_at[u]];
+#pragma unroll
+        for (int q = 0; q < VE; ++q) v[q] = to_f32(src[q]);
+        if (rb) {
+          const T* rr = reinterpret_cast<const T*>(&rv[u]);
+#pragma unroll
+          for (int q = 0; q < VE; ++q) v[q] = to_f32(from_f32<T>(v[q] + to_f32(rr[q])));
+        }
+        uint4 ov;
+        T* oo = reinterpret_cast<T*>(&ov);
+#pragma unroll
+        for (int q = 0; q < VE; ++q) oo[q] = from_f32<T>(p.act == WC_ACT_RELU ? fmaxf(v[q], 0.f) : v[q]);
+        *reinterpret_cast<uint4*>(yb + off[u]) = ov;
+      }
+    }
+  } else {
+    for (int e = tid; e < 64 * TPIX; e += kConvThreads) {
+      const int col = e / TPIX;
+      const int px = e - col * TPIX;
+      const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+      const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
+      if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
+      const int64_t off = static_cast<int64_t>(co) * how + oh * p.wo + ow;
+      float v = to_f32(cs[col * CPITCH + px]);
+      if (rb) v = to_f32(from_f32<T>(v + to_f32(rb[off])));
+      if (p.act == WC_ACT_RELU) v = fmaxf(v, 0.f);
+      yb[off] = from_f32<T>(v);
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
   constexpr int FM = ConvTraits<T>::kFM;
@@ -227,96 +341,307 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
     }
   }
 
-  // ---- epilogue 1: bias + folded BN, into LDS as [co][pixel] (type T) ----
+  float alpha[kFN], beta[kFN];
+  conv_affine(p, mdl, co0, alpha, beta);
   __syncthreads();
-  constexpr int CPITCH = TPIX + 8;
-  T* cs = xs;  // reuse the input tile buffer
+  conv_epilogue<T, FM>(p, acc, xs, mdl, bb, ho0, wo0, co0, alpha, beta);
+}
+
+// ---------------------------------------------------------------------------
+// Fast path (bf16, stride 1, W % 8 == 0, at most kFastTaps taps): per
+// 32-channel chunk, BOTH operands are staged in LDS -- the input tile
+// [row][col][ci] and the packed weights [tap][co][ci] -- so the K loop is LDS
+// reads + MFMAs only.  The NCHW input is read as 16-byte vectors of 8 pixels
+// of one channel; a thread loads 8 channels x 8 pixels and transposes them in
+// registers into 8 pixel vectors of 8 channels (one 16-byte LDS store each).
+// Halo cells outside the image are zero-filled.  Two workgroups share a CU.
+// ---------------------------------------------------------------------------
+constexpr int kFastTaps = 9;
+constexpr int kFCC = 32;                // channels per chunk
+constexpr int kFPitch = kFCC + 8;       // LDS channel pitch (elements): 80 bytes
+
+// 8x8 transpose of bf16: in[q] = 8 pixels of channel q -> out[p] = 8 channels of pixel p
+// (component access only, so the arrays stay in registers)
+__device__ __forceinline__ uint32_t dword_of(const u32x4& v, int i) { return v[i]; }
+
+__device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
 #pragma unroll
-  for (int j = 0; j < kFN; ++j) {
-    const int col = j * 16 + fr;          // output channel within the tile
-    const int co = co0 + col;
-    float alpha = 1.f, beta = 0.f;
-    if (co < p.co) {
-      const int64_t pi = static_cast<int64_t>(mdl) * p.co + co;
-      const float bv = p.bias ? ldp(p.bias, p.pdt, pi) : 0.f;
+  for (int px = 0; px < 8; ++px) {
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = dword_of(in[2 * j], px >> 1), b = dword_of(in[2 * j + 1], px >> 1);
+      o[j] = (px & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+    }
+    out[px] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+template <typename PT>
+__device__ __forceinline__ float ldpt(const void* p, int64_t i) {
+  return to_f32(static_cast<const PT*>(p)[i]);
+}
+
+// Persistent form of the fast path.  One workgroup per CU walks a contiguous
+// range of work items (model, 64-channel output tile, image, pixel tile),
+// ordered so that neighbouring items share the model's weights.  Each item is
+// processed in stages of 32 input channels; a stage's operands (input tile
+// chunk [row][col][ci] and weight chunk [tap][co][ci]) live in one of two LDS
+// buffers, and the next stage's global loads are in flight during the current
+// stage's MFMAs.  The item's epilogue reuses the LDS buffer it just finished.
+struct Stage {
+  int mdl, bb, tco, ho0, wo0, c0;
+};
+
+// KT: compile-time tap count (0: runtime), so 3x3 convolutions get a fully
+// unrolled tap loop whose LDS reads are scheduled ahead of the MFMAs.
+template <typename PT, bool PERSIST, int KT>
+__global__ __launch_bounds__(kConvThreads, PERSIST ? 1 : 2) void conv_persist_kernel(ConvParams p, int per_wg,
+                                                                                   int extra) {
+  using T = bf16;
+  constexpr int FM = 4;                               // 64 pixels per wave
+  extern __shared__ float4 smem4[];
+  const int taps = KT ? KT : p.kh * p.kw;
+  const int in_elems = p.ir * p.ic * kFPitch;
+  const int stage_elems = in_elems + taps * 64 * kFPitch;
+  T* lds0 = reinterpret_cast<T*>(smem4);
+  T* trash = lds0 + (PERSIST ? 2 : 1) * stage_elems; // 16-byte sink for masked-off stores
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  const int nch = p.ci32 / kFCC;
+  const int tiles_img = p.tiles_r * p.tiles_c;
+  const int64_t plane = static_cast<int64_t>(p.h) * p.w;
+  int w = blockIdx.x;
+  if (!PERSIST && p.remap) w = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int i_begin = PERSIST ? w * per_wg + (w < extra ? w : extra) : w;
+  const int n_items = PERSIST ? per_wg + (w < extra ? 1 : 0) : 1;
+  const int S = n_items * nch;
+  const u32x4 z4 = u32x4{0u, 0u, 0u, 0u};
+
+  auto stage_of = [&](int s) {
+    Stage st;
+    const int item = i_begin + s / nch;
+    st.c0 = (s - (s / nch) * nch) * kFCC;
+    const int t = item % tiles_img;
+    int rest = item / tiles_img;
+    st.bb = rest % p.batch;
+    rest /= p.batch;
+    st.tco = rest % p.tiles_co;
+    st.mdl = rest / p.tiles_co;
+    const int trr = t / p.tiles_c;
+    st.ho0 = trr * p.tr;
+    st.wo0 = (t - trr * p.tiles_c) * p.tc;
+    return st;
+  };
+
+  // pixel offsets of this lane's A fragments within an input tile
+  int aoff[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int px = wave * FM * 16 + i * 16 + fr;
+    const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
+    aoff[i] = (pr < p.tr ? (pr * p.ic + pc) * kFPitch : 0) + fk;
+  }
+  // weight pieces of this thread: (co, tap, 8-channel group), fixed over stages
+  constexpr int kWPT = kFastTaps * 64 * (kFCC / 8) / kConvThreads;
+  const int wpieces = 64 * taps * (kFCC / 8);
+  int wco[kWPT], wtq[kWPT], wdst[kWPT];
+#pragma unroll
+  for (int q = 0; q < kWPT; ++q) {
+    const int e0 = tid + q * kConvThreads;
+    const int e = e0 < wpieces ? e0 : wpieces - 1;
+    wco[q] = e / (taps * 4);
+    wtq[q] = e - wco[q] * (taps * 4);                   // tap * 4 + channel group
+    wdst[q] = e0 < wpieces ? in_elems + ((wtq[q] >> 2) * 64 + wco[q]) * kFPitch + (wtq[q] & 3) * 8 : -1;
+  }
+
+  // ---- stage registers and their issue / commit ----
+  u32x4 wreg[kWPT], xreg[8];
+  struct XBlk { int cg, r, v; bool row_ok; } xb_cur;
+  auto xblock = [&](const Stage& st, int e, XBlk& blk, int& hic, int& vclamp, int& v0, int& nv) {
+    const int hi0 = st.ho0 - p.ph, wi0 = st.wo0 - p.pw;
+    const int c_lo = wi0 > 0 ? wi0 : 0;
+    const int c_hi = (wi0 + p.ic < p.w) ? wi0 + p.ic : p.w;
+    v0 = c_lo >> 3;
+    nv = c_hi > c_lo ? ((c_hi + 7) >> 3) - v0 : 0;
+    const int blocks = (kFCC / 8) * p.ir * nv;
+    const int ee = (e < blocks) ? e : 0;
+    blk.cg = nv ? ee / (p.ir * nv) : 0;
+    const int r2 = nv ? ee - blk.cg * (p.ir * nv) : 0;
+    blk.r = nv ? r2 / nv : 0;
+    blk.v = v0 + (nv ? r2 - blk.r * nv : 0);
+    const int hi = hi0 + blk.r;
+    blk.row_ok = e < blocks && hi >= 0 && hi < p.h;
+    hic = hi < 0 ? 0 : (hi >= p.h ? p.h - 1 : hi);
+    vclamp = blk.v * 8 + 8 <= p.w ? blk.v : (p.w >> 3) - 1;
+    return blocks;
+  };
+  auto issue = [&](const Stage& st) {
+    const T* wb = static_cast<const T*>(p.wp) + static_cast<int64_t>(st.mdl) * p.co * taps * p.ci32;
+    const int co0 = st.tco * 64;
+#pragma unroll
+    for (int q = 0; q < kWPT; ++q) {
+      const int co = co0 + wco[q] < p.co ? co0 + wco[q] : p.co - 1;
+      wreg[q] = *reinterpret_cast<const u32x4*>(wb + (static_cast<int64_t>(co) * taps + (wtq[q] >> 2)) * p.ci32 +
+                                                 st.c0 + (wtq[q] & 3) * 8);
+    }
+    int hic, vcl, v0, nv;
+    xblock(st, tid, xb_cur, hic, vcl, v0, nv);
+    const T* xbase = static_cast<const T*>(p.x) + st.mdl * p.x_sn + st.bb * p.x_sb;
+    const int ch0 = st.c0 + xb_cur.cg * 8;
+    const T* src = xbase + static_cast<int64_t>(hic) * p.w + vcl * 8;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int ch = ch0 + q < p.ci ? ch0 + q : p.ci - 1;
+      xreg[q] = *reinterpret_cast<const u32x4*>(src + ch * plane);
+    }
+  };
+  auto store_block = [&](T* buf, const Stage& st, int cg, int r, int v, bool row_ok, const u32x4 (&in)[8]) {
+    const int wi0 = st.wo0 - p.pw;
+    u32x4 out[8];
+    transpose8x8_bf16(in, out);
+#pragma unroll
+    for (int px = 0; px < 8; ++px) {
+      const int col = v * 8 + px - wi0;
+      const bool ok = row_ok && col >= 0 && col < p.ic;
+      T* dst = ok ? buf + (r * p.ic + col) * kFPitch + cg * 8 : trash;
+      *reinterpret_cast<u32x4*>(dst) = out[px];
+    }
+  };
+  auto commit = [&](T* buf, const Stage& st) {
+    const int co0 = st.tco * 64;
+#pragma unroll
+    for (int q = 0; q < kWPT; ++q) {
+      T* dst = wdst[q] >= 0 ? buf + wdst[q] : trash;
+      *reinterpret_cast<u32x4*>(dst) = (wdst[q] >= 0 && co0 + wco[q] < p.co) ? wreg[q] : z4;
+    }
+    int hic, vcl, v0, nv;
+    const int blocks = xblock(st, tid, xb_cur, hic, vcl, v0, nv);
+    {
+      const int ch0 = st.c0 + xb_cur.cg * 8;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (!(xb_cur.row_ok && ch0 + q < p.ci)) xreg[q] = z4;
+      store_block(buf, st, xb_cur.cg, xb_cur.r, xb_cur.v, xb_cur.row_ok, xreg);
+    }
+    // further rounds of input blocks (wide tiles only): load and store directly
+    const T* xbase = static_cast<const T*>(p.x) + st.mdl * p.x_sn + st.bb * p.x_sb;
+    for (int e = tid + kConvThreads; e < blocks; e += kConvThreads) {
+      XBlk blk;
+      int hic2, vcl2, v02, nv2;
+      xblock(st, e, blk, hic2, vcl2, v02, nv2);
+      const int ch0 = st.c0 + blk.cg * 8;
+      u32x4 in[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int ch = ch0 + q < p.ci ? ch0 + q : p.ci - 1;
+        const u32x4 t = *reinterpret_cast<const u32x4*>(xbase + ch * plane + static_cast<int64_t>(hic2) * p.w +
+                                                        vcl2 * 8);
+        in[q] = (blk.row_ok && ch0 + q < p.ci) ? t : z4;
+      }
+      store_block(buf, st, blk.cg, blk.r, blk.v, blk.row_ok, in);
+    }
+    // zero halo cells outside the image
+    const int hi0 = st.ho0 - p.ph, wi0 = st.wo0 - p.pw;
+    const int cells = p.ir * p.ic;
+    for (int e = tid; e < cells * (kFCC / 8); e += kConvThreads) {
+      const int cg = e / cells;
+      const int cell = e - cg * cells;
+      const int r = cell / p.ic, col = cell - (cell / p.ic) * p.ic;
+      const int hi = hi0 + r, wi = wi0 + col;
+      if (hi < 0 || hi >= p.h || wi < 0 || wi >= p.w)
+        *reinterpret_cast<u32x4*>(buf + cell * kFPitch + cg * 8) = z4;
+    }
+  };
+
+  // bias / BN parameters of an item, loaded with straight-line code
+  float pv[5][kFN];
+  auto load_params = [&](const Stage& st) {
+    const void* dummy = p.wp;
+    const void* ptrs[5] = {p.bias ? p.bias : dummy, p.bn_w ? p.bn_w : dummy, p.bn_b ? p.bn_b : dummy,
+                           p.bn_mean ? p.bn_mean : dummy, p.bn_var ? p.bn_var : dummy};
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) {
+      const int co = st.tco * 64 + j * 16 + fr;
+      const int64_t pi = static_cast<int64_t>(st.mdl) * p.co + (co < p.co ? co : p.co - 1);
+#pragma unroll
+      for (int k = 0; k < 5; ++k) pv[k][j] = ldpt<PT>(ptrs[k], pi);
+    }
+  };
+  auto fold_params = [&](float (&alpha)[kFN], float (&beta)[kFN]) {
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) {
+      const float bv = p.bias ? pv[0][j] : 0.f;
       if (p.bn_mean) {
-        const float inv = 1.0f / sqrtf(ldp(p.bn_var, p.pdt, pi) + p.bn_eps);
-        alpha = p.bn_w ? inv * ldp(p.bn_w, p.pdt, pi) : inv;
-        beta = (p.bn_b ? ldp(p.bn_b, p.pdt, pi) : 0.f) - ldp(p.bn_mean, p.pdt, pi) * alpha;
-        beta += bv * alpha;   // (acc + bias) * alpha + beta
+        const float inv = 1.0f / sqrtf(pv[4][j] + p.bn_eps);
+        alpha[j] = p.bn_w ? inv * pv[1][j] : inv;
+        beta[j] = (p.bn_b ? pv[2][j] : 0.f) - pv[3][j] * alpha[j] + bv * alpha[j];
       } else {
-        beta = bv;
+        alpha[j] = 1.f;
+        beta[j] = bv;
       }
     }
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int px = wave * FM * 16 + i * 16 + (lane >> 4) * 4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) cs[col * CPITCH + px + e] = from_f32<T>(acc[i][j][e] * alpha + beta);
-    }
+  };
+
+  f32x4 acc[FM][kFN];
+  if (S > 0) {
+    Stage cur = stage_of(0);
+    if (!PERSIST) load_params(cur);                   // one item: its parameters arrive with the first stage
+    issue(cur);
+    commit(lds0, cur);
   }
   __syncthreads();
-
-  // ---- epilogue 2: residual + activation, coalesced NCHW stores ----
-  T* yb = static_cast<T*>(p.y) + mdl * p.y_sn + bb * p.y_sb;
-  const T* rb = p.res ? static_cast<const T*>(p.res) + mdl * p.r_sn + bb * p.r_sb : nullptr;
-  const int how = p.ho * p.wo;
-  constexpr int VE = 16 / sizeof(T);
-  if (p.vec_out) {
-    // tc % VE == 0, wo0 % VE == 0, rows of y / res 16-byte aligned; EB chunks per
-    // thread are handled together so their residual loads are in flight at once
-    constexpr int EB = 4;
-    const int chunks = 64 * (TPIX / VE);
-    for (int e0 = tid; e0 < chunks; e0 += EB * kConvThreads) {
-      int64_t off[EB];
-      int lds_at[EB];
-      uint4 rv[EB];
+  for (int s = 0; s < S; ++s) {
+    const Stage cur = stage_of(s);
+    T* buf = lds0 + (PERSIST ? (s & 1) * stage_elems : 0);
+    const bool more = s + 1 < S;
+    const Stage nxt = stage_of(more ? s + 1 : s);
+    // (persistent) this item's bias / BN parameters: loaded every stage before
+    // the prefetch, so waiting for them never waits for the prefetch
+    if (PERSIST) load_params(cur);
+    issue(nxt);                                       // unconditional: see the fast kernel
+    if (cur.c0 == 0) {
 #pragma unroll
-      for (int u = 0; u < EB; ++u) {
-        const int e = e0 + u * kConvThreads;
-        off[u] = -1;
-        if (e >= chunks) continue;
-        const int col = e / (TPIX / VE);
-        const int px = (e - col * (TPIX / VE)) * VE;
-        const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
-        const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
-        if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
-        off[u] = static_cast<int64_t>(co) * how + oh * p.wo + ow;
-        lds_at[u] = col * CPITCH + px;
-        if (rb) rv[u] = *reinterpret_cast<const uint4*>(rb + off[u]);
-      }
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int u = 0; u < EB; ++u) {
-        if (off[u] < 0) continue;
-        float v[VE];
-        const T* src = &cs[lds_at[u]];
+        for (int j = 0; j < kFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // ---- K loop: taps x 32 channels, both operands from LDS ----
+    const T* wsm = buf + in_elems;
 #pragma unroll
-        for (int q = 0; q < VE; ++q) v[q] = to_f32(src[q]);
-        if (rb) {
-          const T* rr = reinterpret_cast<const T*>(&rv[u]);
+    for (int tap = 0; tap < (KT ? KT : taps); ++tap) {
+      const int r = tap / p.kw, sc = tap - (tap / p.kw) * p.kw;
+      const int toff = (r * p.dh * p.ic + sc * p.dw) * kFPitch;
+      const T* wt = wsm + tap * 64 * kFPitch + fr * kFPitch + fk;
+      bf16x8 bfr[kFN];
 #pragma unroll
-          for (int q = 0; q < VE; ++q) v[q] = to_f32(from_f32<T>(v[q] + to_f32(rr[q])));
-        }
-        uint4 ov;
-        T* oo = reinterpret_cast<T*>(&ov);
+      for (int j = 0; j < kFN; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(wt + j * 16 * kFPitch);
 #pragma unroll
-        for (int q = 0; q < VE; ++q) oo[q] = from_f32<T>(p.act == WC_ACT_RELU ? fmaxf(v[q], 0.f) : v[q]);
-        *reinterpret_cast<uint4*>(yb + off[u]) = ov;
+      for (int i = 0; i < FM; ++i) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(buf + aoff[i] + toff);
+#pragma unroll
+        for (int j = 0; j < kFN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfr[j], acc[i][j], 0, 0, 0);
       }
     }
-  } else {
-    for (int e = tid; e < 64 * TPIX; e += kConvThreads) {
-      const int col = e / TPIX;
-      const int px = e - col * TPIX;
-      const int pr = px / p.tc, pc = px - (px / p.tc) * p.tc;
-      const int co = co0 + col, oh = ho0 + pr, ow = wo0 + pc;
-      if (co >= p.co || pr >= p.tr || oh >= p.ho || ow >= p.wo) continue;
-      const int64_t off = static_cast<int64_t>(co) * how + oh * p.wo + ow;
-      float v = to_f32(cs[col * CPITCH + px]);
-      if (rb) v = to_f32(from_f32<T>(v + to_f32(rb[off])));
-      if (p.act == WC_ACT_RELU) v = fmaxf(v, 0.f);
-      yb[off] = from_f32<T>(v);
+    __syncthreads();                                  // everyone is done reading buf
+    if (PERSIST && cur.c0 + kFCC >= p.ci32) {
+      // last chunk of the item: epilogue through buf (it has an internal barrier)
+      float alpha[kFN], beta[kFN];
+      fold_params(alpha, beta);
+      conv_epilogue<T, FM>(p, acc, buf, cur.mdl, cur.bb, cur.ho0, cur.wo0, cur.tco * 64, alpha, beta);
     }
+    if (more) commit(lds0 + (PERSIST ? ((s + 1) & 1) * stage_elems : 0), nxt);
+    __syncthreads();
+  }
+  if (!PERSIST && S > 0) {
+    // single item: its epilogue runs after the last stage, through the stage buffer
+    const Stage cur = stage_of(S - 1);
+    float alpha[kFN], beta[kFN];
+    fold_params(alpha, beta);
+    conv_epilogue<T, FM>(p, acc, lds0, cur.mdl, cur.bb, cur.ho0, cur.wo0, cur.tco * 64, alpha, beta);
   }
 }
 
@@ -375,6 +700,28 @@ bool conv_plan(ConvParams& p) {
     } else {
       return false;
     }
+  }
+}
+
+// Tile plan of the fast kernel (256-pixel tiles, one LDS stage of 32
+// channels, ideally <= 80 KB so two workgroups share a CU); false if it does
+// not fit.
+bool conv_fast_plan(ConvParams& p) {
+  constexpr int TPIX = 256;
+  const int taps = p.kh * p.kw;
+  p.tc = p.wo < TPIX ? p.wo : TPIX;
+  p.tr = TPIX / p.tc;
+  if (p.tr > p.ho) p.tr = p.ho;
+  const size_t epi = static_cast<size_t>(64) * (TPIX + 8) * sizeof(bf16);
+  for (;;) {
+    p.ir = p.tr + (p.kh - 1) * p.dh;
+    p.ic = p.tc + (p.kw - 1) * p.dw;
+    const size_t stage = (static_cast<size_t>(p.ir) * p.ic + static_cast<size_t>(taps) * 64) * kFPitch * sizeof(bf16);
+    if (stage < epi) return false;                // the epilogue must fit in the stage buffer
+    if (stage + 16 <= 80 * 1024) return true;
+    if (p.tr > 1) p.tr = (p.tr + 1) / 2;
+    else if (p.tc > 64) p.tc = (p.tc + 1) / 2;
+    else return stage + 16 <= kConvLdsBudget;
   }
 }
 
@@ -485,8 +832,37 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   const size_t in = static_cast<size_t>(p.ir) * p.ic * (p.cc + (f32 ? 4 : 8)) * es;
   const size_t epi = static_cast<size_t>(64) * (4 * (f32 ? 4 : 8) * 16 + 8) * es;
   const size_t lds = in > epi ? in : epi;
-  const dim3 grid(static_cast<uint32_t>(nblk));
   hipStream_t st = as_stream(stream);
+  // fast path: weights and input chunk both staged in LDS (bf16, stride 1, W % 8 == 0)
+  if (!f32 && p.sh == 1 && p.sw == 1 && p.kh * p.kw <= kFastTaps && p.w % 8 == 0 && aligned(p.x, 16) &&
+      (p.x_sn * es) % 16 == 0 && (p.x_sb * es) % 16 == 0 && (static_cast<int64_t>(p.h) * p.w * es) % 16 == 0) {
+    ConvParams q = p;
+    if (conv_fast_plan(q)) {
+      q.tiles_r = static_cast<int>(cdiv(q.ho, q.tr));
+      q.tiles_c = static_cast<int>(cdiv(q.wo, q.tc));
+      q.vec_out = (yal && ral && q.tc % ve == 0 && q.wo % ve == 0) ? 1 : 0;
+      const int64_t fblk = static_cast<int64_t>(q.n) * q.batch * q.tiles_r * q.tiles_c * q.tiles_co;
+      WC_REQUIRE(fblk < 0x7fffffffll, WC_ERR_LIMIT, "wc_conv2d: too many tiles");
+      q.remap = (fblk % 8 == 0) ? 1 : 0;
+      // one item per workgroup, one LDS stage (two workgroups share a CU, so one
+      // workgroup's staging and epilogue overlap the other's MFMAs)
+      const size_t stage = (static_cast<size_t>(q.ir) * q.ic + static_cast<size_t>(q.kh) * q.kw * 64) * kFPitch * es;
+      const size_t flds = stage + 16;
+      const bool k9 = q.kh * q.kw == 9;
+      auto kern = q.pdt == WC_F32 ? (k9 ? conv_persist_kernel<float, false, 9> : conv_persist_kernel<float, false, 0>)
+                                  : (k9 ? conv_persist_kernel<bf16, false, 9> : conv_persist_kernel<bf16, false, 0>);
+      if (flds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(flds));
+        if (e != hipSuccess)
+          return set_error(static_cast<int32_t>(e), "wc_conv2d: LDS of %zu bytes refused: %s", flds,
+                           hipGetErrorString(e));
+      }
+      kern<<<dim3(static_cast<uint32_t>(fblk)), kConvThreads, flds, st>>>(q, 1, 0);
+      return check_launch("wc_conv2d");
+    }
+  }
+  const dim3 grid(static_cast<uint32_t>(nblk));
   if (f32) return launch_big_lds(conv_kernel<float>, p, grid, lds, st);
   return launch_big_lds(conv_kernel<bf16>, p, grid, lds, st);
 }
