@@ -21,6 +21,8 @@
 // channel-packed boundary layout, or [N,B,T,I] inputs) are read in place.
 #include "wc_gemm.h"
 
+#include <type_traits>
+
 namespace wc {
 
 
@@ -406,6 +408,341 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent XL bf16 kernel (bf16 output).  Requires K % 64 == 0, M, O and
+// both row decompositions' rows_inner % 16 == 0, 16-byte aligned output /
+// residual rows and per-model byte offsets below 2^31 (checked on the host).
+//
+// One workgroup per CU walks a list of 256 x 256 output tiles; the tiles of
+// one XCD (workgroup index % 8) form a contiguous range of the (model, column
+// tile, row tile) order, so the 32 CUs sharing an L2 work on neighbouring
+// tiles: the same activation rows and a few weight tiles.  4 waves in 2 x 2,
+// each 128 x 128 as 8 x 8 MFMA 16x16x32 tiles (one wave per SIMD, the 256
+// accumulators per lane in AGPRs).  MFMA roles are swapped with respect to C:
+// the A operand is a W row (o), the B operand an activation row (m), so a
+// lane's 4 accumulators are 4 consecutive output columns of one row, and the
+// bias is folded in by starting the accumulators at it.
+//
+// K advances in stages of 64 (128-byte row segments: whole cache lines)
+// through 2 LDS slots of 64 KB; the stage sequence runs on across tile
+// boundaries, so the next tile's operands load during the current tile's
+// last stage and epilogue.  Operands move global -> LDS with
+// global_load_lds_dwordx4: one instruction moves 8 rows x 128 bytes into a
+// contiguous 1 KB; the 16-byte chunk c of row r sits at position c ^ (r & 7),
+// so the 8 rows a fragment read serves per pass hit 8 distinct bank groups.
+// Fragments are double-buffered in registers per 32-wide half stage: the
+// second half's fragments are read during the first half's MFMAs, and the
+// next stage's first half during the second half's.  Past the last stage the
+// ring is fed copies of the last stage (into the free slot), so the stage
+// loop has no branches.  Barriers are bare s_barrier with explicit waits: a
+// workgroup fence would also wait for the loads in flight.
+//
+// Epilogue: stores and residual loads are buffer operations whose
+// out-of-range lanes the hardware drops, and the next tile's bias loads are
+// issued there too, so every wave issues a fixed number of memory
+// instructions per tile and the vmcnt waits stay exact.
+// ---------------------------------------------------------------------------
+constexpr int kXlB = 256, kXlBK = 64, kXlThreads = 256;
+constexpr int kXlHalf = kXlB * kXlBK * 2;                 // bytes of one operand per stage (32 KB)
+constexpr int kXlStageBytes = 2 * kXlHalf;                // 64 KB
+constexpr int kXlStripPitch = 128 * 2 + 16;               // bf16 epilogue strip row (bytes)
+constexpr int kXlStripBytes = 16 * kXlStripPitch;         // per wave
+constexpr uint32_t kXlOob = 0x80000000u;                  // buffer offset of a dropped lane
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(3))) char lds_char;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// VMEM instructions one wave issues per tile epilogue: 32 stores (+ 32 residual
+// loads) and the 8 bias loads of the next tile.
+template <bool RES>
+struct XlEpi {
+  static constexpr int value = 32 * (RES ? 2 : 1) + 8;
+};
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
+// expcnt 6:4 left at 7, lgkmcnt 11:8)
+template <int N>
+__device__ __forceinline__ void vm_lgkm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// Workgroup barrier without a memory fence: the caller has already waited
+// for what the other waves must see.  The empty asm statements keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void bare_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <typename TB, bool RES>
+__global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, int tiles_total) {
+  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 4 * kXlStripBytes];
+  lds_char* const smem = (lds_char*)smem_raw;        // keeps every LDS address 32-bit
+  constexpr int E = XlEpi<RES>::value;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int ow = (wave & 1) * 128, mw = (wave >> 1) * 128;
+  const int tiles_per_model = p.tiles_m * p.tiles_o;
+  const int KS = p.k / kXlBK;
+
+  // ---- this workgroup's tiles: XCD x = blockIdx % 8 owns a contiguous range ----
+  const int G = gridDim.x;
+  int t_first, t_step, my_tiles;
+  if ((G & 7) == 0) {
+    const int x = blockIdx.x & 7, l = blockIdx.x >> 3, nwx = G >> 3;
+    const int lo = static_cast<int>((static_cast<int64_t>(tiles_total) * x) >> 3);
+    const int hi = static_cast<int>((static_cast<int64_t>(tiles_total) * (x + 1)) >> 3);
+    t_first = lo + l;
+    t_step = nwx;
+    my_tiles = t_first < hi ? (hi - t_first + nwx - 1) / nwx : 0;
+  } else {
+    t_first = blockIdx.x;
+    t_step = G;
+    my_tiles = t_first < tiles_total ? (tiles_total - t_first + G - 1) / G : 0;
+  }
+  const int S = my_tiles * KS;
+  if (S == 0) return;
+
+  struct Tile { int mdl, m0, o0; };
+  auto tile_of = [&](int ti) {
+    Tile t;
+    const int g = t_first + ti * t_step;
+    t.mdl = static_cast<int>(fdiv(static_cast<uint32_t>(g), p.fd_tpm));
+    const int rem = g - t.mdl * tiles_per_model;
+    const int to = static_cast<int>(fdiv(static_cast<uint32_t>(rem), p.fd_tm));
+    t.m0 = (rem - to * p.tiles_m) * kXlB;
+    t.o0 = to * kXlB;
+    return t;
+  };
+
+  // ---- DMA of stage `stage` into slot stage & 1 (stages past the last reload it) ----
+  // Lane l of an 8-row block instruction writes LDS bytes [16 l, 16 l + 16): row
+  // l >> 3, position l & 7, which receives global chunk (l & 7) ^ (l >> 3).
+  const uint32_t dchunk = ((lane & 7) ^ (lane >> 3)) * 8;
+  const uint32_t wlane = ((lane >> 3) * static_cast<uint32_t>(p.k) + dchunk) * 2u;
+  const uint32_t alane = ((lane >> 3) * static_cast<uint32_t>(p.a_si) + dchunk) * 2u;
+  auto issue = [&](int stage) {
+    const int sidx = stage < S ? stage : S - 1;
+    const int ti = static_cast<int>(fdiv(static_cast<uint32_t>(sidx), p.fd_ks));
+    const int ks = sidx - ti * KS;
+    const Tile t = tile_of(ti);
+    const char* wmod = static_cast<const char*>(p.w) + static_cast<int64_t>(t.mdl) * p.w_sn * 2 + ks * 128;
+    const char* amod = static_cast<const char*>(p.a) + static_cast<int64_t>(t.mdl) * p.a_sn * 2 + ks * 128;
+    lds_char* st = smem + (stage & 1) * kXlStageBytes;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int rb = min(t.o0 + 64 * wave + 8 * q, p.o - 8);
+      __builtin_amdgcn_global_load_lds(wmod + static_cast<uint32_t>(rb) * static_cast<uint32_t>(p.k) * 2u + wlane,
+                                       (lds_ptr_t)(st + (64 * wave + 8 * q) * 128), 16, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int rb = min(t.m0 + 64 * wave + 8 * q, p.m - 8);
+      const uint32_t outer = fdiv(static_cast<uint32_t>(rb), p.a_ri);
+      const uint32_t inner = rb - outer * p.a_ri.d;
+      const uint32_t off = (outer * static_cast<uint32_t>(p.a_so) + inner * static_cast<uint32_t>(p.a_si)) * 2u;
+      __builtin_amdgcn_global_load_lds(amod + off + alane, (lds_ptr_t)(st + kXlHalf + (64 * wave + 8 * q) * 128),
+                                       16, 0, 0);
+    }
+  };
+
+  // fragment byte offsets: row = base + 16 * i + (lane & 15), chunk 4 * half + (lane >> 4)
+  const int fr = lane & 15;
+  const int fp0 = (((lane >> 4)) ^ (fr & 7)) << 4;
+  const int fp1 = ((4 + (lane >> 4)) ^ (fr & 7)) << 4;
+  const int wfo = (ow + fr) * 128, afo = kXlHalf + (mw + fr) * 128;
+  auto read_frags = [&](int stage, int fpos, bf16x8 (&wf)[8], bf16x8 (&af)[8]) {
+    const lds_char* st = smem + (stage & 1) * kXlStageBytes + fpos;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wf[i] = *(const lds_bf16x8*)(st + wfo + i * 2048);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) af[j] = *(const lds_bf16x8*)(st + afo + j * 2048);
+  };
+
+  // ---- bias of a tile, in accumulator layout: columns o0 + ow + 16 i + 4 (lane >> 4) + e ----
+  float bacc[8][4];
+  auto load_bias = [&](const Tile& t) {
+    const __amdgpu_buffer_rsrc_t brs =
+        xl_rsrc(p.bias ? static_cast<const TB*>(p.bias) + static_cast<int64_t>(t.mdl) * p.b_sn : p.c);
+    const int cb = t.o0 + ow + 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int col = cb + 16 * i;
+      const uint32_t boff = (p.bias && col < p.o) ? static_cast<uint32_t>(col) * sizeof(TB) : kXlOob;
+      if constexpr (sizeof(TB) == 4) {
+        const i32x4 b4 = __builtin_amdgcn_raw_buffer_load_b128(brs, boff, 0, 0);
+        const float* bt = reinterpret_cast<const float*>(&b4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bacc[i][e] = bt[e];
+      } else {
+        const i32x2 b2 = __builtin_amdgcn_raw_buffer_load_b64(brs, boff, 0, 0);
+        const bf16* bt = reinterpret_cast<const bf16*>(&b2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bacc[i][e] = to_f32(bt[e]);
+      }
+    }
+  };
+
+  f32x4 acc[8][8];
+  auto init_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{bacc[i][0], bacc[i][1], bacc[i][2], bacc[i][3]};
+  };
+
+  // ---- epilogue of tile t: acc (+residual, ReLU) -> C, one 16-row strip at a time
+  // through LDS, then 16-byte row chunks: lane -> row 4 q + (lane >> 4), 8 columns
+  // from 8 (lane & 15) ----
+  lds_char* strip = smem + 2 * kXlStageBytes + wave * kXlStripBytes;
+  auto epilogue = [&](const Tile& t) {
+    const __amdgpu_buffer_rsrc_t crs = xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn);
+    const __amdgpu_buffer_rsrc_t rrs =
+        xl_rsrc(RES ? static_cast<const bf16*>(p.r) + static_cast<int64_t>(t.mdl) * p.r_sn : p.c);
+    const bool relu = p.act == WC_ACT_RELU;
+    const int cc = lane & 15, rsub = lane >> 4;
+    const int col = t.o0 + ow + cc * 8;
+    const bool col_ok = col < p.o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        bf16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[i][j][e];
+          if (!RES && relu) v = relu_f(v);
+          o4[e] = from_f32<bf16>(v);
+        }
+        *(lds_bf16x4*)(strip + fr * kXlStripPitch + (16 * i + 4 * (lane >> 4)) * 2) = o4;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0): strip written
+      __builtin_amdgcn_wave_barrier();
+      // the strip's 16 rows share one row decomposition (rows_inner % 16 == 0)
+      const int row0 = t.m0 + mw + 16 * j;
+      const uint32_t outer = fdiv(static_cast<uint32_t>(row0), p.c_ri);
+      const uint32_t inner = row0 - outer * p.c_ri.d;
+      const bool strip_ok = row0 < p.m && col_ok;
+      const uint32_t cbase = (outer * static_cast<uint32_t>(p.c_so) + inner * static_cast<uint32_t>(p.c_si) + col) * 2u;
+      const uint32_t rbase = (outer * static_cast<uint32_t>(p.r_so) + inner * static_cast<uint32_t>(p.r_si) + col) * 2u;
+      i32x4 raw[4], rv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int lr = 4 * q + rsub;
+        raw[q] = *(const lds_i32x4*)(strip + lr * kXlStripPitch + cc * 16);
+        if constexpr (RES)
+          rv[q] = __builtin_amdgcn_raw_buffer_load_b128(
+              rrs, strip_ok ? rbase + static_cast<uint32_t>(lr * p.r_si) * 2u : kXlOob, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int lr = 4 * q + rsub;
+        i32x4 outv = raw[q];
+        if constexpr (RES) {
+          const bf16* a = reinterpret_cast<const bf16*>(&raw[q]);
+          const bf16* b = reinterpret_cast<const bf16*>(&rv[q]);
+          bf16* o = reinterpret_cast<bf16*>(&outv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float v = to_f32(a[e]) + to_f32(b[e]);
+            if (relu) v = relu_f(v);
+            o[e] = from_f32<bf16>(v);
+          }
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(
+            outv, crs, strip_ok ? cbase + static_cast<uint32_t>(lr * p.c_si) * 2u : kXlOob, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);          // strip reads done before it is rewritten
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+
+  // ---- prologue: stage 0 landed and its first half read, stage 1 in flight ----
+  issue(0);
+  load_bias(tile_of(0));
+  vm_lgkm_wait<0>();
+  bare_barrier();
+  issue(1);
+  bf16x8 w0[8], a0[8], w1[8], a1[8];
+  read_frags(0, fp0, w0, a0);
+  init_acc();
+
+  auto mfma_half = [&](bf16x8 (&wf)[8], bf16x8 (&af)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+  };
+  auto interleave = [&]() {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // one fragment read
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);     // four MFMAs
+    }
+  };
+  // stage s: first half's MFMAs with the second half's fragments read in between;
+  // wait for stage s + 1 (behind it only the epilogue of a tile that ended at
+  // s - 1), refill slot s & 1 with stage s + 2; second half's MFMAs with stage
+  // s + 1's first-half fragments read in between
+  auto step = [&](bool after_epi, int s) {
+    read_frags(s, fp1, w1, a1);
+    mfma_half(w0, a0);
+    interleave();
+    if (after_epi) vm_lgkm_wait<(E > 63 ? 63 : E)>();
+    else vm_lgkm_wait<0>();
+    bare_barrier();
+    issue(s + 2);
+    read_frags(s + 1, fp0, w0, a0);
+    mfma_half(w1, a1);
+    interleave();
+  };
+  for (int ti = 0; ti < my_tiles; ++ti) {
+    step(ti > 0, ti * KS);
+    for (int ks = 1; ks < KS; ++ks) step(false, ti * KS + ks);
+    epilogue(tile_of(ti));
+    load_bias(tile_of(ti + 1 < my_tiles ? ti + 1 : ti));
+    init_acc();
+  }
+}
+
+template <typename TB>
+int32_t launch_xl(GemmParams p, hipStream_t st) {
+  p.tiles_m = static_cast<int>(cdiv(p.m, kXlB));
+  p.tiles_o = static_cast<int>(cdiv(p.o, kXlB));
+  const int64_t tiles = static_cast<int64_t>(p.n) * p.tiles_m * p.tiles_o;
+  if (tiles >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_grouped_gemm: too many tiles");
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      return set_error(WC_ERR_ARG, "wc_grouped_gemm: cannot query the CU count");
+    cus = v;
+  }
+  const int grid = static_cast<int>(tiles < cus ? tiles : cus);
+  p.fd_ks = make_fastdiv(static_cast<uint32_t>(p.k / kXlBK));
+  p.fd_tpm = make_fastdiv(static_cast<uint32_t>(p.tiles_m * p.tiles_o));
+  p.fd_tm = make_fastdiv(static_cast<uint32_t>(p.tiles_m));
+  if (p.r)
+    gemm_xlp_kernel<TB, true><<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
+  else
+    gemm_xlp_kernel<TB, false><<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
+  return check_launch("wc_grouped_gemm");
+}
+
 template <typename TC, typename TB, int WM, int WN, int FM, int FN>
 int32_t launch_big(GemmParams p, hipStream_t st) {
   using C = BigCfg<WM, WN, FM, FN>;
@@ -442,10 +779,40 @@ int32_t launch_cfg(GemmParams p, bool vec, hipStream_t st) {
   return check_launch("wc_grouped_gemm");
 }
 
+// Shapes the persistent XL kernel takes: K a multiple of 64 (an even number of
+// 32-wide stages), M, O and both rows_inner multiples of 16 (a 16-row block
+// never straddles an outer row group), 16-byte aligned output / residual rows
+// and per-model byte offsets below 2^31 (32-bit DMA and buffer offsets).
+template <typename TC>
+bool xl_shape_ok(const GemmParams& p) {
+  const int64_t es = sizeof(TC);
+  if (p.k % 64 != 0 || p.m % 16 != 0 || p.o % 16 != 0 || p.a_ri.d % 16 != 0 || p.c_ri.d % 16 != 0) return false;
+  if (p.a_so < 0 || p.a_si < 0 || p.c_so < 0 || p.c_si < 0 || p.r_so < 0 || p.r_si < 0) return false;
+  const bool c_ok = common_vec_bytes({reinterpret_cast<uintptr_t>(p.c), static_cast<uint64_t>(p.c_sn * es),
+                                      static_cast<uint64_t>(p.c_so * es), static_cast<uint64_t>(p.c_si * es)}) >= 16;
+  const bool r_ok = !p.r || common_vec_bytes({reinterpret_cast<uintptr_t>(p.r), static_cast<uint64_t>(p.r_sn * es),
+                                              static_cast<uint64_t>(p.r_so * es),
+                                              static_cast<uint64_t>(p.r_si * es)}) >= 16;
+  if (!c_ok || !r_ok) return false;
+  const int64_t lim = 0x7fffffffll;
+  auto span = [&](int64_t so, int64_t si, int64_t ri, int64_t width) {
+    const int64_t outer = (p.m - 1) / ri;
+    const int64_t inner = p.m - 1 < ri ? p.m - 1 : ri - 1;
+    return outer * so + inner * si + width;
+  };
+  const int64_t a_end = span(p.a_so, p.a_si, p.a_ri.d, p.k) * 2;
+  const int64_t w_end = static_cast<int64_t>(p.o) * p.k * 2;
+  const int64_t c_end = span(p.c_so, p.c_si, p.c_ri.d, p.o) * es;
+  const int64_t r_end = p.r ? span(p.r_so, p.r_si, p.c_ri.d, p.o) * es : 0;
+  return a_end < lim && w_end < lim && c_end < lim && r_end < lim;
+}
+
 template <typename TA, typename TC, typename TB>
 int32_t launch_gemm_t(const GemmParams& p, bool vec, hipStream_t st) {
   if constexpr (sizeof(TA) == 2) {
     const int64_t tiles256 = static_cast<int64_t>(p.n) * cdiv(p.m, 256) * cdiv(p.o, 256);
+    if constexpr (sizeof(TC) == 2)
+      if (vec && tiles256 >= 256 && xl_shape_ok<TC>(p)) return launch_xl<TB>(p, st);
     if (vec && tiles256 >= 256) return launch_big<TC, TB, 2, 4, 8, 4>(p, st);
   }
   const int64_t tiles128 = static_cast<int64_t>(p.n) * cdiv(p.m, 128) * cdiv(p.o, 128);

@@ -25,6 +25,8 @@ struct GemmParams {
   void* c;
   int64_t c_sn, c_so, c_si;
   FastDiv c_ri;
+  // persistent XL kernel only: dividers of the stage -> tile -> (model, column tile) map
+  FastDiv fd_ks, fd_tpm, fd_tm;
 };
 
 // dtype: A/W element type; out_dtype: WC_F32 or dtype; bias_dtype: WC_F32 or dtype.

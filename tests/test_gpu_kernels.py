@@ -184,7 +184,8 @@ def test_linear(hip, dtype, n, batch, i, o, bias):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("m,o,k", [(300, 300, 264), (256, 260, 64), (257, 255, 72), (512, 256, 512)])
+@pytest.mark.parametrize("m,o,k", [(300, 300, 264), (256, 260, 64), (257, 255, 72), (512, 256, 512),
+                                   (300, 264, 128), (257, 520, 192)])
 @pytest.mark.parametrize("rows_inner", [None, 7])
 def test_grouped_gemm_large_tiles(hip, out_dtype, m, o, k, rows_inner):
     """bf16 problems big enough (>= 256 tiles of 256 x 256) for the large-tile kernel: ragged
