@@ -139,6 +139,105 @@ __global__ __launch_bounds__(kNormBlock) void bn_eval_kernel(
   LoadV<T, V>::st(yp, v);
 }
 
+// DPP lane permutation inside a 16-lane row (register-to-register)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF,
+                                                               0xF, true));
+}
+
+// Sum over groups of L adjacent lanes (L a power of two <= 64), delivered to
+// every lane of the group: DPP inside 16-lane rows, lane exchange beyond.
+template <int L>
+__device__ __forceinline__ float group_reduce(float v) {
+  if (L >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+  if (L >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+  if (L >= 8) v += dpp_f<0x141>(v);   // row_half_mirror
+  if (L >= 16) v += dpp_f<0x140>(v);  // row_mirror
+  if (L >= 32) v += __shfl_xor(v, 16, 64);
+  if (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// Vector LayerNorm: a group of L lanes owns RPG consecutive rows of one model
+// (rows_per_model % RPG == 0); lane j holds the 16-byte vectors (it * L + j)
+// of each row.  All RPG x ITEMS row loads are issued before any arithmetic, so
+// a wave keeps RPG x ITEMS x 1 KB in flight; gamma / beta are read once per
+// group as 16-byte vectors; two-pass statistics in fp32 registers; one
+// reciprocal square root per row.
+template <typename T, typename P, int L, int ITEMS, int RPG>
+__global__ __launch_bounds__(kNormBlock) void layernorm_vec_kernel(
+    const T* __restrict__ x, int64_t xms, int64_t xrs, const P* __restrict__ gamma,
+    const P* __restrict__ beta, T* __restrict__ y, int64_t yms, int64_t yrs, uint32_t rows_total,
+    FastDiv rows_per_model, int dim, float eps) {
+  constexpr int V = 16 / sizeof(T);
+  const int tid = threadIdx.x;
+  const int j = tid & (L - 1);
+  const uint32_t row0 = (blockIdx.x * (kNormBlock / L) + tid / L) * RPG;
+  if (row0 >= rows_total) return;  // whole lane groups leave together
+  const uint32_t m = fdiv(row0, rows_per_model);
+  const uint32_t r0 = row0 - m * rows_per_model.d;
+  const T* xr = x + static_cast<int64_t>(m) * xms + static_cast<int64_t>(r0) * xrs;
+  T* yr = y + static_cast<int64_t>(m) * yms + static_cast<int64_t>(r0) * yrs;
+
+  float v[RPG][ITEMS][V];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r)
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int e = (it * L + j) * V;
+      if (e < dim) LoadV<T, V>::ld(xr + static_cast<int64_t>(r) * xrs + e, v[r][it]);
+    }
+  float gv[ITEMS][V], bv[ITEMS][V];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * L + j) * V;
+    if (e < dim) {
+      const P* g = gamma + static_cast<int64_t>(m) * dim + e;
+      const P* b = beta ? beta + static_cast<int64_t>(m) * dim + e : nullptr;
+#pragma unroll
+      for (int q = 0; q < V; q += 16 / sizeof(P)) {
+        LoadV<P, 16 / sizeof(P)>::ld(g + q, &gv[it][q]);
+        if (b) LoadV<P, 16 / sizeof(P)>::ld(b + q, &bv[it][q]);
+        else
+#pragma unroll
+          for (int u = 0; u < static_cast<int>(16 / sizeof(P)); ++u) bv[it][q + u] = 0.f;
+      }
+    }
+  }
+  const float inv_d = 1.0f / static_cast<float>(dim);
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    float s = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it)
+      if ((it * L + j) * V < dim)
+#pragma unroll
+        for (int q = 0; q < V; ++q) s += v[r][it][q];
+    const float mean = group_reduce<L>(s) * inv_d;
+    float s2 = 0.f;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it)
+      if ((it * L + j) * V < dim)
+#pragma unroll
+        for (int q = 0; q < V; ++q) {
+          const float d = v[r][it][q] - mean;
+          s2 += d * d;
+        }
+    const float rstd = 1.0f / sqrtf(group_reduce<L>(s2) * inv_d + eps);
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int e = (it * L + j) * V;
+      if (e < dim) {
+        float o[V];
+#pragma unroll
+        for (int q = 0; q < V; ++q) o[q] = (v[r][it][q] - mean) * rstd * gv[it][q] + bv[it][q];
+        LoadV<T, V>::st(yr + static_cast<int64_t>(r) * yrs + e, o);
+      }
+    }
+  }
+}
+
 template <typename T, typename P, int V>
 int32_t launch_layernorm_v(const T* x, int64_t xms, int64_t xrs, const P* g, const P* b, T* y,
                            int64_t yms, int64_t yrs, int64_t n, int64_t rpm, int dim, float eps,
@@ -180,6 +279,29 @@ int32_t launch_layernorm(const void* x, int64_t xms, int64_t xrs, const void* g,
                                    static_cast<uint64_t>(yms * es), static_cast<uint64_t>(yrs * es),
                                    static_cast<uint64_t>(dim * sizeof(P))});
   const bool vec_ok = vb >= 16;
+  if (vec_ok && dim % VMAX == 0 && dim <= 4 * 64 * VMAX) {
+    const int64_t nvec = dim / VMAX;
+    const uint32_t rows_total = static_cast<uint32_t>(n * rpm);
+    const FastDiv fr = make_fastdiv(static_cast<uint32_t>(rpm));
+    const int rpg = (rpm % 4 == 0) ? 4 : ((rpm % 2 == 0) ? 2 : 1);
+    const T* xt = static_cast<const T*>(x);
+    const P* gt = static_cast<const P*>(g);
+    const P* bt = static_cast<const P*>(b);
+    T* yt = static_cast<T*>(y);
+#define WC_LNV(L, IT, R)                                                                                 \
+  if (nvec <= (L) * (IT) && rpg == (R)) {                                                              \
+    const int64_t groups = cdiv(rows_total, R);                                                       \
+    const dim3 grid(static_cast<uint32_t>(cdiv(groups, kNormBlock / (L))));                          \
+    layernorm_vec_kernel<T, P, L, IT, R><<<grid, kNormBlock, 0, st>>>(xt, xms, xrs, gt, bt, yt, yms, yrs, \
+                                                                      rows_total, fr, (int)dim, eps);  \
+    return check_launch("wc_layernorm");                                                              \
+  }
+#define WC_LNV_R(L, IT) WC_LNV(L, IT, 4) WC_LNV(L, IT, 2) WC_LNV(L, IT, 1)
+    WC_LNV_R(4, 1) WC_LNV_R(8, 1) WC_LNV_R(16, 1) WC_LNV_R(32, 1) WC_LNV_R(64, 1)
+    WC_LNV_R(64, 2) WC_LNV_R(64, 4)
+#undef WC_LNV_R
+#undef WC_LNV
+  }
   if (vec_ok && dim <= 16 * 64 * VMAX)
     return launch_layernorm_v<T, P, VMAX>(static_cast<const T*>(x), xms, xrs,
                                           static_cast<const P*>(g), static_cast<const P*>(b),

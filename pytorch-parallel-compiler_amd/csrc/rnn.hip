@@ -209,6 +209,14 @@ __global__ __launch_bounds__(rnn_bound(CELL == WC_CELL_GRU ? 3 : 4, UPG, KL)) vo
 
     for (int tt = 0; tt < nt; ++tt) {
       const int cur = (t0 + tt) & 1;
+      // this step's gates_x of the lane's unit, read before the dot products so
+      // its LDS latency is off the critical path (non-leaders read a valid slot)
+      float gxv[GATES];
+      {
+        const float* gxt = sgx + tt * G + (leader ? my_u : 0);
+#pragma unroll
+        for (int q = 0; q < GATES; ++q) gxv[q] = gxt[q * H];
+      }
       float hv[KL];
       const float* hs = sh_h + cur * HP + j * KLP;
 #pragma unroll
@@ -240,18 +248,17 @@ __global__ __launch_bounds__(rnn_bound(CELL == WC_CELL_GRU ? 3 : 4, UPG, KL)) vo
           for (int k = 1; k < UPG; ++k)
             if (j == k) g_h[q] = gh[k][q];
         }
-        const float* gxt = sgx + tt * G + my_u;   // gates_x = x W_ih^T + b_ih
-        float hnew;
+        float hnew;                                // gates_x = x W_ih^T + b_ih in gxv
         if (CELL == WC_CELL_GRU) {
-          const float rg = sigmoid_f(gxt[0] + g_h[0]);
-          const float zg = sigmoid_f(gxt[H] + g_h[1]);
-          const float nn = tanh_f(gxt[2 * H] + rg * g_h[2]);
+          const float rg = sigmoid_f(gxv[0] + g_h[0]);
+          const float zg = sigmoid_f(gxv[1] + g_h[1]);
+          const float nn = tanh_f(gxv[2] + rg * g_h[2]);
           hnew = (1.0f - zg) * nn + zg * h_reg;
         } else {
-          const float ig = sigmoid_f(gxt[0] + g_h[0]);
-          const float fg = sigmoid_f(gxt[H] + g_h[1]);
-          const float gg = tanh_f(gxt[2 * H] + g_h[2]);
-          const float og = sigmoid_f(gxt[3 * H] + g_h[3]);
+          const float ig = sigmoid_f(gxv[0] + g_h[0]);
+          const float fg = sigmoid_f(gxv[1] + g_h[1]);
+          const float gg = tanh_f(gxv[2] + g_h[2]);
+          const float og = sigmoid_f(gxv[3] + g_h[3]);
           c_reg = fg * c_reg + ig * gg;
           hnew = og * tanh_f(c_reg);
         }
