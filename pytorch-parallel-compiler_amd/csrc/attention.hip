@@ -193,13 +193,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
       const float m_new = fmaxf(m_run[nt], tmax);
       // rows with no valid key so far keep m = -inf; use 0 as the exponent base then
       const float base = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run[nt] - base);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[nt] - base);
       float tsum = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pv = exp2f(sacc[mt][nt][e] - base);
+          const float pv = __builtin_amdgcn_exp2f(sacc[mt][nt][e] - base);
           sacc[mt][nt][e] = pv;
           tsum += pv;
         }
@@ -272,6 +272,240 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
       for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc_o[dt][nt][e] * inv);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Resident-KV kernel (bf16, head dim 32 or 64, K and V of one head fit in LDS).
+// One workgroup per (model*batch, head, tile of W*64 queries).  K (row-major,
+// rows padded by 16 bytes) and V^T ([dh][key], rows padded by 8 bytes) of every
+// key are staged in LDS once, so the key loop has no barriers.  Each wave owns
+// 64 queries as two 32-query blocks and walks the keys in blocks of 32 with
+// v_mfma_f32_32x32x16_bf16:
+//   S^T = K Q^T      lane l holds query l%32 and 16 of the block's 32 keys
+//                    (keys 8 (r/4) + 4 (l/32) + r%4 in register r)
+//   softmax          block max in-lane over 16 keys, then across the lane
+//                    halves with v_permlane32_swap (no LDS); the running max
+//                    only moves when a block exceeds it by 2^8 (P <= 2^8 keeps
+//                    fp32 sums exact enough), so most blocks skip the rescale
+//   O^T += V^T P^T   P^T is the S^T register block itself: k-step j takes
+//                    registers 8j..8j+7, i.e. keys 16j + 8 (s/4) + 4 (l/32) + s%4,
+//                    and V^T is read from LDS in that key order (two 8-byte reads)
+// Scores are scaled by log2(e)/sqrt(Dh) inside the exp2 argument (one FMA).
+// ---------------------------------------------------------------------------
+constexpr float kLazyRescale = 8.0f;
+
+// (v of this lane, v of lane l ^ 32) via v_permlane32_swap on an opaque copy:
+// the compiler folds the intrinsic when both operands are the same value, so
+// the exchange is written out, with the wait states around the swap.
+__device__ __forceinline__ void half_swap(float v, float& mine, float& other) {
+  float a = v, b;
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "s_nop 1"
+      : "+v"(a), "=&v"(b));
+  // a = {v[0:31], v[0:31]}, b = {v[32:63], v[32:63]}
+  mine = v;
+  other = (threadIdx.x & 32) ? a : b;
+}
+__device__ __forceinline__ float other_half_max(float v) {
+  float m, o;
+  half_swap(v, m, o);
+  return fmaxf(m, o);
+}
+__device__ __forceinline__ float other_half_sum(float v) {
+  float m, o;
+  half_swap(v, m, o);
+  return m + o;
+}
+
+template <int DH>
+constexpr int res_kpitch() { return DH + 8; }      // K row pitch (bf16 elements)
+
+inline size_t res_lds_bytes(int dh, int skvp) {
+  return (static_cast<size_t>(skvp) * (dh + 8) + static_cast<size_t>(dh) * (skvp + 4)) * sizeof(bf16);
+}
+
+template <int DH, int W, bool CAUSAL>
+__global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp) {
+  constexpr int KP = res_kpitch<DH>();
+  constexpr int NKS = DH / 16;                       // 16-dim k-steps of S^T = K Q^T
+  constexpr int DT = DH / 32;                        // 32-row tiles of O^T
+  const int VTP = skvp + 4;                          // V^T row pitch (bf16 elements)
+  extern __shared__ float4 smem4[];
+  bf16* const ksm = reinterpret_cast<bf16*>(smem4);  // [skvp][KP]
+  bf16* const vts = ksm + static_cast<int64_t>(skvp) * KP;   // [DH][VTP]
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int qt = blockIdx.x % p.q_tiles;
+  const int bh = blockIdx.x / p.q_tiles;
+  const int nb = bh / p.heads, h = bh - (bh / p.heads) * p.heads;
+  const bf16* qb = static_cast<const bf16*>(p.q) + nb * p.q_sb + h * DH;
+  const bf16* kb = static_cast<const bf16*>(p.k) + nb * p.k_sb + h * DH;
+  const bf16* vb = static_cast<const bf16*>(p.v) + nb * p.v_sb + h * DH;
+  bf16* ob = static_cast<bf16*>(p.o) + nb * p.o_sb + h * DH;
+
+  // ---- stage K and V^T of all keys (keys >= skv read as zero) ----
+  {
+    constexpr int CPR = DH / 8;                      // 16-byte chunks per row
+    constexpr int U = 4;                             // chunks per thread in flight
+    const int total = skvp * CPR;
+    for (int e0 = tid; e0 < total; e0 += U * W * 64) {
+      uint4 kv[U], vv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * W * 64;
+        const int key = e / CPR, c = (e - (e / CPR) * CPR) * 8;
+        const bool ok = e < total && key < p.skv;
+        kv[u] = ok ? *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(key) * p.k_ss + c) : make_uint4(0, 0, 0, 0);
+        vv[u] = ok ? *reinterpret_cast<const uint4*>(vb + static_cast<int64_t>(key) * p.v_ss + c) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * W * 64;
+        if (e >= total) continue;
+        const int key = e / CPR, c = (e - (e / CPR) * CPR) * 8;
+        *reinterpret_cast<uint4*>(ksm + key * KP + c) = kv[u];
+        const bf16* v8 = reinterpret_cast<const bf16*>(&vv[u]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vts[(c + i) * VTP + key] = v8[i];
+      }
+    }
+  }
+
+  // ---- this wave's queries and their Q^T fragments (B operand of S^T) ----
+  const int q0 = qt * (W * 64) + wave * 64;
+  bf16x8 qf[2][NKS];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    int q = q0 + b * 32 + l32;
+    q = q < p.sq ? q : p.sq - 1;
+#pragma unroll
+    for (int k = 0; k < NKS; ++k)
+      qf[b][k] = *reinterpret_cast<const bf16x8*>(qb + static_cast<int64_t>(q) * p.q_ss + 16 * k + 8 * hf);
+  }
+  __syncthreads();
+
+  f32x16 oacc[2][DT];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[b][d][e] = 0.f;
+  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.f, 0.f};
+  const float c = p.scale_log2;
+  int nkb = skvp / 32;
+  if (CAUSAL) {
+    const int last = (q0 + 63 < p.sq ? q0 + 63 : p.sq - 1) / 32 + 1;
+    nkb = last < nkb ? last : nkb;
+  }
+  for (int kbk = 0; kbk < nkb; ++kbk) {
+    const int key0 = kbk * 32;
+    bf16x8 kf[NKS];
+#pragma unroll
+    for (int k = 0; k < NKS; ++k)
+      kf[k] = *reinterpret_cast<const bf16x8*>(ksm + (key0 + l32) * KP + 16 * k + 8 * hf);
+    bf16x8 vf[DT][2];
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const bf16* vr = vts + (d * 32 + l32) * VTP + key0 + 16 * j + 4 * hf;
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vf[d][j][e] = lo[e];
+          vf[d][j][4 + e] = hi[e];
+        }
+      }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      f32x16 s;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NKS; ++k) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qf[b][k], s, 0, 0, 0);
+      const int qlo = q0 + b * 32;
+      const bool full = key0 + 32 <= p.skv && (!CAUSAL || key0 + 31 <= qlo);
+      if (!full) {
+        const int q = qlo + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + (r >> 2) * 8 + 4 * hf + (r & 3);
+          if (key >= p.skv || (CAUSAL && key > q)) s[r] = -INFINITY;
+        }
+      }
+      float bm = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+      bm = other_half_max(bm) * c;
+      const bool up = bm > mrun[b] + kLazyRescale;
+      if (__builtin_amdgcn_ballot_w64(up)) {
+        const float mnew = up ? bm : mrun[b];
+        const float alpha = mnew == mrun[b] ? 1.0f : __builtin_amdgcn_exp2f(mrun[b] - mnew);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) oacc[b][d] *= alpha;
+        lrun[b] *= alpha;
+        mrun[b] = mnew;
+      }
+      const float base = mrun[b] == -INFINITY ? 0.f : mrun[b];
+      float psum = 0.f;
+      bf16x8 pf[2];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[r], c, -base));
+        psum += pv;
+        pf[r >> 3][r & 7] = static_cast<bf16>(pv);
+      }
+      lrun[b] += psum;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          oacc[b][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[d][j], pf[j], oacc[b][d], 0, 0, 0);
+    }
+  }
+
+  // ---- O = (O^T / l)^T: lane holds query l%32, dh rows 8 (r/4) + 4 (l/32) + r%4 (+32 d) ----
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const float lt = other_half_sum(lrun[b]);
+    const int q = q0 + b * 32 + l32;
+    if (q >= p.sq) continue;
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bf16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = from_f32<bf16>(oacc[b][d][4 * g4 + e] * inv);
+        *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(q) * p.o_ss + d * 32 + g4 * 8 + 4 * hf) = o4;
+      }
+  }
+}
+
+template <int DH, int W>
+int32_t launch_res(AttnParams p, int skvp, hipStream_t st) {
+  p.q_tiles = static_cast<int>(cdiv(p.sq, W * 64));
+  const int64_t blocks = static_cast<int64_t>(p.nb) * p.heads * p.q_tiles;
+  if (blocks >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_attention: too many tiles");
+  const size_t lds = res_lds_bytes(DH, skvp);
+  auto kernel = p.causal ? attn_res_kernel<DH, W, true> : attn_res_kernel<DH, W, false>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_attention: LDS of %zu bytes refused: %s", lds,
+                       hipGetErrorString(e));
+  }
+  kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(W * 64), lds, st>>>(p, skvp);
+  return check_launch("wc_attention");
 }
 
 template <typename T, int DH>
@@ -348,6 +582,17 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
   p.o = a->o;
   p.o_sb = a->o_stride_nb;
   p.o_ss = a->o_stride_s;
+  if (a->dtype == WC_BF16 && (a->head_dim == 32 || a->head_dim == 64)) {
+    // resident-KV kernel: K and V of one head in LDS, 8-byte aligned output rows
+    const int skvp = static_cast<int>(cdiv(a->skv, 32) * 32);
+    const bool o_al = aligned(a->o, 8) && (a->o_stride_nb * es) % 8 == 0 && (a->o_stride_s * es) % 8 == 0;
+    if (o_al && res_lds_bytes((int)a->head_dim, skvp) <= 150 * 1024) {
+      const bool w8 = a->sq > 256;
+      if (a->head_dim == 32)
+        return w8 ? launch_res<32, 8>(p, skvp, as_stream(stream)) : launch_res<32, 4>(p, skvp, as_stream(stream));
+      return w8 ? launch_res<64, 8>(p, skvp, as_stream(stream)) : launch_res<64, 4>(p, skvp, as_stream(stream));
+    }
+  }
   if (a->dtype == WC_BF16) return launch_attn<bf16>(p, (int)a->head_dim, as_stream(stream));
   return launch_attn<float>(p, (int)a->head_dim, as_stream(stream));
 }
