@@ -240,26 +240,23 @@ def cfg_attention(dev, steps, warmup) -> Dict:
         return max(errs)
 
     def roofline():
-        kv = torch.empty((n, b, s, 2 * d), device=dev, dtype=x.dtype)
-        q = torch.empty((n, b, s, d), device=dev, dtype=x.dtype)
-        o = torch.empty_like(q)
-        x.view(-1)  # contiguous input
-        attn = lambda: _hip.attention(q=q, k=kv, v=kv[..., d:], o=o, nb=n * b, heads=hh, sq=s, skv=s,  # noqa
-                                      head_dim=dh, q_strides=(s * d, d), k_strides=(s * 2 * d, 2 * d),
-                                      v_strides=(s * 2 * d, 2 * d), o_strides=(s * d, d), scale=dh ** -0.5,
-                                      causal=False)
+        qkv = torch.empty((n, b, s, 3 * d), device=dev, dtype=x.dtype)
+        o = torch.empty((n, b, s, d), device=dev, dtype=x.dtype)
+        wqkv, bqkv = wide._qkv_params()
+        st = (s * 3 * d, 3 * d)
+        attn = lambda: _hip.attention(q=qkv, k=qkv[..., d:], v=qkv[..., 2 * d:], o=o, nb=n * b, heads=hh,  # noqa
+                                      sq=s, skv=s, head_dim=dh, q_strides=st, k_strides=st, v_strides=st,
+                                      o_strides=(s * d, d), scale=dh ** -0.5, causal=False)
         with torch.inference_mode():
-            q.copy_(wide._project(x, wide.q_weight, d * d, wide.q_bias, d, d))
-            kv.copy_(wide._project(x, wide.kv_weight, 2 * d * d, wide.kv_bias, 2 * d, 2 * d))
+            qkv.copy_(wide._project(x, wqkv, 3 * d * d, bqkv, 3 * d, 3 * d))
         t_attn = _event_time(attn, steps, warmup)
-        t_kv = _event_time(lambda: wide._project(x, wide.kv_weight, 2 * d * d, wide.kv_bias, 2 * d, 2 * d),
-                           steps, warmup)
-        t_q = _event_time(lambda: wide._project(x, wide.q_weight, d * d, wide.q_bias, d, d), steps, warmup)
+        t_qkv = _event_time(lambda: wide._project(x, wqkv, 3 * d * d, bqkv, 3 * d, 3 * d), steps, warmup)
+        t_out = _event_time(lambda: wide._project(o, wide.out_weight, d * d, wide.out_bias, d, d), steps, warmup)
         flops = 4.0 * n * b * hh * s * s * dh
-        return {"bound": "mfma", "kernel": "attn_kernel (fused softmax(QK^T)V, bf16, head_dim 32)",
+        return {"bound": "mfma", "kernel": "attn_res_kernel (fused softmax(QK^T)V, bf16, head_dim 32, K/V resident "
+                                           "in LDS)",
                 "flops_per_launch": flops, "sec": t_attn, "peak": PEAK["bf16_mfma"],
-                "other_kernels_us": {"kv_projection_gemm": t_kv * 1e6, "q_projection_gemm": t_q * 1e6,
-                                     "out_projection_gemm": t_q * 1e6}}
+                "other_kernels_us": {"qkv_projection_gemm": t_qkv * 1e6, "out_projection_gemm": t_out * 1e6}}
 
     n_cpu = 1
     xs_cpu = x_cpu[:n_cpu].contiguous()

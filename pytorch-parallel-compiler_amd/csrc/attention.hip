@@ -19,6 +19,8 @@
 // Scores are scaled by log2(e)/sqrt(Dh) so the exponentials are v_exp_f32 (2^x).
 #include "wc_common.h"
 
+#include <type_traits>
+
 namespace wc {
 namespace {
 
@@ -403,7 +405,10 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
     const int last = (q0 + 63 < p.sq ? q0 + 63 : p.sq - 1) / 32 + 1;
     nkb = last < nkb ? last : nkb;
   }
-  for (int kbk = 0; kbk < nkb; ++kbk) {
+  // one 32-key block: both query blocks' scores first (their MFMA latency hides
+  // behind the first block's softmax), then per query block softmax and P V
+  auto key_block = [&](int kbk, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int key0 = kbk * 32;
     bf16x8 kf[NKS];
 #pragma unroll
@@ -423,26 +428,27 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
           vf[d][j][4 + e] = hi[e];
         }
       }
+    f32x16 s[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      f32x16 s;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[e] = 0.f;
+      for (int e = 0; e < 16; ++e) s[b][e] = 0.f;
 #pragma unroll
-      for (int k = 0; k < NKS; ++k) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qf[b][k], s, 0, 0, 0);
-      const int qlo = q0 + b * 32;
-      const bool full = key0 + 32 <= p.skv && (!CAUSAL || key0 + 31 <= qlo);
-      if (!full) {
-        const int q = qlo + l32;
+      for (int k = 0; k < NKS; ++k) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qf[b][k], s[b], 0, 0, 0);
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if constexpr (MASK) {
+        const int q = q0 + b * 32 + l32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = key0 + (r >> 2) * 8 + 4 * hf + (r & 3);
-          if (key >= p.skv || (CAUSAL && key > q)) s[r] = -INFINITY;
+          if (key >= p.skv || (CAUSAL && key > q)) s[b][r] = -INFINITY;
         }
       }
-      float bm = s[0];
+      float bm = fmaxf(s[b][0], s[b][1]);
 #pragma unroll
-      for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+      for (int r = 2; r < 16; ++r) bm = fmaxf(bm, s[b][r]);
       bm = other_half_max(bm) * c;
       const bool up = bm > mrun[b] + kLazyRescale;
       if (__builtin_amdgcn_ballot_w64(up)) {
@@ -458,7 +464,7 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
       bf16x8 pf[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(s[r], c, -base));
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[b][r], c, -base));
         psum += pv;
         pf[r >> 3][r & 7] = static_cast<bf16>(pv);
       }
@@ -469,6 +475,15 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
         for (int j = 0; j < 2; ++j)
           oacc[b][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[d][j], pf[j], oacc[b][d], 0, 0, 0);
     }
+  };
+  using masked = std::integral_constant<bool, true>;
+  using unmasked = std::integral_constant<bool, false>;
+  if (CAUSAL) {
+    for (int kbk = 0; kbk < nkb; ++kbk) key_block(kbk, masked{});
+  } else {
+    const int nfull = p.skv / 32;                    // blocks with 32 valid keys
+    for (int kbk = 0; kbk < nfull; ++kbk) key_block(kbk, unmasked{});
+    if (nfull < nkb) key_block(nfull, masked{});
   }
 
   // ---- O = (O^T / l)^T: lane holds query l%32, dh rows 8 (r/4) + 4 (l/32) + r%4 (+32 d) ----

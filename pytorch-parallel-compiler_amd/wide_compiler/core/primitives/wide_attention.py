@@ -88,6 +88,21 @@ class WideAttention(nn.Module):
         out = self._attend(query, key, value, attn_mask, is_causal)
         return (out, None) if mha_mode else out
 
+    def _qkv_params(self) -> Tuple[Tensor, Optional[Tensor]]:
+        """[q_weight; kv_weight] as one [N, 3D, D] weight (and [N, 3D] bias), rebuilt only when a
+        parameter changes (keyed by storage and version counter)."""
+        ps = (self.q_weight, self.kv_weight, self.q_bias, self.kv_bias)
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) if t is not None else None for t in ps)
+        cache = getattr(self, "_qkv_cache", None)
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                w = torch.cat([self.q_weight, self.kv_weight], dim=1).contiguous()
+                bias = None
+                if self.q_bias is not None:
+                    bias = torch.cat([self.q_bias, self.kv_bias], dim=1).contiguous()
+            self._qkv_cache = (key, w, bias)
+        return self._qkv_cache[1], self._qkv_cache[2]
+
     def _project(self, x: Tensor, w: Tensor, w_sn: int, bias: Optional[Tensor], b_sn: int, o: int) -> Tensor:
         """[N, B, T, D] @ W[n]^T + b -> [N, B, T, o] via the grouped GEMM (x read in place)."""
         from .._layout import rows_or_contiguous
@@ -123,6 +138,18 @@ class WideAttention(nn.Module):
         qw = self.q_weight if self.q_weight.is_contiguous() else self.q_weight.contiguous()
         ow = self.out_weight if self.out_weight.is_contiguous() else self.out_weight.contiguous()
         kvb = self.kv_bias
+        if query is key and key is value:
+            # self-attention: one GEMM over [q_weight; kv_weight] reads x once -> [N, B, T, 3D] = Q | K | V
+            wqkv, bqkv = self._qkv_params()
+            qkv = self._project(query, wqkv, 3 * d * d, bqkv, 3 * d, 3 * d)
+            q, k_t, v_t = qkv, qkv[..., d:], qkv[..., 2 * d:]
+            q_strides = k_strides = v_strides = (tq * 3 * d, 3 * d)
+            attn = torch.empty((n, b, tq, d), dtype=query.dtype, device=query.device)
+            if tq > 0:
+                _hip.attention(q=q, k=k_t, v=v_t, o=attn, nb=n * b, heads=hh, sq=tq, skv=tkv, head_dim=dh,
+                               q_strides=q_strides, k_strides=k_strides, v_strides=v_strides,
+                               o_strides=(tq * d, d), scale=dh ** -0.5, causal=is_causal)
+            return self._project(attn, ow, d * d, self.out_bias, d, d)
         q = self._project(query, qw, d * d, self.q_bias, d, d)
         if key is value:
             kv = self._project(key, kvw, 2 * d * d, kvb, 2 * d, 2 * d)       # [N, B, Tkv, 2D]: K | V
