@@ -645,6 +645,424 @@ __global__ __launch_bounds__(kConvThreads, PERSIST ? 1 : 2) void conv_persist_ke
   }
 }
 
+// ---------------------------------------------------------------------------
+// Resident-weight "same" convolution (bf16, stride 1, dilation 1, pad k/2,
+// C_in in {32, 64}, C_out % 64 == 0, width W with 256 / W output rows per
+// item).  A persistent workgroup (4 waves, one per SIMD) walks a contiguous
+// range of items (model, 64-channel output tile, image, row block):
+//  * the weights of the current (model, channel tile) stay in LDS as
+//    [tap][co][ci] and are reloaded only when the range crosses into the next
+//    model or channel tile;
+//  * the input tile (TR + KH - 1 rows x W + KW - 1 cols, channels-last) is
+//    double-buffered in LDS;
+//  * LDS rows are 16-byte chunks of 8 channels whose chunk index is XOR-
+//    swizzled by the pixel (or output channel) index, so the 16 lanes that
+//    read one MFMA fragment row hit 16 distinct bank groups without padding;
+//  * every LDS address of the K loop is a per-lane base plus a compile-time
+//    offset, and the fragments of K-step s + 1 are read during step s.
+// With one wave per SIMD a VALU-only phase would leave the MFMA unit idle, so
+// all other work of an item runs inside the 18 K-steps of the NEXT item's K
+// loop, between its MFMAs: step s < 16 finishes output tile s of the previous
+// item (bias, folded eval BatchNorm, residual, ReLU; one 8-byte store of 4
+// pixels) and issues the residual load that tile s of the current item will
+// need one item later; steps 16 and 17 transpose the next item's input
+// (loaded one item earlier) into the free LDS buffer and issue the loads of
+// the item after it.  Global accesses are buffer operations whose
+// out-of-range lanes the hardware drops (stores) or reads as zero (loads:
+// residual-free calls, rows outside the image, items past the range), so
+// every wave issues the same memory instructions in every item.
+// ---------------------------------------------------------------------------
+template <int KH, int KW, int CI, int W>
+struct ResConv {
+  static constexpr int TR = 256 / W;                 // output rows per item
+  static constexpr int IR = TR + KH - 1;             // staged input rows
+  static constexpr int IC = W + KW - 1;              // staged input cols (halo cols are zero)
+  static constexpr int PH = KH / 2, PW = KW / 2;
+  static constexpr int PXB = CI * 2;                 // bytes per staged pixel
+  static constexpr int NCH = CI / 8;                 // 16-byte chunks per pixel
+  static constexpr int PPB = 256 / PXB;              // pixels per 256-byte bank row
+  static constexpr int TAPS = KH * KW;
+  static constexpr int KS = CI / 32;                 // MFMA k-steps per tap
+  static constexpr int STEPS = TAPS * KS;
+  static constexpr int W_BYTES = TAPS * 64 * PXB;    // resident weights
+  static constexpr int IN_BYTES = IR * IC * PXB;     // one input buffer
+  static constexpr int LDS = W_BYTES + 2 * IN_BYTES;
+  static constexpr int VPR = W / 8;                  // 16-byte vectors per input row and channel
+  static constexpr int UNITS = NCH * IR * VPR;       // staging units (8 channels x 8 pixels)
+  static constexpr int UPT = (UNITS + 255) / 256;    // staging units per thread
+  static_assert(256 % W == 0 && W >= 16, "width");
+  static_assert(CI == 32 || CI == 64, "channels");
+  static_assert(LDS <= 160 * 1024, "LDS");
+  static constexpr int TASKS = 16 + UPT;             // deferred tasks per item (tiles, staging units)
+  __device__ static constexpr int swz(int chunk, int idx) { return chunk ^ ((idx / PPB) & (NCH - 1)); }
+};
+
+struct ResItem {
+  int mdl, tco, b, th;
+};
+
+constexpr uint32_t kResOob = 0x80000000u;            // buffer offset of a dropped / zero lane
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t res_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// 8x8 bf16 transpose with v_perm_b32: in[q] = 8 pixels of channel q -> out[x] =
+// 8 channels of pixel x
+__device__ __forceinline__ void transpose8x8_perm(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    const uint32_t sel = (x & 1) ? 0x07060302u : 0x05040100u;
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = __builtin_amdgcn_perm(in[2 * j + 1][x >> 1], in[2 * j][x >> 1], sel);
+    out[x] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+template <int KH, int KW, int CI, int W, typename PT>
+__global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_wg, int extra) {
+  using C = ResConv<KH, KW, CI, W>;
+  constexpr int TR = C::TR, IR = C::IR, IC = C::IC, PXB = C::PXB, NCH = C::NCH, TAPS = C::TAPS, KS = C::KS;
+  constexpr int STEPS = C::STEPS;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  char* const wlds = lds;                              // [tap][64 co][CI] swizzled
+  char* const ilds = lds + C::W_BYTES;                 // 2 x [IR][IC][CI] swizzled
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int fr = lane & 15, kq = lane >> 4;
+  const int th_n = (p.ho + TR - 1) / TR;
+  const int wg = blockIdx.x;
+  const int i_begin = wg * per_wg + (wg < extra ? wg : extra);
+  const int count = per_wg + (wg < extra ? 1 : 0);
+  if (count <= 0) return;
+  const u32x4 z4 = u32x4{0u, 0u, 0u, 0u};
+
+  auto decode = [&](int item) {
+    ResItem it;
+    it.th = item % th_n;
+    int r = item / th_n;
+    it.b = r % p.batch;
+    r /= p.batch;
+    it.tco = r % p.tiles_co;
+    it.mdl = r / p.tiles_co;
+    return it;
+  };
+  auto advance = [&](ResItem it) {
+    if (++it.th == th_n) {
+      it.th = 0;
+      if (++it.b == p.batch) {
+        it.b = 0;
+        if (++it.tco == p.tiles_co) {
+          it.tco = 0;
+          ++it.mdl;
+        }
+      }
+    }
+    return it;
+  };
+
+  // ---- zero the halo columns of both input buffers (never written again) ----
+  for (int e = tid; e < 2 * IR * (KW - 1) * NCH; e += 256) {
+    const int chunk = e % NCH;
+    int r = e / NCH;
+    const int hc = r % (KW - 1);
+    r /= (KW - 1);
+    const int row = r % IR, buf = r / IR;
+    const int col = hc < C::PW ? hc : W + hc;
+    *reinterpret_cast<u32x4*>(ilds + buf * C::IN_BYTES + (row * IC + col) * PXB + chunk * 16) = z4;
+  }
+
+  // ---- staging: NCHW 16-byte vectors -> registers -> channels-last LDS ----
+  // unit u = (channel group cg fastest, 16-byte column vector v, staged row ir)
+  uint32_t xoff[C::UPT][8];                            // byte offsets within an image (row 0 of the tile)
+  int xrow[C::UPT];
+  int xdst[C::UPT];                                    // LDS byte offset of pixel 0 of the unit's vector
+#pragma unroll
+  for (int k = 0; k < C::UPT; ++k) {
+    const int u = tid + k * 256;
+    const int cg = u % NCH, rest = u / NCH;
+    const int v = rest % C::VPR, ir = rest / C::VPR;
+    xrow[k] = u < C::UNITS ? ir : -0x40000000;         // never inside the image
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xoff[k][q] = static_cast<uint32_t>(((cg * 8 + q) * p.h) * W + v * 8) * 2u;
+    xdst[k] = (ir * IC + C::PW + v * 8) * PXB;
+    (void)cg;
+  }
+  u32x4 xr[C::UPT][8];
+  auto load_input = [&](const ResItem& it, bool valid) {
+    const __amdgpu_buffer_rsrc_t rs =
+        res_rsrc(static_cast<const bf16*>(p.x) + it.mdl * p.x_sn + it.b * p.x_sb);
+    const int r0 = it.th * TR - C::PH;
+#pragma unroll
+    for (int k = 0; k < C::UPT; ++k) {
+      const int row = r0 + xrow[k];
+      const bool ok = valid && row >= 0 && row < p.h;
+      const uint32_t roff = static_cast<uint32_t>(row * W) * 2u;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        xr[k][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? xoff[k][q] + roff : kResOob,
+                                                                                   0, 0));
+    }
+  };
+  auto store_unit = [&](int buf, int k) {
+    const int u = tid + k * 256;
+    if (k == 0 || u < C::UNITS) {                      // (only a partial last round branches)
+      const int cg = u % NCH;
+      u32x4 t[8];
+      transpose8x8_perm(xr[k], t);
+      char* base = ilds + buf * C::IN_BYTES + xdst[k];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const int col = C::PW + ((u / NCH) % C::VPR) * 8 + x;
+        *reinterpret_cast<u32x4*>(base + x * PXB + C::swz(cg, col) * 16) = t[x];
+      }
+    }
+  };
+
+  // ---- resident weights and the folded per-channel affine of the epilogue ----
+  auto load_weights = [&](const ResItem& it, float (&alpha)[kFN], float (&beta)[kFN]) {
+    const bf16* wb = static_cast<const bf16*>(p.wp) +
+                     (static_cast<int64_t>(it.mdl) * p.co + it.tco * 64) * TAPS * CI;
+    // 16-byte pieces, ordered (co, tap, chunk) as in global memory; all loads of a
+    // batch are issued before its LDS stores so their latencies overlap
+    constexpr int PIECES = TAPS * 64 * NCH;
+    constexpr int PPT = (PIECES + 255) / 256;
+    constexpr int BATCH = PPT > 10 ? (PPT + 1) / 2 : PPT;
+#pragma unroll
+    for (int q0 = 0; q0 < PPT; q0 += BATCH) {
+      u32x4 v[BATCH];
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        const int e = tid + (q0 + q) * 256;
+        v[q] = (q0 + q < PPT && e < PIECES) ? *reinterpret_cast<const u32x4*>(wb + static_cast<int64_t>(e) * 8) : z4;
+      }
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        const int e = tid + (q0 + q) * 256;
+        if (q0 + q < PPT && e < PIECES) {
+          const int chunk = e % NCH;
+          const int rest = e / NCH;
+          const int tap = rest % TAPS, co = rest / TAPS;
+          *reinterpret_cast<u32x4*>(wlds + (tap * 64 + co) * PXB + C::swz(chunk, co) * 16) = v[q];
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) {
+      const int64_t pi = static_cast<int64_t>(it.mdl) * p.co + it.tco * 64 + j * 16 + fr;
+      const float bv = p.bias ? ldpt<PT>(p.bias, pi) : 0.f;
+      if (p.bn_mean) {
+        const float inv = 1.0f / sqrtf(ldpt<PT>(p.bn_var, pi) + p.bn_eps);
+        alpha[j] = p.bn_w ? inv * ldpt<PT>(p.bn_w, pi) : inv;
+        beta[j] = (p.bn_b ? ldpt<PT>(p.bn_b, pi) : 0.f) - ldpt<PT>(p.bn_mean, pi) * alpha[j] + bv * alpha[j];
+      } else {
+        alpha[j] = 1.f;
+        beta[j] = bv;
+      }
+    }
+  };
+
+  // ---- per-lane LDS bases of the K loop ----
+  // A (input pixels): lane row fr of MFMA tile i is output pixel wave*64 + i*16 + fr
+  // of the item; tap (r, s) reads staged pixel (pr + r, pc + s).
+  const int px0 = wave * 64 + fr;
+  const int pr0 = px0 / W, pc0 = px0 % W;
+  int abase[KW][KS];
+#pragma unroll
+  for (int s = 0; s < KW; ++s)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      abase[s][ks] = C::W_BYTES + (pr0 * IC + pc0 + s) * PXB + C::swz(ks * 4 + kq, pc0 + s) * 16;
+  auto aoff_i = [](int i) { return ((i * 16) / W * IC + (i * 16) % W) * PXB; };
+  int bbase[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) bbase[ks] = fr * PXB + C::swz(ks * 4 + kq, fr) * 16;
+
+  // ---- output / residual byte offsets of this lane's 4-pixel runs, per tile (i, j) ----
+  const int how = p.ho * W;
+  uint32_t ooff[4][kFN];
+  int orow_i[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int px = wave * 64 + i * 16 + kq * 4;
+    orow_i[i] = px / W;
+#pragma unroll
+    for (int j = 0; j < kFN; ++j)
+      ooff[i][j] = static_cast<uint32_t>((j * 16 + fr) * how + (px / W) * W + px % W) * 2u;
+  }
+  const float relu_floor = p.act == WC_ACT_RELU ? 0.f : -__builtin_huge_valf();
+
+  struct Out {                                           // where an item's tiles go
+    __amdgpu_buffer_rsrc_t y, r;
+    uint32_t base;                                       // byte offset of (co0, row ho0)
+    int rows;                                            // valid output rows of the item (0: none)
+  };
+  auto out_of = [&](const ResItem& it, bool valid) {
+    Out o;
+    o.y = res_rsrc(static_cast<bf16*>(p.y) + it.mdl * p.y_sn + it.b * p.y_sb);
+    o.r = res_rsrc(p.res ? static_cast<const bf16*>(p.res) + it.mdl * p.r_sn + it.b * p.r_sb
+                         : static_cast<const bf16*>(p.y));
+    o.base = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
+    const int left = p.ho - it.th * TR;
+    o.rows = valid ? (left < TR ? left : TR) : 0;
+    return o;
+  };
+  const bool has_res = p.res != nullptr;
+
+  uint2 rv[4][kFN];                                    // residual runs (one item in flight)
+  // finish tile t = (i, j) of an item: affine, residual, ReLU, store
+  auto epi_tile = [&](const f32x4 (&acc)[4][kFN], const float (&alpha)[kFN], const float (&beta)[kFN],
+                      const Out& o, int t) {
+    const int i = t >> 2, j = t & 3;
+    uint32_t w2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t c = pack_bf16x2(acc[i][j][2 * h] * alpha[j] + beta[j], acc[i][j][2 * h + 1] * alpha[j] + beta[j]);
+      const uint32_t r = h ? rv[i][j].y : rv[i][j].x;
+      w2[h] = pack_bf16x2(fmaxf(bf16_lo(c) + bf16_lo(r), relu_floor), fmaxf(bf16_hi(c) + bf16_hi(r), relu_floor));
+    }
+    const bool ok = orow_i[i] < o.rows;
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, make_uint2(w2[0], w2[1])), o.y,
+                                          ok ? o.base + ooff[i][j] : kResOob, 0, 0);
+  };
+  auto res_load = [&](const Out& o, int t) {
+    const int i = t >> 2, j = t & 3;
+    const bool ok = has_res && orow_i[i] < o.rows;
+    rv[i][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(o.r, ok ? o.base + ooff[i][j] : kResOob,
+                                                                              0, 0));
+  };
+
+  auto lds_barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);                 // lgkmcnt(0): this wave's LDS writes landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // One item: the K loop over input buffer `buf` into acc (fresh), with the
+  // previous item's epilogue (accp, alpha_p, beta_p, op) and the staging of the
+  // next item interleaved; sets `nxt` / `nxt2` bookkeeping for the caller.
+  auto item = [&](int k, const ResItem& cur, const ResItem& nxt2, f32x4 (&acc)[4][kFN], const f32x4 (&accp)[4][kFN],
+                  const float (&alpha_p)[kFN], const float (&beta_p)[kFN], const Out& op, const Out& oc) {
+    const int boff = (k & 1) * C::IN_BYTES;
+    bf16x8 fa[2][4], fb[2][kFN];
+    auto frag_load = [&](int step, bf16x8 (&a)[4], bf16x8 (&b)[kFN]) {
+      const int tap = step / KS, ks = step % KS;
+      const int r = tap / KW, s = tap % KW;
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+        b[j] = *reinterpret_cast<const bf16x8*>(wlds + bbase[ks] + (tap * 64 + j * 16) * PXB);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[i] = *reinterpret_cast<const bf16x8*>(lds + abase[s][ks] + boff + r * IC * PXB + aoff_i(i));
+    };
+    frag_load(0, fa[0], fb[0]);
+#pragma unroll
+    for (int step = 0; step < STEPS; ++step) {
+      const int c = step & 1;
+      if (step + 1 < STEPS) frag_load(step + 1, fa[c ^ 1], fb[c ^ 1]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kFN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[c][i], fb[c][j],
+                                                               step == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
+                                                               0, 0, 0);
+      // this step's share of the deferred tasks
+#pragma unroll
+      for (int task = step * C::TASKS / STEPS; task < (step + 1) * C::TASKS / STEPS; ++task) {
+        if (task < 16) {
+          epi_tile(accp, alpha_p, beta_p, op, task);   // previous item, output tile `task`
+          res_load(oc, task);                          // residual of this item, tile `task`
+        } else {
+          store_unit((k + 1) & 1, task - 16);          // next item's input into the free buffer
+          if (task == C::TASKS - 1) load_input(nxt2, k + 2 < count);
+        }
+      }
+      // interleave: fragment reads and deferred VALU work between the MFMAs
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
+      }
+      __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);     // VMEM write
+      __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);     // VMEM read
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- prologue: item 0 staged in buffer 0, item 1 loaded into registers ----
+  f32x4 accA[4][kFN], accB[4][kFN];
+  float alA[kFN], beA[kFN], alB[kFN], beB[kFN];
+  ResItem cur = decode(i_begin);
+  load_input(cur, true);
+  store_unit(0, 0);
+#pragma unroll
+  for (int k = 1; k < C::UPT; ++k) store_unit(0, k);
+  load_weights(cur, alA, beA);
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) {
+    alB[j] = alA[j];
+    beB[j] = beA[j];
+  }
+  ResItem nxt = advance(cur);
+  load_input(nxt, count > 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kFN; ++j) accB[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  Out oprev = out_of(cur, false);                      // no item before the first
+  __syncthreads();
+
+  // After item k: barrier (LDS buffers), then the next item's weights if they change.
+  auto after = [&](int k, ResItem& c, ResItem& n, float (&al_n)[kFN], float (&be_n)[kFN], const float (&al_c)[kFN],
+                   const float (&be_c)[kFN]) {
+    lds_barrier();
+    if (k + 1 < count && (n.mdl != c.mdl || n.tco != c.tco)) {
+      load_weights(n, al_n, be_n);
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        al_n[j] = al_c[j];
+        be_n[j] = be_c[j];
+      }
+    }
+    c = n;
+    n = advance(n);
+  };
+
+  int k = 0;
+  for (; k + 1 < count; k += 2) {
+    {
+      const Out oc = out_of(cur, true);
+      item(k, cur, advance(nxt), accA, accB, alB, beB, oprev, oc);
+      oprev = oc;
+      after(k, cur, nxt, alB, beB, alA, beA);
+    }
+    {
+      const Out oc = out_of(cur, true);
+      item(k + 1, cur, advance(nxt), accB, accA, alA, beA, oprev, oc);
+      oprev = oc;
+      after(k + 1, cur, nxt, alA, beA, alB, beB);
+    }
+  }
+  if (k < count) {                                      // odd count: last item in A
+    const Out oc = out_of(cur, true);
+    item(k, cur, advance(nxt), accA, accB, alB, beB, oprev, oc);
+    oprev = oc;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) epi_tile(accA, alA, beA, oprev, t);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) epi_tile(accB, alB, beB, oprev, t);
+  }
+}
+
 // packed[i][co][r][s][c] = c < ci ? w[i*co_n + co][c][r][s] : 0
 template <typename T>
 __global__ __launch_bounds__(256) void conv_pack_kernel(const T* __restrict__ w, T* __restrict__ out,
@@ -723,6 +1141,47 @@ bool conv_fast_plan(ConvParams& p) {
     else if (p.tc > 64) p.tc = (p.tc + 1) / 2;
     else return stage + 16 <= kConvLdsBudget;
   }
+}
+
+template <int KH, int KW, int CI, int W, typename PT>
+int32_t conv_res_launch(ConvParams p, hipStream_t st) {
+  using C = ResConv<KH, KW, CI, W>;
+  const int64_t items = static_cast<int64_t>(p.n) * p.tiles_co * p.batch * cdiv(p.ho, C::TR);
+  if (items >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_conv2d: too many tiles");
+  const int cus = device_cu_count();
+  if (cus <= 0) return set_error(WC_ERR_ARG, "wc_conv2d: cannot query the CU count");
+  const int grid = static_cast<int>(items < cus ? items : cus);
+  const int per_wg = static_cast<int>(items / grid), extra = static_cast<int>(items % grid);
+  auto kern = conv_res_kernel<KH, KW, CI, W, PT>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+  if (e != hipSuccess)
+    return set_error(static_cast<int32_t>(e), "wc_conv2d: LDS of %d bytes refused: %s", C::LDS,
+                     hipGetErrorString(e));
+  kern<<<dim3(grid), dim3(256), C::LDS, st>>>(p, per_wg, extra);
+  return check_launch("wc_conv2d");
+}
+
+// Launches the resident-weight kernel when the geometry is one it is built
+// for; returns 1 (nothing launched) otherwise.
+int32_t conv_res_dispatch(ConvParams p, hipStream_t st) {
+  const bool same = p.sh == 1 && p.sw == 1 && p.dh == 1 && p.dw == 1 && p.ph == p.kh / 2 && p.pw == p.kw / 2 &&
+                    (p.kh % 2) == 1 && (p.kw % 2) == 1 && p.ho == p.h && p.wo == p.w;
+  if (!same || p.co % 64 != 0 || !(p.ci == 32 || p.ci == 64)) return 1;
+  // 16-byte input vectors, 8-byte output / residual vectors
+  if (!aligned(p.x, 16) || (p.x_sn % 8) || (p.x_sb % 8) || !aligned(p.y, 8) || (p.y_sn % 4) || (p.y_sb % 4) ||
+      !aligned(p.wp, 16))
+    return 1;
+  if (p.res && (!aligned(p.res, 8) || (p.r_sn % 4) || (p.r_sb % 4))) return 1;
+  p.tiles_co = p.co / 64;
+  const bool pf = p.pdt == WC_F32;
+#define WC_RES(KH, KW, CI, W)                                                                        \
+  if (p.kh == KH && p.kw == KW && p.ci == CI && p.w == W)                                         \
+    return pf ? conv_res_launch<KH, KW, CI, W, float>(p, st) : conv_res_launch<KH, KW, CI, W, bf16>(p, st);
+  WC_RES(3, 3, 64, 32) WC_RES(3, 3, 64, 16) WC_RES(3, 3, 32, 32) WC_RES(3, 3, 32, 64)
+  WC_RES(1, 3, 64, 256) WC_RES(1, 3, 32, 256)
+#undef WC_RES
+  return 1;
 }
 
 }  // namespace
@@ -833,6 +1292,11 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   const size_t epi = static_cast<size_t>(64) * (4 * (f32 ? 4 : 8) * 16 + 8) * es;
   const size_t lds = in > epi ? in : epi;
   hipStream_t st = as_stream(stream);
+  // resident-weight path: bf16 "same" convolution, stride 1, C_in 32 / 64, C_out % 64 == 0
+  if (!f32) {
+    const int32_t rc = conv_res_dispatch(p, st);
+    if (rc != 1) return rc;
+  }
   // fast path: weights and input chunk both staged in LDS (bf16, stride 1, W % 8 == 0)
   if (!f32 && p.sh == 1 && p.sw == 1 && p.kh * p.kw <= kFastTaps && p.w % 8 == 0 && aligned(p.x, 16) &&
       (p.x_sn * es) % 16 == 0 && (p.x_sb * es) % 16 == 0 && (static_cast<int64_t>(p.h) * p.w * es) % 16 == 0) {

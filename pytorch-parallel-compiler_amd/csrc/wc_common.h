@@ -6,6 +6,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <initializer_list>
+#include <type_traits>
 
 #include "wc_abi.h"
 
@@ -64,6 +65,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 template <typename T> __device__ __forceinline__ float to_f32(T v);
@@ -76,6 +79,17 @@ template <> __device__ __forceinline__ float from_f32<float>(float v) { return v
 // round-to-nearest-even, as torch's float -> bfloat16 / half casts
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return static_cast<bf16>(v); }
 template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return static_cast<f16>(v); }
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats -> two round-to-nearest-even bf16 in one dword (v_cvt_pk_bf16_f32), low half first
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+// the low / high bf16 of a dword as a float (exact)
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xffff0000u); }
 
 // wave64 reductions (all lanes receive the result)
 __device__ __forceinline__ float wave_sum(float v) {
@@ -112,6 +126,19 @@ inline FastDiv make_fastdiv(uint32_t d) {
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t x, const FastDiv& f) {
   return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(x, f.mul)) + x) >> f.shift);
+}
+
+// Compute units of the current device (cached per device id); 0 if the query fails.
+inline int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 0;
+    cache[dev] = v;
+  }
+  return cache[dev];
 }
 
 // Largest power-of-two byte width <= 16 dividing every given value.

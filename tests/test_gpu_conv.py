@@ -113,6 +113,57 @@ def test_conv_fused_bn_residual_relu(hip, dtype):
     assert rel_err(y, ref) <= tol(dtype)
 
 
+@pytest.mark.parametrize("n,b,ci,co,h,w,fused", [
+    (3, 2, 64, 64, 32, 32, False),     # one 64-channel tile, 8-row blocks
+    (5, 3, 64, 128, 20, 32, True),     # two channel tiles, partial last row block
+    (7, 2, 32, 64, 9, 64, True),       # C_in 32, 4-row blocks
+    (40, 4, 64, 64, 16, 16, True),     # more items than workgroups, model changes inside a range
+    (2, 1, 32, 64, 32, 32, False),
+])
+def test_conv2d_resident_weights(hip, n, b, ci, co, h, w, fused):
+    """bf16 "same" 3x3 convolutions on the resident-weight kernel, with and without the fused
+    BN + residual + ReLU epilogue."""
+    import wide_compiler as wc
+    g = gen(207)
+    torch.manual_seed(207)
+    dtype = torch.bfloat16
+    conv = wc.WideConv2d.from_modules([nn.Conv2d(ci, co, 3, padding=1) for _ in range(n)]).to(DEV, dtype)
+    x = _rand((n, b, ci, h, w), g, dtype)
+    d = lambda t: t.detach().cpu().double()  # noqa: E731
+    ref = wide_ref.conv2d(x.double(), d(conv.grouped_conv.weight), d(conv.grouped_conv.bias), n, padding=(1, 1))
+    kw = {}
+    if fused:
+        bn = wc.WideBatchNorm2d.from_modules(_bn_modules(n, co, 208)).to(DEV, dtype).eval()
+        conv.fused_bn = bn
+        conv.fused_activation = "relu"
+        r = _rand((n, b, co, h, w), g, dtype)
+        kw["residual"] = r.to(DEV)
+        op = bn.op
+        ref = wide_ref.batchnorm_eval(ref, d(op.weight), d(op.bias), d(op.running_mean), d(op.running_var), op.eps,
+                                      n)
+        ref = F.relu(ref + r.double())
+    with torch.no_grad():
+        y = conv(x.to(DEV), **kw).cpu()
+    assert rel_err(y, ref) <= TOL_BF16
+
+
+def test_conv1d_resident_weights(hip):
+    """Conv1d(64 -> 128, k=3, pad 1) over L=256: the 1x3 resident-weight kernel."""
+    import wide_compiler as wc
+    g = gen(209)
+    torch.manual_seed(209)
+    n = 6
+    mods = [nn.Conv1d(64, 128, 3, padding=1) for _ in range(n)]
+    wide = wc.WideConv1d.from_modules(mods).to(DEV, torch.bfloat16)
+    x = _rand((n, 4, 64, 256), g, torch.bfloat16)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    w, bias = wide._filters()
+    w = w.detach().cpu().reshape(n * 128, 64, 3)
+    exact = wide_ref.conv1d(x.double(), w.double(), bias.detach().cpu().double(), n, padding=1)
+    assert rel_err(y, exact) <= TOL_BF16
+
+
 class ResBlock(nn.Module):
     """cli.py:84-97."""
 
