@@ -648,29 +648,26 @@ __global__ __launch_bounds__(kConvThreads, PERSIST ? 1 : 2) void conv_persist_ke
 // ---------------------------------------------------------------------------
 // Resident-weight "same" convolution (bf16, stride 1, dilation 1, pad k/2,
 // C_in in {32, 64}, C_out % 64 == 0, width W with 256 / W output rows per
-// item).  A persistent workgroup (4 waves, one per SIMD) walks a contiguous
-// range of items (model, 64-channel output tile, image, row block):
+// item).  A persistent workgroup walks a contiguous range of items (model,
+// 64-channel output tile, image, row block):
 //  * the weights of the current (model, channel tile) stay in LDS as
 //    [tap][co][ci] and are reloaded only when the range crosses into the next
 //    model or channel tile;
-//  * the input tile (TR + KH - 1 rows x W + KW - 1 cols, channels-last) is
-//    double-buffered in LDS;
 //  * LDS rows are 16-byte chunks of 8 channels whose chunk index is XOR-
 //    swizzled by the pixel (or output channel) index, so the 16 lanes that
 //    read one MFMA fragment row hit 16 distinct bank groups without padding;
 //  * every LDS address of the K loop is a per-lane base plus a compile-time
 //    offset, and the fragments of K-step s + 1 are read during step s.
-// With one wave per SIMD a VALU-only phase would leave the MFMA unit idle, so
-// all other work of an item runs inside the 18 K-steps of the NEXT item's K
-// loop, between its MFMAs: step s < 16 finishes output tile s of the previous
-// item (bias, folded eval BatchNorm, residual, ReLU; one 8-byte store of 4
-// pixels) and issues the residual load that tile s of the current item will
-// need one item later; steps 16 and 17 transpose the next item's input
-// (loaded one item earlier) into the free LDS buffer and issue the loads of
-// the item after it.  Global accesses are buffer operations whose
+// Two groups of 4 waves (one wave of each group per SIMD) take alternate
+// items and alternate roles every phase: while one group runs the MFMA loop of
+// its item out of its own input buffer, the other finishes its previous item
+// (bias, folded eval BatchNorm, residual, ReLU; 8-byte stores of 4 pixels)
+// and stages its next item: NCHW 16-byte vectors loaded one phase earlier are
+// transposed 8x8 in registers into the channels-last swizzled layout.  So on
+// every SIMD one wave issues MFMAs while the other's VALU work and memory
+// waits overlap them.  Global accesses are buffer operations whose
 // out-of-range lanes the hardware drops (stores) or reads as zero (loads:
-// residual-free calls, rows outside the image, items past the range), so
-// every wave issues the same memory instructions in every item.
+// rows outside the image, items past the range).
 // ---------------------------------------------------------------------------
 template <int KH, int KW, int CI, int W>
 struct ResConv {
@@ -685,15 +682,15 @@ struct ResConv {
   static constexpr int KS = CI / 32;                 // MFMA k-steps per tap
   static constexpr int STEPS = TAPS * KS;
   static constexpr int W_BYTES = TAPS * 64 * PXB;    // resident weights
-  static constexpr int IN_BYTES = IR * IC * PXB;     // one input buffer
-  static constexpr int LDS = W_BYTES + 2 * IN_BYTES;
+  static constexpr int IN_BYTES = IR * IC * PXB;     // one input buffer (one per group)
+  static constexpr int PAR_BYTES = 64 * 2 * 4;       // folded (alpha, beta) of the 64 output channels
+  static constexpr int LDS = W_BYTES + 2 * IN_BYTES + PAR_BYTES;
   static constexpr int VPR = W / 8;                  // 16-byte vectors per input row and channel
   static constexpr int UNITS = NCH * IR * VPR;       // staging units (8 channels x 8 pixels)
-  static constexpr int UPT = (UNITS + 255) / 256;    // staging units per thread
+  static constexpr int UPT = (UNITS + 255) / 256;    // staging units per thread of a group
   static_assert(256 % W == 0 && W >= 16, "width");
   static_assert(CI == 32 || CI == 64, "channels");
   static_assert(LDS <= 160 * 1024, "LDS");
-  static constexpr int TASKS = 16 + UPT;             // deferred tasks per item (tiles, staging units)
   __device__ static constexpr int swz(int chunk, int idx) { return chunk ^ ((idx / PPB) & (NCH - 1)); }
 };
 
@@ -721,15 +718,19 @@ __device__ __forceinline__ void transpose8x8_perm(const u32x4 (&in)[8], u32x4 (&
 }
 
 template <int KH, int KW, int CI, int W, typename PT>
-__global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_wg, int extra) {
+__global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_wg, int extra) {
   using C = ResConv<KH, KW, CI, W>;
   constexpr int TR = C::TR, IR = C::IR, IC = C::IC, PXB = C::PXB, NCH = C::NCH, TAPS = C::TAPS, KS = C::KS;
   constexpr int STEPS = C::STEPS;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   char* const wlds = lds;                              // [tap][64 co][CI] swizzled
-  char* const ilds = lds + C::W_BYTES;                 // 2 x [IR][IC][CI] swizzled
+  char* const ilds = lds + C::W_BYTES;                 // 2 x [IR][IC][CI] swizzled, buffer g for group g
+  float* const plds = reinterpret_cast<float*>(lds + C::W_BYTES + 2 * C::IN_BYTES);   // [64][alpha, beta]
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wl = wave & 3;            // group, wave within the group
+  const int gtid = tid & 255;
   const int fr = lane & 15, kq = lane >> 4;
   const int th_n = (p.ho + TR - 1) / TR;
   const int wg = blockIdx.x;
@@ -738,8 +739,9 @@ __global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_
   if (count <= 0) return;
   const u32x4 z4 = u32x4{0u, 0u, 0u, 0u};
 
-  auto decode = [&](int item) {
+  auto decode = [&](int t) {                           // local item t of this workgroup
     ResItem it;
+    const int item = i_begin + t;
     it.th = item % th_n;
     int r = item / th_n;
     it.b = r % p.batch;
@@ -748,22 +750,9 @@ __global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_
     it.mdl = r / p.tiles_co;
     return it;
   };
-  auto advance = [&](ResItem it) {
-    if (++it.th == th_n) {
-      it.th = 0;
-      if (++it.b == p.batch) {
-        it.b = 0;
-        if (++it.tco == p.tiles_co) {
-          it.tco = 0;
-          ++it.mdl;
-        }
-      }
-    }
-    return it;
-  };
 
   // ---- zero the halo columns of both input buffers (never written again) ----
-  for (int e = tid; e < 2 * IR * (KW - 1) * NCH; e += 256) {
+  for (int e = tid; e < 2 * IR * (KW - 1) * NCH; e += 512) {
     const int chunk = e % NCH;
     int r = e / NCH;
     const int hc = r % (KW - 1);
@@ -775,22 +764,21 @@ __global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_
 
   // ---- staging: NCHW 16-byte vectors -> registers -> channels-last LDS ----
   // unit u = (channel group cg fastest, 16-byte column vector v, staged row ir)
-  uint32_t xoff[C::UPT][8];                            // byte offsets within an image (row 0 of the tile)
+  uint32_t xoff[C::UPT];                               // byte offset of (channel cg*8, row 0, vector v)
   int xrow[C::UPT];
-  int xdst[C::UPT];                                    // LDS byte offset of pixel 0 of the unit's vector
 #pragma unroll
   for (int k = 0; k < C::UPT; ++k) {
-    const int u = tid + k * 256;
+    const int u = gtid + k * 256;
     const int cg = u % NCH, rest = u / NCH;
     const int v = rest % C::VPR, ir = rest / C::VPR;
     xrow[k] = u < C::UNITS ? ir : -0x40000000;         // never inside the image
-#pragma unroll
-    for (int q = 0; q < 8; ++q) xoff[k][q] = static_cast<uint32_t>(((cg * 8 + q) * p.h) * W + v * 8) * 2u;
-    xdst[k] = (ir * IC + C::PW + v * 8) * PXB;
-    (void)cg;
+    xoff[k] = static_cast<uint32_t>((cg * 8 * p.h) * W + v * 8) * 2u;
   }
+  const uint32_t cstride = static_cast<uint32_t>(p.h * W) * 2u;   // channel plane bytes
   u32x4 xr[C::UPT][8];
-  auto load_input = [&](const ResItem& it, bool valid) {
+  auto load_input = [&](int t) {
+    const bool valid = t < count;
+    const ResItem it = decode(valid ? t : 0);
     const __amdgpu_buffer_rsrc_t rs =
         res_rsrc(static_cast<const bf16*>(p.x) + it.mdl * p.x_sn + it.b * p.x_sb);
     const int r0 = it.th * TR - C::PH;
@@ -798,139 +786,198 @@ __global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_
     for (int k = 0; k < C::UPT; ++k) {
       const int row = r0 + xrow[k];
       const bool ok = valid && row >= 0 && row < p.h;
-      const uint32_t roff = static_cast<uint32_t>(row * W) * 2u;
+      const uint32_t base = xoff[k] + static_cast<uint32_t>(row * W) * 2u;
 #pragma unroll
       for (int q = 0; q < 8; ++q)
-        xr[k][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? xoff[k][q] + roff : kResOob,
+        xr[k][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? base + q * cstride : kResOob,
                                                                                    0, 0));
     }
   };
-  auto store_unit = [&](int buf, int k) {
-    const int u = tid + k * 256;
-    if (k == 0 || u < C::UNITS) {                      // (only a partial last round branches)
-      const int cg = u % NCH;
-      u32x4 t[8];
-      transpose8x8_perm(xr[k], t);
-      char* base = ilds + buf * C::IN_BYTES + xdst[k];
+  auto store_input = [&]() {
+    char* base = ilds + grp * C::IN_BYTES;
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        const int col = C::PW + ((u / NCH) % C::VPR) * 8 + x;
-        *reinterpret_cast<u32x4*>(base + x * PXB + C::swz(cg, col) * 16) = t[x];
+    for (int k = 0; k < C::UPT; ++k) {
+      const int u = gtid + k * 256;
+      if (k == 0 || u < C::UNITS) {                    // (only a partial last round branches)
+        const int cg = u % NCH, rest = u / NCH;
+        const int v = rest % C::VPR, ir = rest / C::VPR;
+        u32x4 t[8];
+        transpose8x8_perm(xr[k], t);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          const int col = C::PW + v * 8 + x;
+          *reinterpret_cast<u32x4*>(base + (ir * IC + col) * PXB + C::swz(cg, col) * 16) = t[x];
+        }
       }
     }
   };
 
-  // ---- resident weights and the folded per-channel affine of the epilogue ----
-  auto load_weights = [&](const ResItem& it, float (&alpha)[kFN], float (&beta)[kFN]) {
+  // ---- resident weights (all 512 threads) ----
+  auto load_weights = [&](const ResItem& it) {
     const bf16* wb = static_cast<const bf16*>(p.wp) +
                      (static_cast<int64_t>(it.mdl) * p.co + it.tco * 64) * TAPS * CI;
-    // 16-byte pieces, ordered (co, tap, chunk) as in global memory; all loads of a
-    // batch are issued before its LDS stores so their latencies overlap
+    // 16-byte pieces, ordered (co, tap, chunk) as in global memory; all loads are
+    // issued before the LDS stores so their latencies overlap
     constexpr int PIECES = TAPS * 64 * NCH;
-    constexpr int PPT = (PIECES + 255) / 256;
-    constexpr int BATCH = PPT > 10 ? (PPT + 1) / 2 : PPT;
+    constexpr int PPT = (PIECES + 511) / 512;
+    u32x4 v[PPT];
 #pragma unroll
-    for (int q0 = 0; q0 < PPT; q0 += BATCH) {
-      u32x4 v[BATCH];
-#pragma unroll
-      for (int q = 0; q < BATCH; ++q) {
-        const int e = tid + (q0 + q) * 256;
-        v[q] = (q0 + q < PPT && e < PIECES) ? *reinterpret_cast<const u32x4*>(wb + static_cast<int64_t>(e) * 8) : z4;
-      }
-#pragma unroll
-      for (int q = 0; q < BATCH; ++q) {
-        const int e = tid + (q0 + q) * 256;
-        if (q0 + q < PPT && e < PIECES) {
-          const int chunk = e % NCH;
-          const int rest = e / NCH;
-          const int tap = rest % TAPS, co = rest / TAPS;
-          *reinterpret_cast<u32x4*>(wlds + (tap * 64 + co) * PXB + C::swz(chunk, co) * 16) = v[q];
-        }
-      }
+    for (int q = 0; q < PPT; ++q) {
+      const int e = tid + q * 512;
+      v[q] = e < PIECES ? *reinterpret_cast<const u32x4*>(wb + static_cast<int64_t>(e) * 8) : z4;
     }
 #pragma unroll
-    for (int j = 0; j < kFN; ++j) {
-      const int64_t pi = static_cast<int64_t>(it.mdl) * p.co + it.tco * 64 + j * 16 + fr;
+    for (int q = 0; q < PPT; ++q) {
+      const int e = tid + q * 512;
+      if (e < PIECES) {
+        const int chunk = e % NCH;
+        const int rest = e / NCH;
+        const int tap = rest % TAPS, co = rest / TAPS;
+        *reinterpret_cast<u32x4*>(wlds + (tap * 64 + co) * PXB + C::swz(chunk, co) * 16) = v[q];
+      }
+    }
+    // folded per-channel affine of the epilogue: y = acc * alpha + beta
+    if (tid < 64) {
+      const int64_t pi = static_cast<int64_t>(it.mdl) * p.co + it.tco * 64 + tid;
       const float bv = p.bias ? ldpt<PT>(p.bias, pi) : 0.f;
+      float a = 1.f, b = bv;
       if (p.bn_mean) {
         const float inv = 1.0f / sqrtf(ldpt<PT>(p.bn_var, pi) + p.bn_eps);
-        alpha[j] = p.bn_w ? inv * ldpt<PT>(p.bn_w, pi) : inv;
-        beta[j] = (p.bn_b ? ldpt<PT>(p.bn_b, pi) : 0.f) - ldpt<PT>(p.bn_mean, pi) * alpha[j] + bv * alpha[j];
-      } else {
-        alpha[j] = 1.f;
-        beta[j] = bv;
+        a = p.bn_w ? inv * ldpt<PT>(p.bn_w, pi) : inv;
+        b = (p.bn_b ? ldpt<PT>(p.bn_b, pi) : 0.f) - ldpt<PT>(p.bn_mean, pi) * a + bv * a;
       }
+      plds[2 * tid] = a;
+      plds[2 * tid + 1] = b;
     }
   };
 
   // ---- per-lane LDS bases of the K loop ----
-  // A (input pixels): lane row fr of MFMA tile i is output pixel wave*64 + i*16 + fr
+  // A (input pixels): lane row fr of MFMA tile i is output pixel wl*64 + i*16 + fr
   // of the item; tap (r, s) reads staged pixel (pr + r, pc + s).
-  const int px0 = wave * 64 + fr;
+  const int px0 = wl * 64 + fr;
   const int pr0 = px0 / W, pc0 = px0 % W;
   int abase[KW][KS];
 #pragma unroll
   for (int s = 0; s < KW; ++s)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      abase[s][ks] = C::W_BYTES + (pr0 * IC + pc0 + s) * PXB + C::swz(ks * 4 + kq, pc0 + s) * 16;
+      abase[s][ks] = C::W_BYTES + grp * C::IN_BYTES + (pr0 * IC + pc0 + s) * PXB + C::swz(ks * 4 + kq, pc0 + s) * 16;
   auto aoff_i = [](int i) { return ((i * 16) / W * IC + (i * 16) % W) * PXB; };
   int bbase[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) bbase[ks] = fr * PXB + C::swz(ks * 4 + kq, fr) * 16;
 
-  // ---- output / residual byte offsets of this lane's 4-pixel runs, per tile (i, j) ----
+  // ---- output / residual byte offsets: the lane's 4-pixel run of tile (i, j) starts
+  // at pixel wl*64 + i*16 + kq*4 of the item (row-major) and channel j*16 + fr:
+  // lane_off + 32 i (immediate) + 32 j how (scalar) ----
   const int how = p.ho * W;
-  uint32_t ooff[4][kFN];
-  int orow_i[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int px = wave * 64 + i * 16 + kq * 4;
-    orow_i[i] = px / W;
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-      ooff[i][j] = static_cast<uint32_t>((j * 16 + fr) * how + (px / W) * W + px % W) * 2u;
-  }
+  const uint32_t lane_off = static_cast<uint32_t>(fr * how + wl * 64 + kq * 4) * 2u;
+  auto orow = [&](int i) { return (wl * 64 + i * 16 + kq * 4) / W; };
   const float relu_floor = p.act == WC_ACT_RELU ? 0.f : -__builtin_huge_valf();
-
-  struct Out {                                           // where an item's tiles go
-    __amdgpu_buffer_rsrc_t y, r;
-    uint32_t base;                                       // byte offset of (co0, row ho0)
-    int rows;                                            // valid output rows of the item (0: none)
-  };
-  auto out_of = [&](const ResItem& it, bool valid) {
-    Out o;
-    o.y = res_rsrc(static_cast<bf16*>(p.y) + it.mdl * p.y_sn + it.b * p.y_sb);
-    o.r = res_rsrc(p.res ? static_cast<const bf16*>(p.res) + it.mdl * p.r_sn + it.b * p.r_sb
-                         : static_cast<const bf16*>(p.y));
-    o.base = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
-    const int left = p.ho - it.th * TR;
-    o.rows = valid ? (left < TR ? left : TR) : 0;
-    return o;
-  };
   const bool has_res = p.res != nullptr;
 
-  uint2 rv[4][kFN];                                    // residual runs (one item in flight)
-  // finish tile t = (i, j) of an item: affine, residual, ReLU, store
-  auto epi_tile = [&](const f32x4 (&acc)[4][kFN], const float (&alpha)[kFN], const float (&beta)[kFN],
-                      const Out& o, int t) {
-    const int i = t >> 2, j = t & 3;
-    uint32_t w2[2];
+  // ---- state of this group's item between its compute and finish phases ----
+  f32x4 acc[4][kFN];
+  float alpha[kFN], beta[kFN];
+  ResItem fin_it = {0, 0, 0, 0};
+
+  auto compute = [&](int t) {
+    const ResItem it = decode(t);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t c = pack_bf16x2(acc[i][j][2 * h] * alpha[j] + beta[j], acc[i][j][2 * h + 1] * alpha[j] + beta[j]);
-      const uint32_t r = h ? rv[i][j].y : rv[i][j].x;
-      w2[h] = pack_bf16x2(fmaxf(bf16_lo(c) + bf16_lo(r), relu_floor), fmaxf(bf16_hi(c) + bf16_hi(r), relu_floor));
+    for (int j = 0; j < kFN; ++j) {                     // this item's folded affine (LDS, loaded with the weights)
+      alpha[j] = plds[2 * (j * 16 + fr)];
+      beta[j] = plds[2 * (j * 16 + fr) + 1];
     }
-    const bool ok = orow_i[i] < o.rows;
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, make_uint2(w2[0], w2[1])), o.y,
-                                          ok ? o.base + ooff[i][j] : kResOob, 0, 0);
+    fin_it = it;
+    // K loop: taps x k-steps, both operands from LDS.  B fragments are double-
+    // buffered (step s + 1's are read at the start of step s); the A fragment of
+    // row tile i is re-read for step s + 1 right after its last MFMA of step s,
+    // 16 MFMAs ahead of its next use.
+    bf16x8 fa[4], fb[2][kFN];
+    auto b_load = [&](int step, bf16x8 (&b)[kFN]) {
+      const int tap = step / KS, ks = step % KS;
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+        b[j] = *reinterpret_cast<const bf16x8*>(wlds + bbase[ks] + (tap * 64 + j * 16) * PXB);
+    };
+    auto a_load = [&](int step, int i) {
+      const int tap = step / KS, ks = step % KS;
+      const int r = tap / KW, s = tap % KW;
+      fa[i] = *reinterpret_cast<const bf16x8*>(lds + abase[s][ks] + r * IC * PXB + aoff_i(i));
+    };
+    b_load(0, fb[0]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a_load(0, i);
+#pragma unroll
+    for (int step = 0; step < STEPS; ++step) {
+      const int c = step & 1;
+      if (step + 1 < STEPS) b_load(step + 1, fb[c ^ 1]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < kFN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[c][j],
+                                                               step == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
+                                                               0, 0, 0);
+        if (step + 1 < STEPS) a_load(step + 1, i);
+      }
+      if (step + 1 < STEPS) {
+        __builtin_amdgcn_sched_group_barrier(0x100, kFN, 0);   // next step's B fragments
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, kFN, 0); // row tile i's MFMAs
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // then its next A fragment
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  auto res_load = [&](const Out& o, int t) {
-    const int i = t >> 2, j = t & 3;
-    const bool ok = has_res && orow_i[i] < o.rows;
-    rv[i][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(o.r, ok ? o.base + ooff[i][j] : kResOob,
-                                                                              0, 0));
+
+  // Finish the group's last computed item: residual loads first (their latency
+  // overlaps the staging work in between), then affine + residual + ReLU + stores.
+  uint2 rv[2][kFN];                                     // residual runs of two row tiles
+  auto res_issue = [&](int i0) {
+    const ResItem& it = fin_it;
+    const __amdgpu_buffer_rsrc_t rrs =
+        res_rsrc(static_cast<const bf16*>(p.res) + it.mdl * p.r_sn + it.b * p.r_sb);
+    const uint32_t obase = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
+    const int left = p.ho - it.th * TR;
+    const int orows = left < TR ? left : TR;
+#pragma unroll
+    for (int i = i0; i < i0 + 2; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+        rv[i - i0][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                      rrs, orow(i) < orows ? lane_off + i * 32 : kResOob,
+                                                      obase + static_cast<uint32_t>(j * 32 * how), 0));
+  };
+  auto finish = [&](auto res, int i0) {
+    const ResItem& it = fin_it;
+    const __amdgpu_buffer_rsrc_t yrs = res_rsrc(static_cast<bf16*>(p.y) + it.mdl * p.y_sn + it.b * p.y_sb);
+    const uint32_t obase = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
+    const int left = p.ho - it.th * TR;
+    const int orows = left < TR ? left : TR;
+#pragma unroll
+    for (int i = i0; i < i0 + 2; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) {
+        uint32_t w2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float v0 = acc[i][j][2 * h] * alpha[j] + beta[j];
+          float v1 = acc[i][j][2 * h + 1] * alpha[j] + beta[j];
+          if constexpr (decltype(res)::value) {
+            const uint32_t c = pack_bf16x2(v0, v1);
+            const uint32_t r = h ? rv[i - i0][j].y : rv[i - i0][j].x;
+            v0 = bf16_lo(c) + bf16_lo(r);
+            v1 = bf16_hi(c) + bf16_hi(r);
+          }
+          w2[h] = pack_bf16x2(fmaxf(v0, relu_floor), fmaxf(v1, relu_floor));
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, make_uint2(w2[0], w2[1])), yrs,
+                                              orow(i) < orows ? lane_off + i * 32 : kResOob,
+                                              obase + static_cast<uint32_t>(j * 32 * how), 0);
+      }
   };
 
   auto lds_barrier = [&]() {
@@ -940,127 +987,56 @@ __global__ __launch_bounds__(256, 1) void conv_res_kernel(ConvParams p, int per_
     asm volatile("" ::: "memory");
   };
 
-  // One item: the K loop over input buffer `buf` into acc (fresh), with the
-  // previous item's epilogue (accp, alpha_p, beta_p, op) and the staging of the
-  // next item interleaved; sets `nxt` / `nxt2` bookkeeping for the caller.
-  auto item = [&](int k, const ResItem& cur, const ResItem& nxt2, f32x4 (&acc)[4][kFN], const f32x4 (&accp)[4][kFN],
-                  const float (&alpha_p)[kFN], const float (&beta_p)[kFN], const Out& op, const Out& oc) {
-    const int boff = (k & 1) * C::IN_BYTES;
-    bf16x8 fa[2][4], fb[2][kFN];
-    auto frag_load = [&](int step, bf16x8 (&a)[4], bf16x8 (&b)[kFN]) {
-      const int tap = step / KS, ks = step % KS;
-      const int r = tap / KW, s = tap % KW;
-#pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(wlds + bbase[ks] + (tap * 64 + j * 16) * PXB);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(lds + abase[s][ks] + boff + r * IC * PXB + aoff_i(i));
-    };
-    frag_load(0, fa[0], fb[0]);
-#pragma unroll
-    for (int step = 0; step < STEPS; ++step) {
-      const int c = step & 1;
-      if (step + 1 < STEPS) frag_load(step + 1, fa[c ^ 1], fb[c ^ 1]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kFN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[c][i], fb[c][j],
-                                                               step == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
-                                                               0, 0, 0);
-      // this step's share of the deferred tasks
-#pragma unroll
-      for (int task = step * C::TASKS / STEPS; task < (step + 1) * C::TASKS / STEPS; ++task) {
-        if (task < 16) {
-          epi_tile(accp, alpha_p, beta_p, op, task);   // previous item, output tile `task`
-          res_load(oc, task);                          // residual of this item, tile `task`
-        } else {
-          store_unit((k + 1) & 1, task - 16);          // next item's input into the free buffer
-          if (task == C::TASKS - 1) load_input(nxt2, k + 2 < count);
-        }
-      }
-      // interleave: fragment reads and deferred VALU work between the MFMAs
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
-      }
-      __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);     // VMEM write
-      __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);     // VMEM read
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  // ---- prologue: item 0 staged in buffer 0, item 1 loaded into registers ----
-  f32x4 accA[4][kFN], accB[4][kFN];
-  float alA[kFN], beA[kFN], alB[kFN], beB[kFN];
-  ResItem cur = decode(i_begin);
-  load_input(cur, true);
-  store_unit(0, 0);
-#pragma unroll
-  for (int k = 1; k < C::UPT; ++k) store_unit(0, k);
-  load_weights(cur, alA, beA);
-#pragma unroll
-  for (int j = 0; j < kFN; ++j) {
-    alB[j] = alA[j];
-    beB[j] = beA[j];
-  }
-  ResItem nxt = advance(cur);
-  load_input(nxt, count > 1);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < kFN; ++j) accB[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  Out oprev = out_of(cur, false);                      // no item before the first
-  __syncthreads();
-
-  // After item k: barrier (LDS buffers), then the next item's weights if they change.
-  auto after = [&](int k, ResItem& c, ResItem& n, float (&al_n)[kFN], float (&be_n)[kFN], const float (&al_c)[kFN],
-                   const float (&be_c)[kFN]) {
+  // Phases 0..count: in phase t group t & 1 computes item t while the other group
+  // finishes item t - 1 and stages item t + 1.  Each group runs its own straight
+  // sequence (compute, barrier, finish + stage, barrier, ...), group 1 one phase
+  // behind; both pass count + 1 barriers, and after each the weights of the
+  // next phase's item are loaded if they change.
+  int ph = 0;
+  auto phase_end = [&]() {
     lds_barrier();
-    if (k + 1 < count && (n.mdl != c.mdl || n.tco != c.tco)) {
-      load_weights(n, al_n, be_n);
-      __syncthreads();
-    } else {
-#pragma unroll
-      for (int j = 0; j < kFN; ++j) {
-        al_n[j] = al_c[j];
-        be_n[j] = be_c[j];
+    if (ph + 1 < count) {
+      const ResItem a = decode(ph), b = decode(ph + 1);
+      if (a.mdl != b.mdl || a.tco != b.tco) {
+        load_weights(b);
+        __syncthreads();
       }
     }
-    c = n;
-    n = advance(n);
+    ++ph;
   };
 
-  int k = 0;
-  for (; k + 1 < count; k += 2) {
-    {
-      const Out oc = out_of(cur, true);
-      item(k, cur, advance(nxt), accA, accB, alB, beB, oprev, oc);
-      oprev = oc;
-      after(k, cur, nxt, alB, beB, alA, beA);
-    }
-    {
-      const Out oc = out_of(cur, true);
-      item(k + 1, cur, advance(nxt), accB, accA, alA, beA, oprev, oc);
-      oprev = oc;
-      after(k + 1, cur, nxt, alA, beA, alB, beB);
-    }
+  // ---- prologue: group 0 stages item 0 ----
+  if (grp == 0) {
+    load_input(0);
+    store_input();
   }
-  if (k < count) {                                      // odd count: last item in A
-    const Out oc = out_of(cur, true);
-    item(k, cur, advance(nxt), accA, accB, alB, beB, oprev, oc);
-    oprev = oc;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) epi_tile(accA, alA, beA, oprev, t);
-  } else {
-#pragma unroll
-    for (int t = 0; t < 16; ++t) epi_tile(accB, alB, beB, oprev, t);
+  load_weights(decode(0));
+  __syncthreads();
+  if (grp == 1) {                                       // phase 0: stage item 1
+    if (1 < count) {
+      load_input(1);
+      store_input();
+    }
+    phase_end();
   }
+  for (int t = grp; t < count; t += 2) {
+    compute(t);                                         // phase t
+    phase_end();
+    // phase t + 1: residual and next-item loads in flight while item t is finished
+    if (has_res) res_issue(0);
+    if (t + 2 < count) load_input(t + 2);
+    if (has_res) {
+      finish(std::true_type{}, 0);
+      res_issue(2);
+      finish(std::true_type{}, 2);
+    } else {
+      finish(std::false_type{}, 0);
+      finish(std::false_type{}, 2);
+    }
+    if (t + 2 < count) store_input();
+    phase_end();
+  }
+  while (ph <= count) phase_end();
 }
 
 // packed[i][co][r][s][c] = c < ci ? w[i*co_n + co][c][r][s] : 0
@@ -1158,7 +1134,7 @@ int32_t conv_res_launch(ConvParams p, hipStream_t st) {
   if (e != hipSuccess)
     return set_error(static_cast<int32_t>(e), "wc_conv2d: LDS of %d bytes refused: %s", C::LDS,
                      hipGetErrorString(e));
-  kern<<<dim3(grid), dim3(256), C::LDS, st>>>(p, per_wg, extra);
+  kern<<<dim3(grid), dim3(512), C::LDS, st>>>(p, per_wg, extra);
   return check_launch("wc_conv2d");
 }
 
