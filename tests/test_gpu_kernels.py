@@ -252,6 +252,8 @@ def _per_step_err(out, exact):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n,b,t,i,h", [(32, 4, 32, 64, 128), (3, 2, 5, 8, 16), (5, 3, 9, 20, 40),
                                        (2, 1, 3, 130, 24), (4, 2, 6, 16, 64),
+                                       # fused projection: several 16-step chunks, partial last chunk
+                                       (3, 2, 37, 12, 64), (2, 3, 33, 64, 128),
                                        # streamed (one launch per step): W_hh beyond one workgroup
                                        (3, 5, 6, 24, 256), (2, 20, 4, 8, 288)])
 @pytest.mark.parametrize("with_h0", [False, True])
@@ -278,6 +280,7 @@ def test_gru(hip, dtype, n, b, t, i, h, with_h0):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n,b,t,i,h", [(32, 8, 32, 64, 128), (3, 2, 5, 8, 16), (2, 3, 7, 12, 100),
+                                       (2, 3, 21, 64, 32),   # fused projection, partial last chunk
                                        # streamed (one launch per step): W_hh beyond one workgroup
                                        (2, 18, 5, 16, 512), (3, 3, 4, 8, 320)])
 @pytest.mark.parametrize("with_state", [False, True])
