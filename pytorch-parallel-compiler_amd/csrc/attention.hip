@@ -446,9 +446,14 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
           if (key >= p.skv || (CAUSAL && key > q)) s[b][r] = -INFINITY;
         }
       }
-      float bm = fmaxf(s[b][0], s[b][1]);
-#pragma unroll
-      for (int r = 2; r < 16; ++r) bm = fmaxf(bm, s[b][r]);
+      // tree reductions keep the dependency chains short
+      const float m0 = __builtin_fmaxf(__builtin_fmaxf(s[b][0], s[b][1]), s[b][2]);
+      const float m1 = __builtin_fmaxf(__builtin_fmaxf(s[b][3], s[b][4]), s[b][5]);
+      const float m2 = __builtin_fmaxf(__builtin_fmaxf(s[b][6], s[b][7]), s[b][8]);
+      const float m3 = __builtin_fmaxf(__builtin_fmaxf(s[b][9], s[b][10]), s[b][11]);
+      const float m4 = __builtin_fmaxf(__builtin_fmaxf(s[b][12], s[b][13]), s[b][14]);
+      float bm = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(m0, m1), m2),
+                                 __builtin_fmaxf(__builtin_fmaxf(m3, m4), s[b][15]));
       bm = other_half_max(bm) * c;
       const bool up = bm > mrun[b] + kLazyRescale;
       if (__builtin_amdgcn_ballot_w64(up)) {
@@ -460,15 +465,18 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
         mrun[b] = mnew;
       }
       const float base = mrun[b] == -INFINITY ? 0.f : mrun[b];
-      float psum = 0.f;
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(s[b][r], c, -base));
       bf16x8 pf[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(s[b][r], c, -base));
-        psum += pv;
-        pf[r >> 3][r & 7] = static_cast<bf16>(pv);
-      }
-      lrun[b] += psum;
+      for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = static_cast<bf16>(pv[r]);
+      float ps[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) ps[r] = pv[2 * r] + pv[2 * r + 1];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ps[r] += ps[r + 4];
+      lrun[b] += (ps[0] + ps[2]) + (ps[1] + ps[3]);
 #pragma unroll
       for (int d = 0; d < DT; ++d)
 #pragma unroll
