@@ -153,8 +153,14 @@ def cfg_mlp(dev, steps, warmup) -> Dict:
                                          b2.double()))
 
     def roofline():
-        fc1 = wide.stages["fc1"]
         xn = packed.view(b, n, 64).movedim(1, 0)
+        fused = getattr(wide, "_mlp2", {}).get("fc2")
+        if fused is not None:
+            sec = _event_time(lambda: fused(xn), steps, warmup)
+            byts = 4.0 * (n * 128 * 64 + n * 128 + n * 64 * 128 + n * 64 + n * b * 64 + n * b * 64)
+            return {"bound": "hbm", "kernel": "mlp2_kernel (fc1 + bias + ReLU + fc2 + bias, fp32)",
+                    "bytes_per_launch": byts, "sec": sec, "peak": PEAK["hbm"]}
+        fc1 = wide.stages["fc1"]
         sec = _event_time(lambda: fc1(xn), steps, warmup)
         byts = 4.0 * (n * 128 * 64 + n * 128 + n * b * 64 + n * b * 128)
         return {"bound": "hbm", "kernel": "gemm_kernel (fc1 + bias + ReLU, fp32)", "bytes_per_launch": byts,

@@ -220,6 +220,40 @@ typedef struct wc_gemm_args {
 int32_t wc_grouped_gemm(const wc_gemm_args* args, void* stream);
 
 /*
+ * Two chained WideLinear stages in one launch -- replaces, for a traced
+ * Linear -> [ReLU] -> Linear chain, the two einsum + bias calls of
+ * WideLinear._forward_einsum (wide_compiler/core/primitives/wide_linear.py:
+ * 150-173) and the F.relu FunctionalOp between them that TracedWideModel runs
+ * (wide_compiler/core/traced_wide.py:174-211, 471-514):
+ *   h[i][m] = act1(x[i][m] W1[i]^T + b1[i]),  y[i][m] = act2(h[i][m] W2[i]^T + b2[i])
+ * with h rounded to `dtype` (as the first stage would store it) but never
+ * written to memory.  x / y rows use the two-level addressing of
+ * wc_gemm_args (row m = (m / rows_inner) * stride_outer + (m % rows_inner) *
+ * stride_inner within model i's block at stride_n).  W1 [n, hidden, in],
+ * W2 [n, out, hidden] contiguous; biases [n, hidden] / [n, out] or NULL; all of
+ * one element type.  Sizes must satisfy wc_mlp2_supported.
+ */
+typedef struct wc_mlp2_args {
+  int32_t dtype, act1, act2;
+  int64_t n, m, in_features, hidden, out_features;
+  const void* x;
+  int64_t x_stride_n, x_stride_outer, x_stride_inner, x_rows_inner;
+  const void* w1;
+  const void* b1;
+  const void* w2;
+  const void* b2;
+  void* y;
+  int64_t y_stride_n, y_stride_outer, y_stride_inner, y_rows_inner;
+} wc_mlp2_args;
+
+/* 1 if wc_mlp2 handles these sizes, else 0: in and hidden multiples of 32
+ * (fp32) or 64 (bf16), out a multiple of 16, hidden and out at most 256, and
+ * 32 rows of x and h plus W1 and W2 of one model within 160 KB of LDS. */
+int32_t wc_mlp2_supported(int32_t dtype, int64_t in_features, int64_t hidden, int64_t out_features);
+
+int32_t wc_mlp2(const wc_mlp2_args* args, void* stream);
+
+/*
  * Convolution weights packed for wc_conv2d: out[i, co, r, s, c] = w[i*c_out + co, c, r, s]
  * for c < c_in and 0 for c_in <= c < Ci32 (c_in rounded up to 32).  w is the grouped
  * filter bank [n*c_out, c_in, kh, kw] of WideConv2d.grouped_conv / WideConv1d.op

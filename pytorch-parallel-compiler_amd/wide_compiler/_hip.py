@@ -73,6 +73,19 @@ class _GemmArgs(ctypes.Structure):
     ]
 
 
+class _Mlp2Args(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("act1", ctypes.c_int32), ("act2", ctypes.c_int32),
+        ("n", ctypes.c_int64), ("m", ctypes.c_int64), ("in_features", ctypes.c_int64),
+        ("hidden", ctypes.c_int64), ("out_features", ctypes.c_int64),
+        ("x", ctypes.c_void_p), ("x_stride_n", ctypes.c_int64), ("x_stride_outer", ctypes.c_int64),
+        ("x_stride_inner", ctypes.c_int64), ("x_rows_inner", ctypes.c_int64),
+        ("w1", ctypes.c_void_p), ("b1", ctypes.c_void_p), ("w2", ctypes.c_void_p), ("b2", ctypes.c_void_p),
+        ("y", ctypes.c_void_p), ("y_stride_n", ctypes.c_int64), ("y_stride_outer", ctypes.c_int64),
+        ("y_stride_inner", ctypes.c_int64), ("y_rows_inner", ctypes.c_int64),
+    ]
+
+
 class _ConvArgs(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32), ("param_dtype", ctypes.c_int32), ("act", ctypes.c_int32),
@@ -122,6 +135,8 @@ SIGNATURES = {
     "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_recurrence": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_grouped_gemm": (_I32, [ctypes.POINTER(_GemmArgs), _P]),
+    "wc_mlp2_supported": (_I32, [_I32, _I64, _I64, _I64]),
+    "wc_mlp2": (_I32, [ctypes.POINTER(_Mlp2Args), _P]),
     "wc_conv_pack_weights": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P]),
     "wc_conv_packed_weight_elems": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "wc_conv2d": (_I32, [ctypes.POINTER(_ConvArgs), _P]),
@@ -257,6 +272,28 @@ def grouped_gemm(*, n: int, m: int, o: int, k: int,
     g.residual, g.r_stride_n, g.r_stride_outer, g.r_stride_inner = ptr(residual), r_sn, r_so, r_si
     g.c, g.c_stride_n, g.c_stride_outer, g.c_stride_inner, g.c_rows_inner = c.data_ptr(), c_sn, c_so, c_si, c_rows_inner
     _check(lib().wc_grouped_gemm(ctypes.byref(g), stream_of(a)), "wc_grouped_gemm")
+
+
+def mlp2_supported(dtype: torch.dtype, in_features: int, hidden: int, out_features: int) -> bool:
+    if dtype not in (torch.float32, torch.bfloat16):
+        return False
+    return bool(lib().wc_mlp2_supported(dtype_code(dtype, "mlp2"), in_features, hidden, out_features))
+
+
+def mlp2(*, n: int, m: int, in_features: int, hidden: int, out_features: int,
+         x: Tensor, x_sn: int, x_so: int, x_si: int, x_rows_inner: int,
+         w1: Tensor, b1: Optional[Tensor], w2: Tensor, b2: Optional[Tensor],
+         y: Tensor, y_sn: int, y_so: int, y_si: int, y_rows_inner: int,
+         relu1: bool, relu2: bool) -> None:
+    a = _Mlp2Args()
+    a.dtype = dtype_code(x.dtype, "mlp2")
+    a.act1 = ACT_RELU if relu1 else ACT_NONE
+    a.act2 = ACT_RELU if relu2 else ACT_NONE
+    a.n, a.m, a.in_features, a.hidden, a.out_features = n, m, in_features, hidden, out_features
+    a.x, a.x_stride_n, a.x_stride_outer, a.x_stride_inner, a.x_rows_inner = x.data_ptr(), x_sn, x_so, x_si, x_rows_inner
+    a.w1, a.b1, a.w2, a.b2 = w1.data_ptr(), ptr(b1), w2.data_ptr(), ptr(b2)
+    a.y, a.y_stride_n, a.y_stride_outer, a.y_stride_inner, a.y_rows_inner = y.data_ptr(), y_sn, y_so, y_si, y_rows_inner
+    _check(lib().wc_mlp2(ctypes.byref(a), stream_of(x)), "wc_mlp2")
 
 
 def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional[Tensor],

@@ -12,7 +12,7 @@ from .wide_conv2d import (
     STRATEGY_THRESHOLDS as CONV_THRESHOLDS,
 )
 from .wide_conv3d import WideConv3d, Conv3dStrategy
-from .wide_linear import WideLinear, LinearStrategy, select_linear_strategy, LINEAR_THRESHOLDS
+from .wide_linear import WideLinear, WideMLP2, LinearStrategy, select_linear_strategy, LINEAR_THRESHOLDS
 from .wide_batchnorm_1d import WideBatchNorm1d
 from .wide_batchnorm_2d import WideBatchNorm2d
 from .wide_layernorm import WideLayerNorm
@@ -26,7 +26,7 @@ from .wide_lstm import WideLSTM, LSTMStrategy
 __all__ = [
     "WideConv1d", "Conv1dStrategy", "WideConv2d", "ConvStrategy", "select_conv_strategy",
     "create_wide_conv2d", "CONV_THRESHOLDS", "WideConv3d", "Conv3dStrategy",
-    "WideLinear", "LinearStrategy", "select_linear_strategy", "LINEAR_THRESHOLDS",
+    "WideLinear", "WideMLP2", "LinearStrategy", "select_linear_strategy", "LINEAR_THRESHOLDS",
     "WideBatchNorm1d", "WideBatchNorm2d", "WideLayerNorm", "WideGroupNorm", "GroupNormStrategy",
     "WideInstanceNorm1d", "WideInstanceNorm2d", "InstanceNormStrategy",
     "WideEmbedding", "EmbeddingStrategy", "WideAttention", "AttentionStrategy",

@@ -138,4 +138,64 @@ class WideLinear(nn.Module):
                 f"strategy={self._strategy.value}{act})")
 
 
-__all__ = ["WideLinear", "LinearStrategy", "select_linear_strategy", "LINEAR_THRESHOLDS"]
+class WideMLP2(nn.Module):
+    """Two chained WideLinear stages (the first optionally followed by ReLU) run as one
+    wc_mlp2 launch; TracedWideModel builds it when it finds a Linear -> [ReLU] -> Linear
+    chain whose intermediate has no other consumer.  The hidden activations never reach
+    memory; they are rounded to the parameter dtype as the first stage would store them.
+    Parameters stay in the two WideLinear modules (state_dict keys unchanged)."""
+
+    def __init__(self, first: WideLinear, second: WideLinear, relu1: bool):
+        super().__init__()
+        self.first = first
+        self.second = second
+        self.relu1 = relu1
+        self.n = first.n
+        self.in_features = first.in_features
+        self.hidden = first.out_features
+        self.out_features = second.out_features
+        self.fused_activation: Optional[str] = None
+
+    @staticmethod
+    def supported(first: WideLinear, second: WideLinear) -> bool:
+        return (first.n == second.n and first.out_features == second.in_features and
+                first.weight.dtype == second.weight.dtype and
+                _hip.mlp2_supported(first.weight.dtype, first.in_features, first.out_features,
+                                    second.out_features))
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.forward_into(x, None, relu=self.fused_activation == "relu")
+
+    def forward_into(self, x: Tensor, out: Optional[Tensor], relu: bool = False) -> Tensor:
+        what = "WideMLP2"
+        if x.dim() < 2 or x.shape[0] != self.n or x.shape[-1] != self.in_features:
+            raise RuntimeError(f"{what}: expected input [N={self.n}, ..., {self.in_features}], got {list(x.shape)}")
+        params = (self.first.weight, self.first.bias, self.second.weight, self.second.bias)
+        _hip.require_device(what, x, *params)
+        _hip.require_forward_only(what, x, *params)
+        if x.dtype != self.first.weight.dtype:
+            raise RuntimeError(f"{what}: input dtype {x.dtype} != weight dtype {self.first.weight.dtype}")
+        x, r = rows_or_contiguous(x)
+        batch = tuple(x.shape[1:-1])
+        if out is None:
+            out = torch.empty((self.n, *batch, self.out_features), dtype=x.dtype, device=x.device)
+        cr = rows_of(out)
+        if cr is None or tuple(out.shape) != (self.n, *batch, self.out_features):
+            raise RuntimeError(f"{what}: output view {list(out.shape)} is not addressable")
+        if r.rows == 0:
+            return out
+        c = lambda t: None if t is None else (t if t.is_contiguous() else t.contiguous())  # noqa: E731
+        _hip.mlp2(n=self.n, m=r.rows, in_features=self.in_features, hidden=self.hidden,
+                  out_features=self.out_features,
+                  x=x, x_sn=r.stride_n, x_so=r.stride_outer, x_si=r.stride_inner, x_rows_inner=r.rows_inner,
+                  w1=c(self.first.weight), b1=c(self.first.bias), w2=c(self.second.weight), b2=c(self.second.bias),
+                  y=out, y_sn=cr.stride_n, y_so=cr.stride_outer, y_si=cr.stride_inner, y_rows_inner=cr.rows_inner,
+                  relu1=self.relu1, relu2=relu)
+        return out
+
+    def __repr__(self) -> str:
+        mid = " -> relu" if self.relu1 else ""
+        return f"WideMLP2({self.n}x[{self.in_features} -> {self.hidden}{mid} -> {self.out_features}])"
+
+
+__all__ = ["WideLinear", "LinearStrategy", "select_linear_strategy", "LINEAR_THRESHOLDS", "WideMLP2"]

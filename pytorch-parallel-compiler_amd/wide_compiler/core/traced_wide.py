@@ -36,6 +36,7 @@ from .ensemble_util import pack_inputs, unpack_outputs  # noqa: F401  (re-export
 from .primitives import (
     WideAttention, WideBatchNorm1d, WideBatchNorm2d, WideConv1d, WideConv2d, WideConv3d, WideEmbedding,
     WideGRU, WideGroupNorm, WideInstanceNorm1d, WideInstanceNorm2d, WideLayerNorm, WideLinear, WideLSTM,
+    WideMLP2,
 )
 from .registry import get_registry
 
@@ -178,6 +179,12 @@ class TracedWideModel(nn.Module):
         self._aliases: Dict[str, str] = {}
         self._residual_of: Dict[str, str] = {}
         self._relu_kind: Dict[str, str] = {}
+        # Linear -> [ReLU] -> Linear chains run as one wc_mlp2 launch: second stage -> runner
+        # (kept out of the module tree, so parameters and state_dict keys stay per stage),
+        # its chain input, and the first stages that are no longer run on their own
+        self._mlp2: Dict[str, WideMLP2] = {}
+        self._chain_input: Dict[str, str] = {}
+        self._skipped: Dict[str, str] = {}
 
     # ----------------------------------------------------------------------------------
     @classmethod
@@ -350,6 +357,42 @@ class TracedWideModel(nn.Module):
                         prod.fused_activation is None and sole_user(args[0], name):
                     prod.fused_activation = "relu"
                     self._aliases[name] = args[0]
+        self._fuse_linear_chains(users)
+
+    def _fuse_linear_chains(self, users: Dict[str, List[str]]) -> None:
+        """WideLinear B fed only by WideLinear A (through at most A's folded ReLU) -> one
+        wc_mlp2 launch, when the fused kernel supports the sizes."""
+        def consumers(src: str) -> List[str]:
+            out: List[str] = []
+            for u in users.get(src, []):
+                if u in self._aliases and self._resolve(u) == src:
+                    out.extend(consumers(u))
+                else:
+                    out.append(u)
+            return out
+
+        for name in self._execution_order:
+            if name not in self.stage_info or name in self._aliases or name in self._skipped:
+                continue
+            op = self._op(name)
+            args = self._node_args[name]
+            if not isinstance(op, WideLinear) or len(args) != 1 or not isinstance(args[0], str) or \
+                    self._node_kwargs[name]:
+                continue
+            src = self._resolve(args[0])
+            prod = self._op(src)
+            if not isinstance(prod, WideLinear) or src in self._skipped or src in self._mlp2:
+                continue
+            pargs = self._node_args[src]
+            if len(pargs) != 1 or not isinstance(pargs[0], str) or self._node_kwargs[src]:
+                continue
+            if consumers(src) != [name] or not WideMLP2.supported(prod, op):
+                continue
+            fused = WideMLP2(prod, op, relu1=prod.fused_activation == "relu")
+            fused.fused_activation = op.fused_activation
+            self._mlp2[name] = fused
+            self._chain_input[name] = pargs[0]
+            self._skipped[src] = name
 
     # ----------------------------------------------------------------------------------
     def forward(self, x: Tensor) -> Tensor:
@@ -368,11 +411,17 @@ class TracedWideModel(nn.Module):
         for name in self._execution_order:
             if name in self._attr_names or name not in self.stage_info:
                 continue
+            if name in self._skipped:
+                continue
             if name in self._aliases:
-                values[name] = values[self._aliases[name]]
+                if self._resolve(name) not in self._skipped:
+                    values[name] = values[self._aliases[name]]
                 continue
             op = self.stages[name.replace(".", "_")]
             args = [values[a] if isinstance(a, str) and a in values else a for a in self._node_args[name]]
+            if name in self._mlp2:
+                op = self._mlp2[name]
+                args = [values[self._chain_input[name]]]
             kwargs = {k: (values[v] if isinstance(v, str) and v in values else v)
                       for k, v in self._node_kwargs.get(name, {}).items()}
             if name in self._residual_of:
@@ -399,7 +448,7 @@ class TracedWideModel(nn.Module):
     def _into_packed(self, op: nn.Module, x: Tensor, kwargs: Dict[str, Any]) -> Optional[Tuple[Tensor, Tensor]]:
         """Run the output stage writing straight into the packed [B, N*C, *S] layout when it
         is a WideLinear or WideConv2d; returns (packed, N-first view of it) or None."""
-        if isinstance(op, WideLinear) and not kwargs and x.dim() >= 3:
+        if isinstance(op, (WideLinear, WideMLP2)) and not kwargs and x.dim() >= 3:
             nf_shape = (x.shape[0], x.shape[1], *x.shape[2:-1], op.out_features)
         elif isinstance(op, WideConv2d) and set(kwargs) <= {"residual"} and x.dim() == 5:
             kh, kw = op.kernel_size
@@ -413,7 +462,7 @@ class TracedWideModel(nn.Module):
         n, b, c = nf_shape[0], nf_shape[1], nf_shape[2]
         packed = torch.empty((b, n * c, *nf_shape[3:]), dtype=x.dtype, device=x.device)
         view = packed.view(b, n, *nf_shape[2:]).movedim(1, 0)
-        if isinstance(op, WideLinear):
+        if isinstance(op, (WideLinear, WideMLP2)):
             op.forward_into(x, view, relu=op.fused_activation == "relu")
         else:
             op(x, out=view, **kwargs)
@@ -466,6 +515,10 @@ class TracedWideModel(nn.Module):
             total += params
             args = ", ".join(str(a) for a in self._node_args[name])
             note = f"  -> fused into {self._aliases[name]}" if name in self._aliases else ""
+            if name in self._skipped:
+                note = f"  -> fused into {self._skipped[name]} (one two-layer launch)"
+            elif name in self._mlp2:
+                note = f"  (runs {self._mlp2[name]!r})"
             lines.append(f"  [{st.order}] {name}({args}): {type(op).__name__} ({params:,} params){note}")
         lines.append("")
         lines.append(f"Total: {total:,} params ({total // max(self.n, 1):,} per model)")

@@ -99,3 +99,29 @@ def test_cpu_tensors_raise_without_touching_a_device():
         wc.WideLinear(2, 4, 3)(torch.zeros(2, 5, 4))
     with pytest.raises(RuntimeError, match="ROCm device tensors only"):
         wc.WideLayerNorm(2, 4)(torch.zeros(2, 3, 4))
+
+
+def test_mlp2_supported_rules(hip):
+    s = hip.lib().wc_mlp2_supported
+    assert s(hip.F32, 64, 128, 64) == 1
+    assert s(hip.BF16, 64, 128, 64) == 1
+    assert s(hip.F32, 32, 64, 16) == 1
+    assert s(hip.BF16, 32, 64, 16) == 0          # bf16 rows need 64-element multiples
+    assert s(hip.F32, 64, 96, 64) == 1 and s(hip.F32, 64, 80, 64) == 0
+    assert s(hip.F32, 64, 128, 24) == 0          # out in whole 16-column tiles
+    assert s(hip.F32, 64, 288, 64) == 0          # hidden and out at most 256
+    assert s(hip.F32, 1024, 256, 256) == 0       # beyond 160 KB of LDS
+    assert s(hip.F32, 64, 128, 64) == 1 and s(7, 64, 128, 64) == 0
+
+
+def test_mlp2_arg_checks(hip):
+    a = hip._Mlp2Args()
+    a.dtype, a.n, a.m = hip.F32, 1, 4
+    a.in_features, a.hidden, a.out_features = 64, 80, 64
+    assert hip.lib().wc_mlp2(ctypes.byref(a), None) < 0
+    assert "not supported" in hip.last_error()
+    a.hidden = 128
+    a.x = a.w1 = a.w2 = a.y = 16                 # never dereferenced: rejected before any launch
+    a.x_rows_inner, a.y_rows_inner = 0, 4
+    assert hip.lib().wc_mlp2(ctypes.byref(a), None) < 0
+    assert "rows_inner" in hip.last_error()

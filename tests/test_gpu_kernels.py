@@ -355,6 +355,86 @@ def test_traced_mlp_config(hip):
             assert rel_err(outs[k], models[k].cpu()(ins[k])) <= TOL_F32
 
 
+class _MLP(nn.Module):
+    def __init__(self, d_in, d_hidden, d_out, relu=True):
+        super().__init__()
+        self.fc1 = nn.Linear(d_in, d_hidden)
+        self.fc2 = nn.Linear(d_hidden, d_out)
+        self.relu = relu
+
+    def forward(self, x):
+        h = self.fc1(x)
+        return self.fc2(F.relu(h) if self.relu else h)
+
+
+class _MLPTap(_MLP):
+    """fc1's output feeds fc2 and the model output: the chain must not be fused."""
+
+    def forward(self, x):
+        h = self.fc1(x)
+        return self.fc2(F.relu(h)) + h.sum(dim=-1, keepdim=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,b,d_in,d_hidden,d_out,relu", [
+    (100, 32, 64, 128, 64, True),     # the MLP configuration's shapes
+    (7, 37, 32, 64, 16, True),        # rows straddle two 32-row blocks
+    (3, 5, 96, 32, 48, False),        # no activation between the layers
+    (4, 9, 20, 40, 12, True),         # sizes the fused kernel does not take: two launches
+    (5, 100, 64, 96, 128, True),      # fp32: 24-chunk h rows (swizzle over 8), 4 row blocks
+    (3, 40, 128, 192, 128, True),     # bf16: 12 hidden column blocks; fp32 exceeds LDS: two launches
+])
+def test_traced_linear_chain(hip, dtype, n, b, d_in, d_hidden, d_out, relu):
+    """Linear -> [ReLU] -> Linear runs as one wc_mlp2 launch when the sizes allow it."""
+    import wide_compiler as wc
+    models = []
+    for i in range(n):
+        torch.manual_seed(2000 + i)
+        models.append(_MLP(d_in, d_hidden, d_out, relu).to(dtype))
+    g = gen(114)
+    ins = [torch.randn(b, d_in, generator=g).to(dtype) for _ in range(n)]
+    packed = wide_ref.pack_inputs(ins)
+    wide = wc.compile([m.to(DEV) for m in models], ins[0].to(DEV))
+    fused = "one two-layer launch" in wide.summary()
+    assert fused == _hip_supported(dtype, d_in, d_hidden, d_out)
+    with torch.no_grad():
+        y = wide(packed.to(DEV)).cpu()
+    st = lambda k: torch.stack([getattr(getattr(m, k.split('.')[0]), k.split('.')[1]).detach().cpu().double()
+                                for m in models])  # noqa: E731
+    w1, b1, w2, b2 = st("fc1.weight"), st("fc1.bias"), st("fc2.weight"), st("fc2.bias")
+    xn = packed.double().view(b, n, d_in).movedim(1, 0)
+    h = torch.einsum("nbi,noi->nbo", xn, w1) + b1[:, None]
+    h = F.relu(h) if relu else h
+    exact = (torch.einsum("nbi,noi->nbo", h, w2) + b2[:, None]).movedim(0, 1).reshape(b, n * d_out)
+    assert rel_err(y, exact) <= tol(dtype)
+    if dtype == torch.bfloat16:   # the reference's rounding points: bf16 layer outputs
+        with torch.no_grad():
+            for k in (0, n - 1):
+                assert rel_err(y[:, k * d_out:(k + 1) * d_out], models[k].cpu()(ins[k]).float()) <= TOL_BF16
+
+
+def test_traced_linear_chain_with_tap_is_not_fused(hip):
+    import wide_compiler as wc
+    n, b = 4, 8
+    models = []
+    for i in range(n):
+        torch.manual_seed(3000 + i)
+        models.append(_MLPTap(32, 64, 32))
+    g = gen(115)
+    ins = [torch.randn(b, 32, generator=g) for _ in range(n)]
+    wide = wc.compile([m.to(DEV) for m in models], ins[0].to(DEV))
+    assert "one two-layer launch" not in wide.summary()
+    with torch.no_grad():
+        y = wide(wide_ref.pack_inputs(ins).to(DEV)).cpu()
+        for k in range(n):
+            assert rel_err(y[:, k * 32:(k + 1) * 32], models[k].cpu()(ins[k])) <= TOL_F32
+
+
+def _hip_supported(dtype, d_in, d_hidden, d_out):
+    from wide_compiler import _hip
+    return _hip.mlp2_supported(dtype, d_in, d_hidden, d_out)
+
+
 def test_compile_validate_true(hip):
     import wide_compiler as wc
     models = [MLP(16, 32, 8).to(DEV) for _ in range(12)]
