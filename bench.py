@@ -202,7 +202,7 @@ def cfg_resblock(dev, steps, warmup) -> Dict:
         xn = x.view(b, n, c, hw, hw).movedim(1, 0)
         sec = _event_time(lambda: conv1(xn), steps, warmup)
         flops = 2.0 * n * b * hw * hw * c * c * 9
-        return {"bound": "mfma", "kernel": "conv_kernel (conv3x3 + BN + ReLU, bf16)", "flops_per_launch": flops,
+        return {"bound": "mfma", "kernel": "conv_res_kernel (resident-weight conv3x3 + BN + ReLU, bf16)", "flops_per_launch": flops,
                 "sec": sec, "peak": PEAK["bf16_mfma"]}
 
     n_cpu = 4
