@@ -795,9 +795,13 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
   };
   auto store_input = [&]() {
     char* base = ilds + grp * C::IN_BYTES;
+    // the LDS addresses are recomputed per call (an opaque copy of the thread index
+    // keeps the compiler from holding 8 of them per unit live across phases)
+    int g_op = gtid;
+    asm volatile("" : "+v"(g_op));
 #pragma unroll
     for (int k = 0; k < C::UPT; ++k) {
-      const int u = gtid + k * 256;
+      const int u = g_op + k * 256;
       if (k == 0 || u < C::UNITS) {                    // (only a partial last round branches)
         const int cg = u % NCH, rest = u / NCH;
         const int v = rest % C::VPR, ir = rest / C::VPR;
@@ -867,12 +871,16 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) bbase[ks] = fr * PXB + C::swz(ks * 4 + kq, fr) * 16;
 
-  // ---- output / residual byte offsets: the lane's 4-pixel run of tile (i, j) starts
-  // at pixel wl*64 + i*16 + kq*4 of the item (row-major) and channel j*16 + fr:
-  // lane_off + 32 i (immediate) + 32 j how (scalar) ----
+  // ---- output / residual byte offsets.  The epilogue regroups each 16-channel tile
+  // j so that one 16-byte store per lane covers whole 128-byte runs (the wave's 64
+  // pixels) of 8 channels: the lane stores 8 pixels starting at pixel wl*64 + 8 g
+  // of the item, of channel j*16 + (fr & ~1) (store A) and the next channel
+  // (store B, one channel plane further) ----
   const int how = p.ho * W;
-  const uint32_t lane_off = static_cast<uint32_t>(fr * how + wl * 64 + kq * 4) * 2u;
-  auto orow = [&](int i) { return (wl * 64 + i * 16 + kq * 4) / W; };
+  const int g_st = 4 * (fr & 1) + 2 * (kq & 1) + (kq >> 1);
+  const uint32_t lane_off = static_cast<uint32_t>((fr & ~1) * how + wl * 64 + 8 * g_st) * 2u;
+  const int lane_orow = (wl * 64 + 8 * g_st) / W;
+  const uint32_t plane = static_cast<uint32_t>(how) * 2u;
   const float relu_floor = p.act == WC_ACT_RELU ? 0.f : -__builtin_huge_valf();
   const bool has_res = p.res != nullptr;
 
@@ -933,51 +941,89 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
     }
   };
 
-  // Finish the group's last computed item: residual loads first (their latency
-  // overlaps the staging work in between), then affine + residual + ReLU + stores.
-  uint2 rv[2][kFN];                                     // residual runs of two row tiles
-  auto res_issue = [&](int i0) {
+  // Finish the group's last computed item, two channel tiles at a time: residual loads
+  // first (their latency overlaps the staging work in between), then affine (+ ReLU),
+  // the regrouping, residual + ReLU and the stores.
+  //
+  // Regrouping of tile j.  After the MFMAs lane (fr, kq) holds channel j*16 + fr at
+  // pixels i*16 + kq*4 + [0, 4) of the wave's 64 (row tiles i = 0..3), packed to bf16
+  // pairs: X = tiles 0, 2 and Y = tiles 1, 3.  (1) v_permlane16_swap exchanges X of
+  // the odd 16-lane rows (kq = 1, 3) with Y of the even rows, so every lane holds two
+  // 8-pixel chunks of its channel, chunk s = {X[2s], X[2s+1], Y[2s], Y[2s+1]} at
+  // pixels 8 (4 s + 2 (kq & 1) + (kq >> 1)).  (2) Lanes fr and fr ^ 1 (a DPP quad
+  // permutation) trade chunks, so the even lane holds chunk 0 of both channels and
+  // the odd lane chunk 1 of both: store A writes channel fr & ~1, store B channel
+  // fr | 1, each as 8 lanes x 16 contiguous bytes.
+  uint4 rv[2][2];                                       // residual chunks (A, B) of two tiles
+  auto res_issue = [&](int j0) {
     const ResItem& it = fin_it;
     const __amdgpu_buffer_rsrc_t rrs =
         res_rsrc(static_cast<const bf16*>(p.res) + it.mdl * p.r_sn + it.b * p.r_sb);
     const uint32_t obase = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
     const int left = p.ho - it.th * TR;
-    const int orows = left < TR ? left : TR;
+    const uint32_t off = lane_orow < (left < TR ? left : TR) ? lane_off : kResOob;
 #pragma unroll
-    for (int i = i0; i < i0 + 2; ++i)
+    for (int j = j0; j < j0 + 2; ++j)
 #pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        rv[i - i0][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                      rrs, orow(i) < orows ? lane_off + i * 32 : kResOob,
-                                                      obase + static_cast<uint32_t>(j * 32 * how), 0));
+      for (int h = 0; h < 2; ++h)
+        rv[j - j0][h] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rrs, off, obase + static_cast<uint32_t>(j * 32 * how) + h * plane, 0));
   };
-  auto finish = [&](auto res, int i0) {
+  auto finish = [&](auto res, int j0) {
+    constexpr bool kRes = decltype(res)::value;
     const ResItem& it = fin_it;
     const __amdgpu_buffer_rsrc_t yrs = res_rsrc(static_cast<bf16*>(p.y) + it.mdl * p.y_sn + it.b * p.y_sb);
     const uint32_t obase = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
     const int left = p.ho - it.th * TR;
-    const int orows = left < TR ? left : TR;
+    const uint32_t off = lane_orow < (left < TR ? left : TR) ? lane_off : kResOob;
+    const bool odd = fr & 1;
 #pragma unroll
-    for (int i = i0; i < i0 + 2; ++i)
+    for (int j = j0; j < j0 + 2; ++j) {
+      uint32_t xy[2][4];                                // [X, Y][tile pair, bf16 pair]
 #pragma unroll
-      for (int j = 0; j < kFN; ++j) {
-        uint32_t w2[2];
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float v0 = acc[i][j][2 * h] * alpha[j] + beta[j];
           float v1 = acc[i][j][2 * h + 1] * alpha[j] + beta[j];
-          if constexpr (decltype(res)::value) {
-            const uint32_t c = pack_bf16x2(v0, v1);
-            const uint32_t r = h ? rv[i - i0][j].y : rv[i - i0][j].x;
-            v0 = bf16_lo(c) + bf16_lo(r);
-            v1 = bf16_hi(c) + bf16_hi(r);
+          if constexpr (!kRes) {
+            v0 = fmaxf(v0, relu_floor);
+            v1 = fmaxf(v1, relu_floor);
           }
-          w2[h] = pack_bf16x2(fmaxf(v0, relu_floor), fmaxf(v1, relu_floor));
+          xy[i & 1][(i >> 1) * 2 + h] = pack_bf16x2(v0, v1);
         }
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, make_uint2(w2[0], w2[1])), yrs,
-                                              orow(i) < orows ? lane_off + i * 32 : kResOob,
-                                              obase + static_cast<uint32_t>(j * 32 * how), 0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(xy[0][k], xy[1][k], false, false);
+        xy[0][k] = sw[0];
+        xy[1][k] = sw[1];
       }
+      uint32_t va[4], vb[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t c0 = xy[k >> 1][k & 1], c1 = xy[k >> 1][2 + (k & 1)];
+        const uint32_t recv = static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(0, static_cast<int>(odd ? c0 : c1), 0xB1, 0xF, 0xF, true));
+        va[k] = odd ? recv : c0;
+        vb[k] = odd ? c1 : recv;
+      }
+      if constexpr (kRes) {
+        const uint32_t* ra = reinterpret_cast<const uint32_t*>(&rv[j - j0][0]);
+        const uint32_t* rb = reinterpret_cast<const uint32_t*>(&rv[j - j0][1]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          va[k] = pack_bf16x2(fmaxf(bf16_lo(va[k]) + bf16_lo(ra[k]), relu_floor),
+                              fmaxf(bf16_hi(va[k]) + bf16_hi(ra[k]), relu_floor));
+          vb[k] = pack_bf16x2(fmaxf(bf16_lo(vb[k]) + bf16_lo(rb[k]), relu_floor),
+                              fmaxf(bf16_hi(vb[k]) + bf16_hi(rb[k]), relu_floor));
+        }
+      }
+      const uint32_t sb = obase + static_cast<uint32_t>(j * 32 * how);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, make_uint4(va[0], va[1], va[2], va[3])), yrs, off,
+                                             sb, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, make_uint4(vb[0], vb[1], vb[2], vb[3])), yrs, off,
+                                             sb + plane, 0);
+    }
   };
 
   auto lds_barrier = [&]() {
