@@ -16,6 +16,9 @@ configurations are selectable with --config (mlp, resblock, attention, seq).
 * roofline = the dominant kernel: algorithmic flops (or bytes) per launch divided by its
   average duration, timed with HIP events on the stream it is launched on; peaks are MI355X
   datasheet values (dense MFMA fp32 157.3 TFLOP/s, bf16 2516.6 TFLOP/s; HBM 8 TB/s).
+* cache regimes: per-step GPU times (HIP events around each step, in the mode used) over K
+  steps, median reported hot (steps back to back) and cold (a 512 MiB buffer rewritten before
+  every step, so the 256 MB Infinity Cache and the L2s hold none of the step's data).
 * cpu_baseline = the oracle (op-for-op CPU restatement of the reference wide path, torch CPU
   ops) on the host cores over a bounded sample, scaled to samples/s.
 """
@@ -63,6 +66,27 @@ def _event_time(fn: Callable[[], None], k: int, w: int) -> float:
     e1.record(st)
     e1.synchronize()
     return e0.elapsed_time(e1) / k * 1e-3
+
+
+def _step_times(fn: Callable[[], None], k: int, flush=None) -> list:
+    """GPU seconds of each of k calls of fn (HIP events on torch's current stream around each
+    call); with flush, the buffer is rewritten before every call, outside the timed window."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(k)]
+    st = torch.cuda.current_stream()
+    for i in range(k):
+        if flush is not None:
+            flush.fill_(i & 0x7f)
+        ev[i][0].record(st)
+        fn()
+        ev[i][1].record(st)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e-3 for a, b in ev]
+
+
+def _median(v: list) -> float:
+    v = sorted(v)
+    return v[len(v) // 2] if len(v) % 2 else 0.5 * (v[len(v) // 2 - 1] + v[len(v) // 2])
 
 
 def _cpu_loop(fn: Callable[[], None], seconds: float, min_iters: int = 2):
@@ -419,6 +443,15 @@ def main() -> int:
     else:
         wall, used = (graph_s, "graph") if graph_s <= eager_s else (eager_s, "eager")
 
+    # hot / cold cache regimes: per-step GPU times in the mode used
+    run_step = graph.replay if used == "graph" else step
+    with torch.inference_mode():
+        hot = _step_times(run_step, args.steps)
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        cold = _step_times(run_step, args.steps, flush)
+        del flush
+    hot_med, cold_med = _median(hot), _median(cold)
+
     with torch.inference_mode():
         rf = cfg["roofline"]()
     if "flops_per_launch" in rf:
@@ -464,6 +497,9 @@ def main() -> int:
         "config": {"workload": cfg["name"], "n_models": n, "batch": b, "mode": used, **cfg["extra"]},
         "roofline": roofline,
         "eager_samples_per_s": n * b * args.steps / eager_s,
+        "cache_regimes": {"mode": used, "steps": args.steps, "flush_bytes": 512 << 20,
+                          "hot_median_ms": hot_med * 1e3, "hot_samples_per_s": n * b / hot_med,
+                          "cold_median_ms": cold_med * 1e3, "cold_samples_per_s": n * b / cold_med},
         "graph_samples_per_s": None if graph_s is None else n * b * args.steps / graph_s,
         "parity_rel_err_vs_oracle": parity,
         "cpu_baseline": cpu,
