@@ -6,7 +6,7 @@ Wide-forward throughput of the MI355X build on one GPU.  Prints ONE JSON line.
 
 Default workload (the configuration the headline metric is quoted on): WideGRU over N=32
 nn.GRU(64 -> 128, batch_first) models, x [32, 4, 32, 64] ~ N(0, 1) fp32, h0 = 0.  The other
-configurations are selectable with --config (mlp, resblock, attention, seq).
+configurations are selectable with --config (mlp, resblock, attention, seq, groupnorm).
 
 * step  = one wide forward over one batch, inputs already resident in HBM.
 * value = samples/s = N*B*K / wall time of K steps, bracketed by torch.cuda.synchronize().
@@ -364,8 +364,51 @@ def cfg_seq(dev, steps, warmup) -> Dict:
             "extra": {"seq_len": t, "vocab": v, "embed": 256, "hidden": hdim}}
 
 
+def cfg_groupnorm(dev, steps, warmup) -> Dict:
+    """WideGroupNorm over N=32 nn.GroupNorm(8, 64) (the reference benchmark's groups = min(8, C),
+    wide_groupnorm.py:281), x [32, 8, 64, 32, 32] ~ N(0, 1) fp32."""
+    import torch
+    import torch.nn as nn
+    import wide_compiler as wc
+    from oracle import wide_ref
+
+    n, b, c, groups, hw = 32, 8, 64, 8, 32
+    torch.manual_seed(1234)
+    mods = [nn.GroupNorm(groups, c) for _ in range(n)]
+    with torch.no_grad():
+        for m in mods:
+            m.weight.normal_(1, 0.1)
+            m.bias.normal_(0, 0.1)
+    wide = wc.WideGroupNorm.from_modules(mods).to(dev)
+    g = torch.Generator().manual_seed(4321)
+    x_cpu = torch.randn(n, b, c, hw, hw, generator=g)
+    x = x_cpu.to(dev)
+    w_cpu, b_cpu = wide.norm.weight.detach().cpu(), wide.norm.bias.detach().cpu()
+
+    def parity():
+        with torch.inference_mode():
+            y = wide(x)
+        return _rel(y, wide_ref.group_norm(x_cpu.double(), w_cpu.double(), b_cpu.double(), groups, 1e-5))
+
+    def roofline():
+        sec = _event_time(lambda: wide(x), steps, warmup)
+        byts = 2.0 * x.numel() * 4 + 2 * n * c * 4
+        return {"bound": "hbm", "kernel": "groupnorm_kernel (8192-element rows, fp32)", "bytes_per_launch": byts,
+                "sec": sec, "peak": PEAK["hbm"]}
+
+    n_cpu = 8
+
+    def cpu_run():
+        wide_ref.group_norm(x_cpu[:n_cpu], w_cpu[:n_cpu * c], b_cpu[:n_cpu * c], groups, 1e-5)
+
+    return {"name": f"WideGroupNorm N={n} B={b} C={c} G={groups} {hw}x{hw} fp32", "n": n, "batch": b,
+            "dtype": "fp32", "step": lambda: wide(x), "parity": parity, "roofline": roofline, "cpu": cpu_run,
+            "cpu_samples": n_cpu * b, "cpu_sample": f"{n_cpu} of the {n} models (no cross-model terms)",
+            "extra": {"channels": c, "groups": groups, "spatial": [hw, hw]}}
+
+
 CONFIGS = {"gru": cfg_gru, "mlp": cfg_mlp, "resblock": cfg_resblock, "attention": cfg_attention,
-           "seq": cfg_seq}
+           "seq": cfg_seq, "groupnorm": cfg_groupnorm}
 
 
 def main() -> int:

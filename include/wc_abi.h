@@ -145,6 +145,22 @@ int32_t wc_bn_eval(const void* x, int64_t x_stride_n, int64_t x_stride_b,
                    int32_t dtype, int32_t param_dtype, int32_t act, void* stream);
 
 /*
+ * GroupNorm / InstanceNorm on N-first activations -- replaces the channel-packed
+ * nn.GroupNorm(N*G, N*C) of WideGroupNorm.forward (wide_compiler/core/primitives/
+ * wide_groupnorm.py:89-117) and nn.InstanceNorm1d/2d(N*C) of WideInstanceNorm1d/2d
+ * .forward (wide_instancenorm.py:82-101, 213-232) together with the permutes and
+ * .contiguous() around them.  x, y contiguous [n, b, c, s] (s = product of the
+ * spatial dims); c % groups == 0 (instance norm: groups = c).  Each (model i,
+ * batch row, group) normalises its (c / groups) * s elements with the biased
+ * variance, in fp32:
+ *   y = (x - mean) / sqrt(var + eps) * weight[i*c + ch] + bias[i*c + ch]
+ * weight and bias both NULL when not affine; act = WC_ACT_NONE or WC_ACT_RELU.
+ */
+int32_t wc_group_norm(const void* x, void* y, int64_t n, int64_t b, int64_t c, int64_t s,
+                      int64_t groups, const void* weight, const void* bias, float eps,
+                      int32_t dtype, int32_t param_dtype, int32_t act, void* stream);
+
+/*
  * Recurrent layer forward (single layer, unidirectional) -- replaces the fused
  * input projection einsum + T-step Python loop of
  *   WideGRU._forward_fused  (wide_compiler/core/primitives/wide_gru.py:148-213)

@@ -121,6 +121,32 @@ def layernorm(x: Tensor, weight_flat: Tensor, bias_flat: Tensor, n: int, eps: fl
     return x * weight + bias
 
 
+def group_norm(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], groups: int, eps: float) -> Tensor:
+    """WideGroupNorm.forward (fused strategy), wide_groupnorm.py:89-117: nn.GroupNorm(N*G, N*C) over the
+    channel-packed view.  x [N, B, C, *spatial]; each (model, batch row, group) is normalised over its
+    C/G channels x spatial with the biased variance; weight / bias [N*C] (model i's channel c at i*C + c)
+    or None."""
+    n, b, c = x.shape[:3]
+    xg = x.reshape(n, b, groups, -1)
+    mean = xg.mean(dim=-1, keepdim=True)
+    var = xg.var(dim=-1, unbiased=False, keepdim=True)
+    y = ((xg - mean) / torch.sqrt(var + eps)).reshape(x.shape)
+    if weight is not None:
+        shape = (n, 1, c) + (1,) * (x.dim() - 3)
+        y = y * weight.reshape(shape) + bias.reshape(shape)
+    return y
+
+
+def instance_norm(x: Tensor, weight: Optional[Tensor], bias: Optional[Tensor], eps: float,
+                  running_mean: Optional[Tensor] = None, running_var: Optional[Tensor] = None) -> Tensor:
+    """WideInstanceNorm1d/2d.forward (fused strategy), wide_instancenorm.py:82-101 / 213-232:
+    nn.InstanceNorm*(N*C) on the channel-packed view -- instance statistics per (model, batch row,
+    channel), or, in eval mode with track_running_stats, the running statistics."""
+    if running_mean is not None:
+        return batchnorm_eval(x, weight, bias, running_mean, running_var, eps, x.shape[0])
+    return group_norm(x, weight, bias, x.shape[2], eps)
+
+
 def embedding(weight: Tensor, ids: Tensor) -> Tensor:
     """WideEmbedding._forward_indexed, wide_embedding.py:100-102 (shared ids)."""
     return weight[:, ids]

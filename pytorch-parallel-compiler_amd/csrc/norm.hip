@@ -342,6 +342,187 @@ int32_t launch_bn(const void* x, int64_t xsn, int64_t xsb, const void* w, const 
   return check_launch("wc_bn_eval");
 }
 
+// ---------------------------------------------------------------------------
+// GroupNorm / InstanceNorm.  A row is one (model, batch row, group): R = cpg * s
+// contiguous elements of the N-first activation (cpg channels of s spatial
+// elements).  WPR waves own a row; lane t of the row holds the V-element vectors
+// (it * 64 WPR + t) for it < ITEMS in registers, so the row is read once and
+// written once.  Statistics are two-pass fp32 (mean, then the mean squared
+// deviation: the biased variance torch uses); one reciprocal square root per row.
+// The affine weight of element e is that of channel g * cpg + e / s of its model
+// (a vector never straddles two channels: s % V == 0).
+// ---------------------------------------------------------------------------
+struct GnParams {
+  uint32_t rows;
+  int r, s, cpg, c;
+  FastDiv groups;       // row -> (model * batch + batch row, group)
+  FastDiv per_model;    // row -> model (batch * groups rows per model)
+  FastDiv sdiv;
+  float eps;
+  int relu;
+};
+
+template <int WPR>
+__device__ __forceinline__ float gn_row_sum(float v, float* red) {
+  v = group_reduce<64>(v);
+  if constexpr (WPR == 1) {
+    return v;
+  } else {
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();                      // red[] of the previous reduction has been read
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+  }
+}
+
+template <typename T, typename P, int V, int WPR, int ITEMS>
+__global__ __launch_bounds__(kNormBlock) void groupnorm_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                              const P* __restrict__ w, const P* __restrict__ bias,
+                                                              GnParams p) {
+  constexpr int RPB = 4 / WPR;                           // rows per block
+  constexpr int LT = 64 * WPR;                           // lanes per row
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const uint32_t row = blockIdx.x * RPB + (tid >> 6) / WPR;
+  if (WPR == 1 && row >= p.rows) return;                 // whole waves leave together
+  const bool live = row < p.rows;                        // (WPR == 4: one row per block)
+  const int lt = tid & (LT - 1);
+  const int64_t base = static_cast<int64_t>(live ? row : 0) * p.r;
+  const T* xr = x + base;
+  float v[ITEMS][V];
+  float sum = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * LT + lt) * V;
+    if (live && e < p.r) {
+      LoadV<T, V>::ld(xr + e, v[it]);
+#pragma unroll
+      for (int k = 0; k < V; ++k) sum += v[it][k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) v[it][k] = 0.f;
+    }
+  }
+  const float inv_r = 1.0f / static_cast<float>(p.r);
+  const float mean = gn_row_sum<WPR>(sum, red) * inv_r;
+  float sq = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * LT + lt) * V;
+    if (e < p.r) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        const float d = v[it][k] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float rstd = 1.0f / sqrtf(gn_row_sum<WPR>(sq, red) * inv_r + p.eps);
+  if (!live) return;
+  const uint32_t mb = fdiv(row, p.groups);
+  const int g = static_cast<int>(row - mb * p.groups.d);
+  const uint32_t mdl = fdiv(row, p.per_model);
+  const int64_t ch0 = static_cast<int64_t>(mdl) * p.c + g * p.cpg;
+  T* yr = y + base;
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = (it * LT + lt) * V;
+    if (e < p.r) {
+      const int64_t ch = ch0 + fdiv(static_cast<uint32_t>(e), p.sdiv);
+      const float a = (w ? to_f32(w[ch]) : 1.f) * rstd;
+      const float b = (bias ? to_f32(bias[ch]) : 0.f) - mean * a;
+      float o[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        o[k] = v[it][k] * a + b;
+        if (p.relu) o[k] = fmaxf(o[k], 0.f);
+      }
+      LoadV<T, V>::st(yr + e, o);
+    }
+  }
+}
+
+// Rows longer than the register-resident configurations: one block per row,
+// three passes over the row (sum, squared deviations, normalise).
+template <typename T, typename P>
+__global__ __launch_bounds__(kNormBlock) void groupnorm_long_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                                   const P* __restrict__ w,
+                                                                   const P* __restrict__ bias, GnParams p) {
+  __shared__ float red[4];
+  const uint32_t row = blockIdx.x;
+  const int64_t base = static_cast<int64_t>(row) * p.r;
+  const T* xr = x + base;
+  float sum = 0.f;
+  for (int e = threadIdx.x; e < p.r; e += kNormBlock) sum += to_f32(xr[e]);
+  const float inv_r = 1.0f / static_cast<float>(p.r);
+  const float mean = gn_row_sum<4>(sum, red) * inv_r;
+  float sq = 0.f;
+  for (int e = threadIdx.x; e < p.r; e += kNormBlock) {
+    const float d = to_f32(xr[e]) - mean;
+    sq += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(gn_row_sum<4>(sq, red) * inv_r + p.eps);
+  const uint32_t mb = fdiv(row, p.groups);
+  const int g = static_cast<int>(row - mb * p.groups.d);
+  const uint32_t mdl = fdiv(row, p.per_model);
+  const int64_t ch0 = static_cast<int64_t>(mdl) * p.c + g * p.cpg;
+  T* yr = y + base;
+  for (int e = threadIdx.x; e < p.r; e += kNormBlock) {
+    const int64_t ch = ch0 + fdiv(static_cast<uint32_t>(e), p.sdiv);
+    const float a = (w ? to_f32(w[ch]) : 1.f) * rstd;
+    float o = (to_f32(xr[e]) - mean) * a + (bias ? to_f32(bias[ch]) : 0.f);
+    if (p.relu) o = fmaxf(o, 0.f);
+    yr[e] = from_f32<T>(o);
+  }
+}
+
+template <typename T, typename P, int V>
+int32_t launch_gn_v(const T* x, T* y, const P* w, const P* b, const GnParams& p, hipStream_t st) {
+  const int r = p.r;
+  auto go = [&](auto kern, int rows_per_block) {
+    kern<<<dim3(static_cast<uint32_t>(cdiv(p.rows, rows_per_block))), kNormBlock, 0, st>>>(x, y, w, b, p);
+    return check_launch("wc_group_norm");
+  };
+  if (r <= 64 * V * 1) return go(groupnorm_kernel<T, P, V, 1, 1>, 4);
+  if (r <= 64 * V * 2) return go(groupnorm_kernel<T, P, V, 1, 2>, 4);
+  if (r <= 64 * V * 4) return go(groupnorm_kernel<T, P, V, 1, 4>, 4);
+  if (r <= 256 * V * 2) return go(groupnorm_kernel<T, P, V, 4, 2>, 1);
+  if (r <= 256 * V * 4) return go(groupnorm_kernel<T, P, V, 4, 4>, 1);
+  if (r <= 256 * V * 8) return go(groupnorm_kernel<T, P, V, 4, 8>, 1);
+  if (V > 1 && r <= 256 * V * 16) return go(groupnorm_kernel<T, P, V, 4, 16>, 1);
+  return go(groupnorm_long_kernel<T, P>, 1);
+}
+
+template <typename T, typename P>
+int32_t launch_gn(const void* x, void* y, const void* w, const void* b, int64_t n, int64_t bt, int64_t c,
+                  int64_t s, int64_t groups, float eps, int act, hipStream_t st) {
+  constexpr int VMAX = 16 / sizeof(T);
+  const int64_t cpg = c / groups;
+  const int64_t r = cpg * s;
+  const int64_t rows = n * bt * groups;
+  if (r >= 0x7fffffffll || rows >= 0x7fffffffll || s >= 0x7fffffffll || n * c >= 0x7fffffffll)
+    return set_error(WC_ERR_LIMIT, "wc_group_norm: tensor too large");
+  GnParams p;
+  p.rows = static_cast<uint32_t>(rows);
+  p.r = static_cast<int>(r);
+  p.s = static_cast<int>(s);
+  p.cpg = static_cast<int>(cpg);
+  p.c = static_cast<int>(c);
+  p.groups = make_fastdiv(static_cast<uint32_t>(groups));
+  p.per_model = make_fastdiv(static_cast<uint32_t>(bt * groups));
+  p.sdiv = make_fastdiv(static_cast<uint32_t>(s));
+  p.eps = eps;
+  p.relu = act == WC_ACT_RELU;
+  const T* xt = static_cast<const T*>(x);
+  T* yt = static_cast<T*>(y);
+  const P* wt = static_cast<const P*>(w);
+  const P* bt_ = static_cast<const P*>(b);
+  const bool vec = s % VMAX == 0 &&
+                   common_vec_bytes({reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(y)}) >= 16;
+  return vec ? launch_gn_v<T, P, VMAX>(xt, yt, wt, bt_, p, st) : launch_gn_v<T, P, 1>(xt, yt, wt, bt_, p, st);
+}
+
 }  // namespace
 }  // namespace wc
 
@@ -398,5 +579,29 @@ extern "C" int32_t wc_bn_eval(const void* x, int64_t x_stride_n, int64_t x_strid
     return launch_bn<f16, f16>(x, x_stride_n, x_stride_b, weight, bias, running_mean, running_var,
                                eps, y, n, b, c, hw, act, st);
   return set_error(WC_ERR_DTYPE, "wc_bn_eval: unsupported dtype pair (%s, %s)", dtype_name(dtype),
+                   dtype_name(param_dtype));
+}
+
+extern "C" int32_t wc_group_norm(const void* x, void* y, int64_t n, int64_t b, int64_t c, int64_t s,
+                                 int64_t groups, const void* weight, const void* bias, float eps,
+                                 int32_t dtype, int32_t param_dtype, int32_t act, void* stream) {
+  clear_error();
+  WC_REQUIRE(n >= 0 && b >= 0 && c >= 0 && s >= 0, WC_ERR_SHAPE, "wc_group_norm: negative size");
+  WC_REQUIRE(groups > 0 && c % groups == 0, WC_ERR_SHAPE, "wc_group_norm: %lld channels not divisible into %lld groups",
+             (long long)c, (long long)groups);
+  WC_REQUIRE(act == WC_ACT_NONE || act == WC_ACT_RELU, WC_ERR_ARG, "wc_group_norm: bad act %d", act);
+  WC_REQUIRE((weight == nullptr) == (bias == nullptr), WC_ERR_ARG, "wc_group_norm: weight and bias go together");
+  if (n == 0 || b == 0 || c == 0 || s == 0) return WC_OK;
+  WC_REQUIRE(x && y, WC_ERR_NULL, "wc_group_norm: null pointer");
+  hipStream_t st = as_stream(stream);
+  if (dtype == WC_F32 && param_dtype == WC_F32)
+    return launch_gn<float, float>(x, y, weight, bias, n, b, c, s, groups, eps, act, st);
+  if (dtype == WC_BF16 && param_dtype == WC_BF16)
+    return launch_gn<bf16, bf16>(x, y, weight, bias, n, b, c, s, groups, eps, act, st);
+  if (dtype == WC_BF16 && param_dtype == WC_F32)
+    return launch_gn<bf16, float>(x, y, weight, bias, n, b, c, s, groups, eps, act, st);
+  if (dtype == WC_F16 && param_dtype == WC_F16)
+    return launch_gn<f16, f16>(x, y, weight, bias, n, b, c, s, groups, eps, act, st);
+  return set_error(WC_ERR_DTYPE, "wc_group_norm: unsupported dtype pair (%s, %s)", dtype_name(dtype),
                    dtype_name(param_dtype));
 }

@@ -130,6 +130,7 @@ SIGNATURES = {
     "wc_embedding_gather": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _P, _P, _P]),
     "wc_layernorm": (_I32, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I32, _I32, _P]),
     "wc_bn_eval": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P]),
+    "wc_group_norm": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F, _I32, _I32, _I32, _P]),
     "wc_rnn_workspace_bytes": (_I64, [ctypes.POINTER(_RnnArgs)]),
     "wc_rnn_forward": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
@@ -251,6 +252,15 @@ def bn_eval(x: Tensor, xsn: int, xsb: int, weight: Optional[Tensor], bias: Optio
                             float(eps), y.data_ptr(), n, b, c, hw, dtype_code(x.dtype, "batchnorm"),
                             dtype_code(rmean.dtype, "batchnorm"), ACT_RELU if relu else ACT_NONE,
                             stream_of(x)), "wc_bn_eval")
+
+
+def group_norm(x: Tensor, y: Tensor, n: int, b: int, c: int, s: int, groups: int,
+               weight: Optional[Tensor], bias: Optional[Tensor], eps: float, relu: bool = False) -> None:
+    """x, y contiguous [n, b, c, s]; statistics per (model, batch row, group of c // groups channels)."""
+    pdt = weight.dtype if weight is not None else x.dtype
+    _check(lib().wc_group_norm(x.data_ptr(), y.data_ptr(), n, b, c, s, groups, ptr(weight), ptr(bias), float(eps),
+                               dtype_code(x.dtype, "group_norm"), dtype_code(pdt, "group_norm"),
+                               ACT_RELU if relu else ACT_NONE, stream_of(x)), "wc_group_norm")
 
 
 def grouped_gemm(*, n: int, m: int, o: int, k: int,
