@@ -462,11 +462,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void* base) {
 }
 
 // VMEM instructions one wave issues per tile epilogue: 32 stores (+ 32 residual
-// loads) and the 8 bias loads of the next tile.
+// loads) and the LDS-DMA load of its quarter of the next tile's bias.
 template <bool RES>
 struct XlEpi {
-  static constexpr int value = 32 * (RES ? 2 : 1) + 8;
+  static constexpr int value = 32 * (RES ? 2 : 1) + 1;
 };
+constexpr int kXlBiasSlot = kXlB * 4;                     // bytes of one tile's bias (fp32 at most)
 
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
 // expcnt 6:4 left at 7, lgkmcnt 11:8)
@@ -485,9 +486,9 @@ __device__ __forceinline__ void bare_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <typename TB, bool RES>
+template <typename TB, bool RES, bool RELU>
 __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, int tiles_total) {
-  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 4 * kXlStripBytes];
+  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 4 * kXlStripBytes + 2 * kXlBiasSlot];
   lds_char* const smem = (lds_char*)smem_raw;        // keeps every LDS address 32-bit
   constexpr int E = XlEpi<RES>::value;
 
@@ -572,46 +573,67 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   };
 
   // ---- bias of a tile, in accumulator layout: columns o0 + ow + 16 i + 4 (lane >> 4) + e ----
-  float bacc[8][4];
-  auto load_bias = [&](const Tile& t) {
-    const __amdgpu_buffer_rsrc_t brs =
-        xl_rsrc(p.bias ? static_cast<const TB*>(p.bias) + static_cast<int64_t>(t.mdl) * p.b_sn : p.c);
-    const int cb = t.o0 + ow + 4 * (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int col = cb + 16 * i;
-      const uint32_t boff = (p.bias && col < p.o) ? static_cast<uint32_t>(col) * sizeof(TB) : kXlOob;
-      if constexpr (sizeof(TB) == 4) {
-        const i32x4 b4 = __builtin_amdgcn_raw_buffer_load_b128(brs, boff, 0, 0);
-        const float* bt = reinterpret_cast<const float*>(&b4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bacc[i][e] = bt[e];
-      } else {
-        const i32x2 b2 = __builtin_amdgcn_raw_buffer_load_b64(brs, boff, 0, 0);
-        const bf16* bt = reinterpret_cast<const bf16*>(&b2);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bacc[i][e] = to_f32(bt[e]);
-      }
-    }
+  // ---- bias of a tile: wave w moves the tile's columns [64 w, 64 w + 64) into LDS slot
+  // (tile index & 1) with one LDS-DMA load (columns past o read a valid column; the
+  // stores of those columns are dropped).  The epilogue adds it; the accumulators of
+  // a tile start at zero (the first MFMA of each takes a zero C operand). ----
+  lds_char* const bias_lds = smem + 2 * kXlStageBytes + 4 * kXlStripBytes;
+  // The lane index, recomputed (v_mbcnt) where it is needed outside the stage loop: a
+  // lane-derived value kept live across the loop gets spilled, and a spill reload's
+  // vmcnt wait would also wait for the operand loads of the next stages.
+  auto lane_now = []() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+  };
+  const char* const bias_base = p.bias ? static_cast<const char*>(p.bias) : static_cast<const char*>(p.c);
+  auto load_bias = [&](const Tile& t, int slot) {
+    constexpr int EPC = 16 / static_cast<int>(sizeof(TB));       // bias elements per 16-byte chunk
+    constexpr int LANES = 64 / EPC;                               // lanes that move the wave's 64 columns
+    const int lane = lane_now();
+    const int col = t.o0 + 64 * wave + EPC * (lane < LANES ? lane : 0);
+    const int cl = col < p.o ? col : p.o - EPC;
+    const int64_t eoff = p.bias ? static_cast<int64_t>(t.mdl) * p.b_sn + cl : 0;
+    if (lane < LANES)
+      __builtin_amdgcn_global_load_lds(bias_base + eoff * static_cast<int64_t>(sizeof(TB)),
+                                       (lds_ptr_t)(bias_lds + slot * kXlBiasSlot + 64 * wave * sizeof(TB)), 16, 0, 0);
   };
 
   f32x4 acc[8][8];
-  auto init_acc = [&]() {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{bacc[i][0], bacc[i][1], bacc[i][2], bacc[i][3]};
-  };
 
   // ---- epilogue of tile t: acc (+residual, ReLU) -> C, one 16-row strip at a time
   // through LDS, then 16-byte row chunks: lane -> row 4 q + (lane >> 4), 8 columns
   // from 8 (lane & 15) ----
   lds_char* strip = smem + 2 * kXlStageBytes + wave * kXlStripBytes;
-  auto epilogue = [&](const Tile& t) {
+  auto epilogue = [&](const Tile& t, int ti_parity) {
     const __amdgpu_buffer_rsrc_t crs = xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn);
     const __amdgpu_buffer_rsrc_t rrs =
         xl_rsrc(RES ? static_cast<const bf16*>(p.r) + static_cast<int64_t>(t.mdl) * p.r_sn : p.c);
-    const bool relu = p.act == WC_ACT_RELU;
+    constexpr bool relu = RELU;
+    const int lane = lane_now();
+    const int fr = lane & 15;
+    // bias of the lane's columns ow + 16 i + 4 (lane >> 4) + e.  With one stage per
+    // tile no stage wait has covered the bias load issued after the previous epilogue.
+    if (KS == 1) {
+      vm_lgkm_wait<0>();
+      bare_barrier();
+    }
+    float bv[8][4];
+    {
+      const lds_char* bl = bias_lds + (ti_parity & 1) * kXlBiasSlot + (ow + 4 * (lane >> 4)) * sizeof(TB);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (sizeof(TB) == 4) {
+          const f32x4 b4 = *(const __attribute__((address_space(3))) f32x4*)(bl + 16 * i * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? b4[e] : 0.f;
+        } else {
+          const bf16x4 b4 = *(const lds_bf16x4*)(bl + 16 * i * 2);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? to_f32(b4[e]) : 0.f;
+        }
+      }
+    }
     const int cc = lane & 15, rsub = lane >> 4;
     const int col = t.o0 + ow + cc * 8;
     const bool col_ok = col < p.o;
@@ -622,7 +644,7 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
         bf16x4 o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = acc[i][j][e];
+          float v = acc[i][j][e] + bv[i][e];
           if (!RES && relu) v = relu_f(v);
           o4[e] = from_f32<bf16>(v);
         }
@@ -671,20 +693,21 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
 
   // ---- prologue: stage 0 landed and its first half read, stage 1 in flight ----
   issue(0);
-  load_bias(tile_of(0));
+  load_bias(tile_of(0), 0);
   vm_lgkm_wait<0>();
   bare_barrier();
   issue(1);
   bf16x8 w0[8], a0[8], w1[8], a1[8];
   read_frags(0, fp0, w0, a0);
-  init_acc();
 
-  auto mfma_half = [&](bf16x8 (&wf)[8], bf16x8 (&af)[8]) {
+  auto mfma_half = [&](bf16x8 (&wf)[8], bf16x8 (&af)[8], auto first_tag) {
+    constexpr bool kFirst = decltype(first_tag)::value;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
+                                                            0, 0, 0);
   };
   auto interleave = [&]() {
 #pragma unroll
@@ -697,24 +720,35 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   // wait for stage s + 1 (behind it only the epilogue of a tile that ended at
   // s - 1), refill slot s & 1 with stage s + 2; second half's MFMAs with stage
   // s + 1's first-half fragments read in between
-  auto step = [&](bool after_epi, int s) {
+  //
+  // The last stage of a tile does not read the next stage's fragments: they are read
+  // after the epilogue, so that 64 fragment registers are free while it runs.
+  using yes = std::true_type;
+  using no = std::false_type;
+  auto step = [&](bool after_epi, int s, auto first_tag, auto last_tag) {
+    constexpr bool kLast = decltype(last_tag)::value;
     read_frags(s, fp1, w1, a1);
-    mfma_half(w0, a0);
+    mfma_half(w0, a0, first_tag);
     interleave();
     if (after_epi) vm_lgkm_wait<(E > 63 ? 63 : E)>();
     else vm_lgkm_wait<0>();
     bare_barrier();
     issue(s + 2);
-    read_frags(s + 1, fp0, w0, a0);
-    mfma_half(w1, a1);
-    interleave();
+    if constexpr (!kLast) read_frags(s + 1, fp0, w0, a0);
+    mfma_half(w1, a1, no{});
+    if constexpr (!kLast) interleave();
   };
   for (int ti = 0; ti < my_tiles; ++ti) {
-    step(ti > 0, ti * KS);
-    for (int ks = 1; ks < KS; ++ks) step(false, ti * KS + ks);
-    epilogue(tile_of(ti));
-    load_bias(tile_of(ti + 1 < my_tiles ? ti + 1 : ti));
-    init_acc();
+    if (KS == 1) {
+      step(ti > 0, ti * KS, yes{}, yes{});
+    } else {
+      step(ti > 0, ti * KS, yes{}, no{});
+      for (int ks = 1; ks < KS - 1; ++ks) step(false, ti * KS + ks, no{}, no{});
+      step(false, ti * KS + KS - 1, no{}, yes{});
+    }
+    epilogue(tile_of(ti), ti);
+    load_bias(tile_of(ti + 1 < my_tiles ? ti + 1 : ti), (ti + 1) & 1);
+    read_frags((ti + 1) * KS, fp0, w0, a0);
   }
 }
 
@@ -736,10 +770,10 @@ int32_t launch_xl(GemmParams p, hipStream_t st) {
   p.fd_ks = make_fastdiv(static_cast<uint32_t>(p.k / kXlBK));
   p.fd_tpm = make_fastdiv(static_cast<uint32_t>(p.tiles_m * p.tiles_o));
   p.fd_tm = make_fastdiv(static_cast<uint32_t>(p.tiles_m));
-  if (p.r)
-    gemm_xlp_kernel<TB, true><<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
-  else
-    gemm_xlp_kernel<TB, false><<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
+  const bool relu = p.act == WC_ACT_RELU;
+  auto kern = p.r ? (relu ? gemm_xlp_kernel<TB, true, true> : gemm_xlp_kernel<TB, true, false>)
+                  : (relu ? gemm_xlp_kernel<TB, false, true> : gemm_xlp_kernel<TB, false, false>);
+  kern<<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
   return check_launch("wc_grouped_gemm");
 }
 
