@@ -316,6 +316,31 @@ typedef struct wc_conv_args {
 int32_t wc_conv2d(const wc_conv_args* args, void* stream);
 
 /*
+ * Grouped 3-D convolution -- replaces the permute/reshape + grouped nn.Conv3d +
+ * permute().contiguous() of WideConv3d.forward (wide_compiler/core/primitives/
+ * wide_conv3d.py:102-124):
+ *   y = act(conv3d(x, W) + bias)
+ * x: [n, batch, c_in, d, h, w] with each (i, b) block [c_in, d, h, w] contiguous
+ * (strides x_stride_n, x_stride_b); y likewise with [c_out, d_out, h_out, w_out]
+ * blocks.  packed_weight from wc_conv_pack_weights(w, n, c_out, c_in, kd * kh, kw, ...)
+ * on the grouped filter bank [n*c_out, c_in, kd, kh, kw]; bias [n*c_out] of
+ * param_dtype or NULL.  dtype in {WC_F32, WC_BF16}; fp32 accumulation on MFMA.
+ */
+typedef struct wc_conv3d_args {
+  int32_t dtype, param_dtype, act;
+  int64_t n, batch, c_in, c_out, d, h, w, kd, kh, kw;
+  int64_t stride_d, stride_h, stride_w, pad_d, pad_h, pad_w, dil_d, dil_h, dil_w, d_out, h_out, w_out;
+  const void* x;
+  int64_t x_stride_n, x_stride_b;
+  const void* packed_weight;
+  const void* bias;
+  void* y;
+  int64_t y_stride_n, y_stride_b;
+} wc_conv3d_args;
+
+int32_t wc_conv3d(const wc_conv3d_args* args, void* stream);
+
+/*
  * Fused multi-head attention core -- replaces the view/permute/reshape to
  * [N*B, H, T, Dh], F.scaled_dot_product_attention and the permute back of
  * WideAttention._forward_fused (wide_compiler/core/primitives/wide_attention.py:

@@ -86,6 +86,16 @@ def conv2d(x: Tensor, weight: Tensor, bias: Optional[Tensor], n: int, stride=(1,
     return out.view(b, n, nco // n, ho, wo).permute(1, 0, 2, 3, 4).contiguous()
 
 
+def conv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], n: int, stride=(1, 1, 1), padding=(0, 0, 0),
+           dilation=(1, 1, 1)) -> Tensor:
+    """WideConv3d.forward (grouped strategy), wide_conv3d.py:102-124; weight [N*Co, Ci, kd, kh, kw]."""
+    nn_, b, c, d, h, w = x.shape
+    xp = x.permute(1, 0, 2, 3, 4, 5).reshape(b, n * c, d, h, w)
+    out = F.conv3d(xp, weight, bias, stride=stride, padding=padding, dilation=dilation, groups=n)
+    b, nco, do, ho, wo = out.shape
+    return out.view(b, n, nco // n, do, ho, wo).permute(1, 0, 2, 3, 4, 5).contiguous()
+
+
 def conv1d(x: Tensor, weight: Tensor, bias: Optional[Tensor], n: int, stride: int = 1, padding: int = 0,
            dilation: int = 1) -> Tensor:
     """WideConv1d.forward (grouped strategy), wide_conv1d.py:125-141; weight [N*Co, Ci, k]."""

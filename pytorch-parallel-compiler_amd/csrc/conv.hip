@@ -25,6 +25,10 @@ namespace {
 
 struct ConvParams {
   int n, batch, ci, co, h, w, kh, kw, sh, sw, ph, pw, dh, dw, ho, wo;
+  // depth of a 3-D convolution (2-D: kd = d = dout = 1, sd = dd = 1, pd = 0); only the
+  // general kernel reads them.  x_cs / y_cs: channel-plane strides (d*h*w, dout*ho*wo).
+  int kd, sd, pd, dd, d, dout;
+  int64_t x_cs, y_cs;
   int ci32;                 // input channels padded to a multiple of 32
   int cc;                   // input channels staged per LDS chunk (multiple of 32)
   int tr, tc;               // output tile rows / cols
@@ -98,7 +102,7 @@ __device__ __forceinline__ void conv_affine(const ConvParams& p, int mdl, int co
 template <typename T, int FM>
 __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const f32x4 (&acc)[FM][kFN], T* xs, int mdl,
                                               int bb, int ho0, int wo0, int co0, const float (&alpha)[kFN],
-                                              const float (&beta)[kFN]) {
+                                              const float (&beta)[kFN], int od = 0) {
   constexpr int TPIX = 4 * FM * 16;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -119,9 +123,10 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const f32x4 (
   __syncthreads();
 
   // ---- epilogue 2: residual + activation, coalesced NCHW stores ----
-  T* yb = static_cast<T*>(p.y) + mdl * p.y_sn + bb * p.y_sb;
-  const T* rb = p.res ? static_cast<const T*>(p.res) + mdl * p.r_sn + bb * p.r_sb : nullptr;
-  const int how = p.ho * p.wo;
+  const int64_t dpl = static_cast<int64_t>(od) * p.ho * p.wo;   // output depth slice
+  T* yb = static_cast<T*>(p.y) + mdl * p.y_sn + bb * p.y_sb + dpl;
+  const T* rb = p.res ? static_cast<const T*>(p.res) + mdl * p.r_sn + bb * p.r_sb + dpl : nullptr;
+  const int64_t how = p.y_cs;                                    // channel-plane stride
   constexpr int VE = 16 / sizeof(T);
   if (p.vec_out) {
     // tc % VE == 0, wo0 % VE == 0, rows of y / res 16-byte aligned; EB chunks per
@@ -192,17 +197,19 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
 
   // ---- tile coordinates ----
   const int per_img = p.tiles_r * p.tiles_c * p.tiles_co;
-  const int nblk = p.n * p.batch * per_img;
+  const int nblk = p.n * p.batch * p.dout * per_img;
   int bid = blockIdx.x;
   if (p.remap) bid = (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3);
-  const int img = bid / per_img;                      // (model, image)
+  const int img = bid / per_img;                      // (model, image, output depth)
   int rem = bid - img * per_img;
   const int tco = rem / (p.tiles_r * p.tiles_c);
   rem -= tco * (p.tiles_r * p.tiles_c);
   const int trr = rem / p.tiles_c;
   const int tcc = rem - trr * p.tiles_c;
-  const int mdl = img / p.batch;
-  const int bb = img - mdl * p.batch;
+  const int mdl = img / (p.batch * p.dout);
+  const int bd = img - mdl * (p.batch * p.dout);
+  const int bb = bd / p.dout;
+  const int od = bd - bb * p.dout;
   const int ho0 = trr * p.tr, wo0 = tcc * p.tc, co0 = tco * 64;
   const int hi0 = ho0 * p.sh - p.ph, wi0 = wo0 * p.sw - p.pw;
 
@@ -211,7 +218,8 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
   const int fr = lane & 15, fk = (lane >> 4) * 8;
 
   const T* xb = static_cast<const T*>(p.x) + mdl * p.x_sn + bb * p.x_sb;
-  const T* wb = static_cast<const T*>(p.wp) + static_cast<int64_t>(mdl) * p.co * p.kh * p.kw * p.ci32;
+  const int taps_all = p.kd * p.kh * p.kw;
+  const T* wb = static_cast<const T*>(p.wp) + static_cast<int64_t>(mdl) * p.co * taps_all * p.ci32;
 
   // LDS offset (elements, tap (0,0), channel fk) of each A-fragment pixel
   int aoff[FM];
@@ -227,7 +235,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
 #pragma unroll
   for (int j = 0; j < kFN; ++j) {
     const int co = co0 + j * 16 + fr;
-    wrow[j] = (co < p.co) ? wb + static_cast<int64_t>(co) * p.kh * p.kw * p.ci32 + fk : nullptr;
+    wrow[j] = (co < p.co) ? wb + static_cast<int64_t>(co) * taps_all * p.ci32 + fk : nullptr;
   }
 
   f32x4 acc[FM][kFN];
@@ -237,11 +245,17 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
     for (int j = 0; j < kFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int taps = p.kh * p.kw;
+  bool staged = false;
+  // depth taps (one for 2-D): input depth slice di; slices outside the input add zero
+  for (int t = 0; t < p.kd; ++t) {
+  const int di = od * p.sd - p.pd + t * p.dd;
+  if (di < 0 || di >= p.d) continue;                  // uniform over the workgroup
   for (int c0 = 0; c0 < p.ci32; c0 += p.cc) {
     // ---- stage input channels [c0, c0+cc) of the tile as [row][col][ci] ----
     // unit = (group of 8 channels, tile pixel): 8 loads (consecutive lanes read
     // consecutive pixels of one channel plane -> coalesced), one 16-byte LDS store.
-    if (c0 > 0) __syncthreads();
+    if (staged) __syncthreads();
+    staged = true;
     {
       const int plane = p.ir * p.ic;
       const int units = (p.cc >> 3) * plane;
@@ -260,8 +274,8 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
             const int col = rc - r * p.ic;
             const int hi = hi0 + r, wi = wi0 + col, ch0 = c0 + cg * 8;
             const bool in = hi >= 0 && hi < p.h && wi >= 0 && wi < p.w;
-            const T* src = xb + (static_cast<int64_t>(ch0) * p.h + hi) * p.w + wi;
-            const int64_t cstride = static_cast<int64_t>(p.h) * p.w;
+            const T* src = xb + static_cast<int64_t>(ch0) * p.x_cs + (static_cast<int64_t>(di) * p.h + hi) * p.w + wi;
+            const int64_t cstride = p.x_cs;
 #pragma unroll
             for (int q = 0; q < 8; ++q)
               v[u][q] = (in && ch0 + q < p.ci) ? src[q * cstride] : from_f32<T>(0.f);
@@ -287,7 +301,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
     auto bload = [&](int ks, uint4* dst) {
       const int tap = ks / (p.cc / 32);
       const int cs = ks - tap * (p.cc / 32);
-      const int64_t koff = static_cast<int64_t>(tap) * p.ci32 + c0 + cs * 32;
+      const int64_t koff = static_cast<int64_t>(t * taps + tap) * p.ci32 + c0 + cs * 32;
 #pragma unroll
       for (int j = 0; j < kFN; ++j) {
         if (sizeof(T) == 2) {
@@ -340,11 +354,12 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
       }
     }
   }
+  }
 
   float alpha[kFN], beta[kFN];
   conv_affine(p, mdl, co0, alpha, beta);
   __syncthreads();
-  conv_epilogue<T, FM>(p, acc, xs, mdl, bb, ho0, wo0, co0, alpha, beta);
+  conv_epilogue<T, FM>(p, acc, xs, mdl, bb, ho0, wo0, co0, alpha, beta, od);
 }
 
 // ---------------------------------------------------------------------------
@@ -1293,6 +1308,10 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   p.y = a->y;
   p.y_sn = a->y_stride_n;
   p.y_sb = a->y_stride_b;
+  p.kd = p.sd = p.dd = p.d = p.dout = 1;
+  p.pd = 0;
+  p.x_cs = static_cast<int64_t>(p.h) * p.w;
+  p.y_cs = static_cast<int64_t>(p.ho) * p.wo;
   const bool f32 = a->dtype == WC_F32;
   if (!(f32 ? conv_plan<float>(p) : conv_plan<bf16>(p)))
     return set_error(WC_ERR_LIMIT, "wc_conv2d: tile does not fit in LDS");
@@ -1349,6 +1368,94 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
     }
   }
   const dim3 grid(static_cast<uint32_t>(nblk));
+  if (f32) return launch_big_lds(conv_kernel<float>, p, grid, lds, st);
+  return launch_big_lds(conv_kernel<bf16>, p, grid, lds, st);
+}
+
+extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
+  clear_error();
+  WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_conv3d: null args");
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "wc_conv3d: unsupported dtype %s",
+             dtype_name(a->dtype));
+  WC_REQUIRE(a->param_dtype == WC_F32 || a->param_dtype == a->dtype, WC_ERR_DTYPE,
+             "wc_conv3d: parameter dtype %s", dtype_name(a->param_dtype));
+  WC_REQUIRE(a->act == WC_ACT_NONE || a->act == WC_ACT_RELU, WC_ERR_ARG, "wc_conv3d: bad act %d", a->act);
+  WC_REQUIRE(a->n >= 0 && a->batch >= 0 && a->c_in > 0 && a->c_out >= 0 && a->d > 0 && a->h > 0 && a->w > 0 &&
+                 a->kd > 0 && a->kh > 0 && a->kw > 0 && a->stride_d > 0 && a->stride_h > 0 && a->stride_w > 0 &&
+                 a->pad_d >= 0 && a->pad_h >= 0 && a->pad_w >= 0 && a->dil_d > 0 && a->dil_h > 0 && a->dil_w > 0,
+             WC_ERR_SHAPE, "wc_conv3d: bad sizes");
+  const int64_t dout = (a->d + 2 * a->pad_d - a->dil_d * (a->kd - 1) - 1) / a->stride_d + 1;
+  const int64_t ho = (a->h + 2 * a->pad_h - a->dil_h * (a->kh - 1) - 1) / a->stride_h + 1;
+  const int64_t wo = (a->w + 2 * a->pad_w - a->dil_w * (a->kw - 1) - 1) / a->stride_w + 1;
+  WC_REQUIRE(dout == a->d_out && ho == a->h_out && wo == a->w_out, WC_ERR_SHAPE,
+             "wc_conv3d: output %lldx%lldx%lld does not match the geometry (%lldx%lldx%lld)", (long long)a->d_out,
+             (long long)a->h_out, (long long)a->w_out, (long long)dout, (long long)ho, (long long)wo);
+  if (a->n == 0 || a->batch == 0 || a->c_out == 0 || dout <= 0 || ho <= 0 || wo <= 0) return WC_OK;
+  WC_REQUIRE(a->x && a->packed_weight && a->y, WC_ERR_NULL, "wc_conv3d: null pointer");
+  WC_REQUIRE(a->c_in * a->d * a->h * a->w < 0x7fffffffll && a->c_out * dout * ho * wo < 0x7fffffffll &&
+                 a->n * a->c_out < 0x7fffffffll && a->kd * a->kh * a->kw < 0x10000,
+             WC_ERR_LIMIT, "wc_conv3d: sizes too large");
+  ConvParams p;
+  p.n = (int)a->n;
+  p.batch = (int)a->batch;
+  p.ci = (int)a->c_in;
+  p.co = (int)a->c_out;
+  p.h = (int)a->h;
+  p.w = (int)a->w;
+  p.kh = (int)a->kh;
+  p.kw = (int)a->kw;
+  p.sh = (int)a->stride_h;
+  p.sw = (int)a->stride_w;
+  p.ph = (int)a->pad_h;
+  p.pw = (int)a->pad_w;
+  p.dh = (int)a->dil_h;
+  p.dw = (int)a->dil_w;
+  p.ho = (int)ho;
+  p.wo = (int)wo;
+  p.kd = (int)a->kd;
+  p.sd = (int)a->stride_d;
+  p.pd = (int)a->pad_d;
+  p.dd = (int)a->dil_d;
+  p.d = (int)a->d;
+  p.dout = (int)dout;
+  p.x_cs = a->d * a->h * a->w;
+  p.y_cs = dout * ho * wo;
+  p.act = a->act;
+  p.x = a->x;
+  p.x_sn = a->x_stride_n;
+  p.x_sb = a->x_stride_b;
+  p.wp = a->packed_weight;
+  p.bias = a->bias;
+  p.bn_w = p.bn_b = p.bn_mean = p.bn_var = nullptr;
+  p.bn_eps = 0.f;
+  p.pdt = a->param_dtype;
+  p.res = nullptr;
+  p.r_sn = p.r_sb = 0;
+  p.y = a->y;
+  p.y_sn = a->y_stride_n;
+  p.y_sb = a->y_stride_b;
+  const bool f32 = a->dtype == WC_F32;
+  if (!(f32 ? conv_plan<float>(p) : conv_plan<bf16>(p)))
+    return set_error(WC_ERR_LIMIT, "wc_conv3d: tile does not fit in LDS");
+  p.fd_plane = make_fastdiv(static_cast<uint32_t>(p.ir * p.ic));
+  p.fd_ic = make_fastdiv(static_cast<uint32_t>(p.ic));
+  p.tiles_r = static_cast<int>(cdiv(p.ho, p.tr));
+  p.tiles_c = static_cast<int>(cdiv(p.wo, p.tc));
+  p.tiles_co = static_cast<int>(cdiv(p.co, 64));
+  const int es = f32 ? 4 : 2;
+  const int ve = 16 / es;
+  const bool yal = aligned(p.y, 16) && (p.y_sn * es) % 16 == 0 && (p.y_sb * es) % 16 == 0 &&
+                   (p.y_cs * es) % 16 == 0 && (static_cast<int64_t>(p.ho) * p.wo * es) % 16 == 0;
+  p.vec_out = (yal && p.tc % ve == 0 && p.wo % ve == 0) ? 1 : 0;
+  WC_REQUIRE(aligned(p.wp, 16), WC_ERR_ALIGN, "wc_conv3d: packed weights not 16-byte aligned");
+  const int64_t nblk = static_cast<int64_t>(p.n) * p.batch * p.dout * p.tiles_r * p.tiles_c * p.tiles_co;
+  WC_REQUIRE(nblk < 0x7fffffffll, WC_ERR_LIMIT, "wc_conv3d: too many tiles");
+  p.remap = (nblk % 8 == 0) ? 1 : 0;
+  const size_t in = static_cast<size_t>(p.ir) * p.ic * (p.cc + (f32 ? 4 : 8)) * es;
+  const size_t epi = static_cast<size_t>(64) * (4 * (f32 ? 4 : 8) * 16 + 8) * es;
+  const size_t lds = in > epi ? in : epi;
+  const dim3 grid(static_cast<uint32_t>(nblk));
+  hipStream_t st = as_stream(stream);
   if (f32) return launch_big_lds(conv_kernel<float>, p, grid, lds, st);
   return launch_big_lds(conv_kernel<bf16>, p, grid, lds, st);
 }

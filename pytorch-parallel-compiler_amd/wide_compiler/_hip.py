@@ -103,6 +103,22 @@ class _ConvArgs(ctypes.Structure):
     ]
 
 
+class _Conv3dArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("param_dtype", ctypes.c_int32), ("act", ctypes.c_int32),
+        ("n", ctypes.c_int64), ("batch", ctypes.c_int64), ("c_in", ctypes.c_int64), ("c_out", ctypes.c_int64),
+        ("d", ctypes.c_int64), ("h", ctypes.c_int64), ("w", ctypes.c_int64),
+        ("kd", ctypes.c_int64), ("kh", ctypes.c_int64), ("kw", ctypes.c_int64),
+        ("stride_d", ctypes.c_int64), ("stride_h", ctypes.c_int64), ("stride_w", ctypes.c_int64),
+        ("pad_d", ctypes.c_int64), ("pad_h", ctypes.c_int64), ("pad_w", ctypes.c_int64),
+        ("dil_d", ctypes.c_int64), ("dil_h", ctypes.c_int64), ("dil_w", ctypes.c_int64),
+        ("d_out", ctypes.c_int64), ("h_out", ctypes.c_int64), ("w_out", ctypes.c_int64),
+        ("x", ctypes.c_void_p), ("x_stride_n", ctypes.c_int64), ("x_stride_b", ctypes.c_int64),
+        ("packed_weight", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p), ("y_stride_n", ctypes.c_int64), ("y_stride_b", ctypes.c_int64),
+    ]
+
+
 class _AttnArgs(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
@@ -141,6 +157,7 @@ SIGNATURES = {
     "wc_conv_pack_weights": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P]),
     "wc_conv_packed_weight_elems": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "wc_conv2d": (_I32, [ctypes.POINTER(_ConvArgs), _P]),
+    "wc_conv3d": (_I32, [ctypes.POINTER(_Conv3dArgs), _P]),
     "wc_attention": (_I32, [ctypes.POINTER(_AttnArgs), _P]),
 }
 
@@ -376,6 +393,27 @@ def conv2d(*, x: Tensor, packed_w: Tensor, n: int, c_in: int, c_out: int, kernel
         a.residual, a.r_stride_n, a.r_stride_b = residual.data_ptr(), residual.stride(0), residual.stride(1)
     a.y, a.y_stride_n, a.y_stride_b = y.data_ptr(), y.stride(0), y.stride(1)
     _check(lib().wc_conv2d(ctypes.byref(a), stream_of(x)), "wc_conv2d")
+
+
+def conv3d(*, x: Tensor, packed_w: Tensor, n: int, c_in: int, c_out: int, kernel, stride, padding, dilation,
+           y: Tensor, bias: Optional[Tensor] = None, relu: bool = False) -> None:
+    """x / y are [n, b, C, D, H, W] with dense [C, D, H, W] blocks."""
+    a = _Conv3dArgs()
+    a.dtype = dtype_code(x.dtype, "conv3d")
+    a.param_dtype = dtype_code(bias.dtype, "conv3d") if bias is not None else a.dtype
+    a.act = ACT_RELU if relu else ACT_NONE
+    a.n, a.batch, a.c_in, a.c_out = n, x.shape[1], c_in, c_out
+    a.d, a.h, a.w = x.shape[3], x.shape[4], x.shape[5]
+    a.kd, a.kh, a.kw = kernel
+    a.stride_d, a.stride_h, a.stride_w = stride
+    a.pad_d, a.pad_h, a.pad_w = padding
+    a.dil_d, a.dil_h, a.dil_w = dilation
+    a.d_out, a.h_out, a.w_out = y.shape[3], y.shape[4], y.shape[5]
+    a.x, a.x_stride_n, a.x_stride_b = x.data_ptr(), x.stride(0), x.stride(1)
+    a.packed_weight = packed_w.data_ptr()
+    a.bias = ptr(bias)
+    a.y, a.y_stride_n, a.y_stride_b = y.data_ptr(), y.stride(0), y.stride(1)
+    _check(lib().wc_conv3d(ctypes.byref(a), stream_of(x)), "wc_conv3d")
 
 
 def attention(*, q: Tensor, k: Tensor, v: Tensor, o: Tensor, nb: int, heads: int, sq: int, skv: int,

@@ -237,3 +237,47 @@ def test_resblock_config_n100(hip):
         pk = {kk: (v.double() if torch.is_tensor(v) else v) for kk, v in _params([mods[k].cpu()]).items()}
         exact = wide_ref.resblock_wide(x[:, k * c:(k + 1) * c].double(), 1, pk)
         assert rel_err(y[:, k * c:(k + 1) * c], exact) <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n,b,ci,co,dhw,k,stride,pad,dil", [
+    (4, 2, 8, 16, (6, 10, 12), 3, 1, 1, 1),
+    (3, 1, 3, 70, (5, 7, 9), (1, 3, 3), 1, (0, 1, 1), 1),       # 2 output-channel tiles, C_in < 32
+    (2, 2, 40, 24, (7, 8, 6), (3, 1, 1), (2, 1, 1), (1, 0, 0), 1),
+    (2, 1, 16, 8, (9, 9, 9), 3, 2, 2, 2),                       # depth taps past both ends skipped
+    (2, 2, 32, 32, (4, 16, 16), (2, 3, 3), 1, (0, 1, 1), 1),
+])
+def test_conv3d(hip, dtype, n, b, ci, co, dhw, k, stride, pad, dil):
+    import wide_compiler as wc
+    torch.manual_seed(500)
+    mods = [nn.Conv3d(ci, co, k, stride=stride, padding=pad, dilation=dil).to(dtype) for _ in range(n)]
+    wide = wc.WideConv3d.from_modules([m.to(DEV) for m in mods])
+    assert set(wide.state_dict()) == {"conv.weight", "conv.bias"}
+    x = _rand((n, b, ci) + dhw, gen(501), dtype)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    w, bias = wide.conv.weight.detach().cpu(), wide.conv.bias.detach().cpu()
+    c = wide.conv
+    exact = wide_ref.conv3d(x.double(), w.double(), bias.double(), n, c.stride, c.padding, c.dilation)
+    assert rel_err(y, exact) <= tol(dtype)
+    if dtype == torch.bfloat16:    # the reference's own bf16 path (CPU)
+        assert rel_err(y, wide_ref.conv3d(x, w, bias, n, c.stride, c.padding, c.dilation)) <= TOL_BF16
+
+
+def test_conv3d_sequential_matches_grouped_and_relu(hip):
+    import wide_compiler as wc
+    torch.manual_seed(502)
+    n, ci, co = 3, 6, 10
+    mods = [nn.Conv3d(ci, co, 3, padding=1, bias=False).to(DEV) for _ in range(n)]
+    grouped = wc.WideConv3d.from_modules(mods)
+    seq = wc.WideConv3d.from_modules(mods, strategy="sequential")
+    assert seq.strategy.value == "sequential" and len(seq.convs) == n
+    x = torch.randn(n, 2, ci, 4, 5, 6, generator=gen(503)).to(DEV)
+    with torch.no_grad():
+        yg = grouped(x)
+        assert torch.equal(yg, seq(x))
+        grouped.fused_activation = "relu"
+        assert torch.equal(grouped(x), F.relu(yg))
+    for i in range(n):
+        with torch.no_grad():
+            assert rel_err(yg[i].cpu(), mods[i].cpu()(x[i].cpu())) <= TOL_F32

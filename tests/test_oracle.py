@@ -139,6 +139,31 @@ def test_layernorm_vs_f_layer_norm():
         assert torch.allclose(y[i], exp, atol=1e-12)
 
 
+def test_conv3d_vs_per_model_and_brute_force():
+    g = gen(53)
+    n, b, ci, co = 2, 2, 3, 4
+    torch.manual_seed(53)
+    mods = [nn.Conv3d(ci, co, (2, 3, 2), stride=(1, 2, 1), padding=(1, 1, 0), dilation=(2, 1, 1)).double()
+            for _ in range(n)]
+    x = torch.randn(n, b, ci, 4, 5, 3, generator=g, dtype=torch.float64)
+    w = torch.cat([m.weight for m in mods]).detach()
+    bias = torch.cat([m.bias for m in mods]).detach()
+    y = wide_ref.conv3d(x, w, bias, n, (1, 2, 1), (1, 1, 0), (2, 1, 1))
+    for i in range(n):
+        assert torch.allclose(y[i], mods[i](x[i]), atol=1e-12)
+    # brute force for model 1, batch 0, output channel 2 at a few positions
+    xp = F.pad(x[1, 0], (0, 0, 1, 1, 1, 1))
+    wt = mods[1].weight.detach()
+    for (od, oh, ow) in [(0, 0, 0), (1, 2, 1), (2, 1, 0)]:
+        acc = mods[1].bias[2].item()
+        for c in range(ci):
+            for t in range(2):
+                for r in range(3):
+                    for q in range(2):
+                        acc += wt[2, c, t, r, q].item() * xp[c, od + 2 * t, oh * 2 + r, ow + q].item()
+        assert abs(acc - y[1, 0, 2, od, oh, ow].item()) < 1e-10
+
+
 def test_group_norm_vs_nn_group_norm():
     g = gen(51)
     n, b, c, groups = 3, 2, 6, 3
