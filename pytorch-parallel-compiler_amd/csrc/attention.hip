@@ -295,6 +295,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 // Scores are scaled by log2(e)/sqrt(Dh) inside the exp2 argument (one FMA).
 // ---------------------------------------------------------------------------
 constexpr float kLazyRescale = 8.0f;
+constexpr bf16x2 kOnes2 = {bf16(1.0f), bf16(1.0f)};
 
 // (v of this lane, v of lane l ^ 32) via v_permlane32_swap on an opaque copy:
 // the compiler folds the intrinsic when both operands are the same value, so
@@ -471,12 +472,18 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
       bf16x8 pf[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = static_cast<bf16>(pv[r]);
-      float ps[8];
+      // row sum of the bf16-rounded P that P V uses: v_dot2_f32_bf16 against (1, 1), two
+      // bf16 values per instruction on two independent chains
+      float l0 = 0.f, l1 = 0.f;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) ps[r] = pv[2 * r] + pv[2 * r + 1];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ps[r] += ps[r + 4];
-      lrun[b] += (ps[0] + ps[2]) + (ps[1] + ps[3]);
+      for (int r = 0; r < 8; ++r) {
+        const bf16x2 pair = {pf[r >> 2][2 * (r & 3)], pf[r >> 2][2 * (r & 3) + 1]};
+        if (r & 1)
+          l1 = __builtin_amdgcn_fdot2_f32_bf16(pair, kOnes2, l1, false);
+        else
+          l0 = __builtin_amdgcn_fdot2_f32_bf16(pair, kOnes2, l0, false);
+      }
+      lrun[b] += l0 + l1;
 #pragma unroll
       for (int d = 0; d < DT; ++d)
 #pragma unroll
