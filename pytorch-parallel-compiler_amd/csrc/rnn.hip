@@ -523,12 +523,12 @@ size_t step_lds_bytes(int hid) {
 using namespace wc;
 
 // Chooses the lane layout of the register-resident kernel; false when the
-// weights of one (model, batch row) do not fit the register file.
-// Pick the lane shape of the persistent kernel.  Per step every SIMD issues,
-// for each of its waves, the lane's GATES*UPG*KL FMAs, KL/4 LDS reads,
-// GATES*UPG*log2(LG) DPP adds and a roughly fixed cell update (~60 issue
-// slots with its transcendentals); the shape with the fewest slots on the
-// busiest SIMD wins.  Weight registers stay <= 176 per lane (no spills).
+// weights of one (model, batch row) do not fit the register file.  Per step
+// every SIMD issues, for each of its waves, the lane's GATES*UPG*KL FMAs,
+// KL/4 LDS reads (each costed as 6 slots), GATES*UPG*log2(LG) DPP adds and a
+// roughly fixed cell update (~60 issue slots with its transcendentals); the
+// shape with the fewest slots on the busiest SIMD wins.  Weight registers stay
+// <= 176 per lane (no spills).
 static bool rnn_plan(int gates, int hid, RnnParams& p) {
   static const int kShapes[][3] = {   // {LG, UPG, KL}: the instantiated kernels
       {16, 1, 4}, {16, 2, 4}, {16, 4, 4}, {16, 1, 8}, {16, 2, 8}, {16, 4, 8}, {16, 1, 16}, {16, 2, 16},
@@ -546,7 +546,10 @@ static bool rnn_plan(int gates, int hid, RnnParams& p) {
     const int waves_per_simd = (threads / 64 + 3) / 4;
     int lg2 = 0;
     while ((1 << lg2) < lg) ++lg2;
-    const long cost = static_cast<long>(waves_per_simd) * (regs + kl / 4 + gates * upg * lg2 + 60);
+    // LDS reads: a wave's 16-byte read moves 1 KB through the CU's shared LDS port, about
+    // 6 VALU issue slots' worth of time (measured: for GRU H = 128, 8 lanes x 2 units x 16
+    // columns runs 6% faster than 4 x 1 x 32, which a 1-slot read cost would have picked)
+    const long cost = static_cast<long>(waves_per_simd) * (regs + 6 * (kl / 4) + gates * upg * lg2 + 60);
     if (best < 0 || cost < best) {
       best = cost;
       p.lg = lg;
