@@ -683,8 +683,9 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
             o[e] = from_f32<bf16>(v);
           }
         }
+        // non-temporal (nt): the output streams past the L2s, which keep the operand tiles
         __builtin_amdgcn_raw_buffer_store_b128(
-            outv, crs, strip_ok ? cbase + static_cast<uint32_t>(lr * p.c_si) * 2u : kXlOob, 0, 0);
+            outv, crs, strip_ok ? cbase + static_cast<uint32_t>(lr * p.c_si) * 2u : kXlOob, 0, 2);
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);          // strip reads done before it is rewritten
       __builtin_amdgcn_wave_barrier();
