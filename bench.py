@@ -341,7 +341,7 @@ def cfg_seq(dev, steps, warmup) -> Dict:
             t_emb = _event_time(lambda: wide.emb(ids, per_model=True), 10, 2)
             t_ln = _event_time(lambda: wide.ln(x), 10, 2)
         flops = 2.0 * n * b * t * hdim * v
-        return {"bound": "mfma", "kernel": "gemm_kernel (vocab projection 512 -> 8192 + bias, bf16)",
+        return {"bound": "mfma", "kernel": "gemm_xlp_kernel (vocab projection 512 -> 8192 + bias, bf16)",
                 "flops_per_launch": flops, "sec": t_fc, "peak": PEAK["bf16_mfma"],
                 "other_kernels_us": {"lstm_recurrence_128_steps": t_rec * 1e6,
                                      "lstm_input_projection_gemm": t_proj * 1e6,
