@@ -486,6 +486,26 @@ __device__ __forceinline__ void bare_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// One LDS-DMA instruction of a stage: block q < 8 moves W rows r0 + 64 wave + 8 q,
+// block q >= 8 A rows r0 + 64 wave + 8 (q - 8) (r0 = the tile's first column / row),
+// 128 bytes of K each, into the stage slot at `st`.  Blocks past the last row
+// reload the last 8 rows (their results are never stored).
+__device__ __forceinline__ void xl_dma_block(const GemmParams& p, const char* wmod, const char* amod, lds_char* st,
+                                             int r0, int wave, int q, uint32_t wlane, uint32_t alane) {
+  if (q < 8) {
+    const int rb = min(r0 + 64 * wave + 8 * q, p.o - 8);
+    __builtin_amdgcn_global_load_lds(wmod + static_cast<uint32_t>(rb) * static_cast<uint32_t>(p.k) * 2u + wlane,
+                                     (lds_ptr_t)(st + (64 * wave + 8 * q) * 128), 16, 0, 0);
+  } else {
+    const int rb = min(r0 + 64 * wave + 8 * (q - 8), p.m - 8);
+    const uint32_t outer = fdiv(static_cast<uint32_t>(rb), p.a_ri);
+    const uint32_t inner = rb - outer * p.a_ri.d;
+    const uint32_t off = (outer * static_cast<uint32_t>(p.a_so) + inner * static_cast<uint32_t>(p.a_si)) * 2u;
+    __builtin_amdgcn_global_load_lds(amod + off + alane, (lds_ptr_t)(st + kXlHalf + (64 * wave + 8 * (q - 8)) * 128),
+                                     16, 0, 0);
+  }
+}
+
 template <typename TB, bool RES, bool RELU>
 __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, int tiles_total) {
   __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 4 * kXlStripBytes + 2 * kXlBiasSlot];
@@ -516,47 +536,55 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   const int S = my_tiles * KS;
   if (S == 0) return;
 
-  struct Tile { int mdl, m0, o0; };
+  // A tile's K stages run in a rotated order, starting at stage (m-tile index mod
+  // KS): the workgroups that share a block of W rows (same model and column tile,
+  // consecutive m tiles, resident on one XCD at the same time) then read different
+  // K slices of it at any moment, and only the first to reach a slice misses in L2.
+  struct Tile { int mdl, m0, o0, rot; };
   auto tile_of = [&](int ti) {
     Tile t;
     const int g = t_first + ti * t_step;
     t.mdl = static_cast<int>(fdiv(static_cast<uint32_t>(g), p.fd_tpm));
     const int rem = g - t.mdl * tiles_per_model;
     const int to = static_cast<int>(fdiv(static_cast<uint32_t>(rem), p.fd_tm));
-    t.m0 = (rem - to * p.tiles_m) * kXlB;
+    const int mt = rem - to * p.tiles_m;
+    t.m0 = mt * kXlB;
     t.o0 = to * kXlB;
+    t.rot = mt - static_cast<int>(fdiv(static_cast<uint32_t>(mt), p.fd_ks)) * KS;
     return t;
   };
 
   // ---- DMA of stage `stage` into slot stage & 1 (stages past the last reload it) ----
   // Lane l of an 8-row block instruction writes LDS bytes [16 l, 16 l + 16): row
   // l >> 3, position l & 7, which receives global chunk (l & 7) ^ (l >> 3).
+  // Block q < 8 is W rows o0 + 64 wave + 8 q, block q >= 8 A rows m0 + 64 wave + 8 (q - 8).
   const uint32_t dchunk = ((lane & 7) ^ (lane >> 3)) * 8;
   const uint32_t wlane = ((lane >> 3) * static_cast<uint32_t>(p.k) + dchunk) * 2u;
   const uint32_t alane = ((lane >> 3) * static_cast<uint32_t>(p.a_si) + dchunk) * 2u;
-  auto issue = [&](int stage) {
+  // DMA source of stage `stage`: model bases of W and A at the stage's (rotated) K
+  // slice, and the tile's first rows
+  struct Dma { const char* wmod; const char* amod; int slot, o0, m0; };
+  auto dma_of = [&](int stage) {
     const int sidx = stage < S ? stage : S - 1;
     const int ti = static_cast<int>(fdiv(static_cast<uint32_t>(sidx), p.fd_ks));
-    const int ks = sidx - ti * KS;
     const Tile t = tile_of(ti);
-    const char* wmod = static_cast<const char*>(p.w) + static_cast<int64_t>(t.mdl) * p.w_sn * 2 + ks * 128;
-    const char* amod = static_cast<const char*>(p.a) + static_cast<int64_t>(t.mdl) * p.a_sn * 2 + ks * 128;
-    lds_char* st = smem + (stage & 1) * kXlStageBytes;
+    int ks = sidx - ti * KS + t.rot;
+    if (ks >= KS) ks -= KS;
+    Dma d;
+    d.wmod = static_cast<const char*>(p.w) + static_cast<int64_t>(t.mdl) * p.w_sn * 2 + ks * 128;
+    d.amod = static_cast<const char*>(p.a) + static_cast<int64_t>(t.mdl) * p.a_sn * 2 + ks * 128;
+    d.slot = (stage & 1) * kXlStageBytes;
+    d.o0 = t.o0;
+    d.m0 = t.m0;
+    return d;
+  };
+  auto dma_block = [&](const Dma& d, int q) {
+    xl_dma_block(p, d.wmod, d.amod, smem + d.slot, q < 8 ? d.o0 : d.m0, wave, q, wlane, alane);
+  };
+  auto issue = [&](int stage) {
+    const Dma d = dma_of(stage);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int rb = min(t.o0 + 64 * wave + 8 * q, p.o - 8);
-      __builtin_amdgcn_global_load_lds(wmod + static_cast<uint32_t>(rb) * static_cast<uint32_t>(p.k) * 2u + wlane,
-                                       (lds_ptr_t)(st + (64 * wave + 8 * q) * 128), 16, 0, 0);
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int rb = min(t.m0 + 64 * wave + 8 * q, p.m - 8);
-      const uint32_t outer = fdiv(static_cast<uint32_t>(rb), p.a_ri);
-      const uint32_t inner = rb - outer * p.a_ri.d;
-      const uint32_t off = (outer * static_cast<uint32_t>(p.a_so) + inner * static_cast<uint32_t>(p.a_si)) * 2u;
-      __builtin_amdgcn_global_load_lds(amod + off + alane, (lds_ptr_t)(st + kXlHalf + (64 * wave + 8 * q) * 128),
-                                       16, 0, 0);
-    }
+    for (int q = 0; q < 16; ++q) dma_block(d, q);
   };
 
   // fragment byte offsets: row = base + 16 * i + (lane & 15), chunk 4 * half + (lane >> 4)
@@ -564,12 +592,17 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   const int fp0 = (((lane >> 4)) ^ (fr & 7)) << 4;
   const int fp1 = ((4 + (lane >> 4)) ^ (fr & 7)) << 4;
   const int wfo = (ow + fr) * 128, afo = kXlHalf + (mw + fr) * 128;
-  auto read_frags = [&](int stage, int fpos, bf16x8 (&wf)[8], bf16x8 (&af)[8]) {
+  // fragment g of a K half: g < 8 is W rows ow + 16 g, g >= 8 A rows mw + 16 (g - 8)
+  auto read_frag = [&](int stage, int fpos, int g, bf16x8 (&wf)[8], bf16x8 (&af)[8]) {
     const lds_char* st = smem + (stage & 1) * kXlStageBytes + fpos;
+    if (g < 8)
+      wf[g] = *(const lds_bf16x8*)(st + wfo + g * 2048);
+    else
+      af[g - 8] = *(const lds_bf16x8*)(st + afo + (g - 8) * 2048);
+  };
+  auto read_frags = [&](int stage, int fpos, bf16x8 (&wf)[8], bf16x8 (&af)[8]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wf[i] = *(const lds_bf16x8*)(st + wfo + i * 2048);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) af[j] = *(const lds_bf16x8*)(st + afo + j * 2048);
+    for (int g = 0; g < 16; ++g) read_frag(stage, fpos, g, wf, af);
   };
 
   // ---- bias of a tile, in accumulator layout: columns o0 + ow + 16 i + 4 (lane >> 4) + e ----
@@ -726,6 +759,21 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   // after the epilogue, so that 64 fragment registers are free while it runs.
   using yes = std::true_type;
   using no = std::false_type;
+  //
+  // The 16 DMA instructions of stage s + 2 are spread over the second half's MFMAs
+  // (program order DMA g, fragment read g; the scheduler puts two MFMAs between
+  // them): issued back to back they stall the wave while the address unit
+  // drains them, and no MFMA issues meanwhile.
+  auto interleave_dma = [&](auto reads_tag) {
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);     // one DMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);     // two MFMAs
+      if constexpr (decltype(reads_tag)::value)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one fragment read
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);     // two MFMAs
+    }
+  };
   auto step = [&](bool after_epi, int s, auto first_tag, auto last_tag) {
     constexpr bool kLast = decltype(last_tag)::value;
     read_frags(s, fp1, w1, a1);
@@ -734,10 +782,17 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
     if (after_epi) vm_lgkm_wait<(E > 63 ? 63 : E)>();
     else vm_lgkm_wait<0>();
     bare_barrier();
-    issue(s + 2);
-    if constexpr (!kLast) read_frags(s + 1, fp0, w0, a0);
+    {
+      const Dma d = dma_of(s + 2);
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        dma_block(d, g);
+        if constexpr (!kLast) read_frag(s + 1, fp0, g, w0, a0);
+      }
+    }
     mfma_half(w1, a1, no{});
-    if constexpr (!kLast) interleave();
+    if constexpr (kLast) interleave_dma(no{});
+    else interleave_dma(yes{});
   };
   for (int ti = 0; ti < my_tiles; ++ti) {
     if (KS == 1) {
