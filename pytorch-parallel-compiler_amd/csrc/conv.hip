@@ -1087,14 +1087,16 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
     if (has_res) res_issue(0);
     if (t + 2 < count) load_input(t + 2);
     if (has_res) {
+      // the second residual half lands while the next input is staged
       finish(std::true_type{}, 0);
       res_issue(2);
+      if (t + 2 < count) store_input();
       finish(std::true_type{}, 2);
     } else {
       finish(std::false_type{}, 0);
       finish(std::false_type{}, 2);
+      if (t + 2 < count) store_input();
     }
-    if (t + 2 < count) store_input();
     phase_end();
   }
   while (ph <= count) phase_end();
