@@ -380,15 +380,38 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
   }
 
   // ---- this wave's queries and their Q^T fragments (B operand of S^T) ----
-  const int q0 = qt * (W * 64) + wave * 64;
+  // first query rows of the wave's two 32-query blocks: blocks wave and 2W - 1 - wave of
+  // the tile's 2W, so that under a causal mask every wave has the same number of key
+  // blocks to process (a block is skipped for the query block it lies wholly after)
+  const int qt0 = qt * (W * 64);
+  const int qrow[2] = {qt0 + wave * 32, qt0 + (2 * W - 1 - wave) * 32};
   bf16x8 qf[2][NKS];
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    int q = q0 + b * 32 + l32;
+    int q = qrow[b] + l32;
     q = q < p.sq ? q : p.sq - 1;
 #pragma unroll
     for (int k = 0; k < NKS; ++k)
       qf[b][k] = *reinterpret_cast<const bf16x8*>(qb + static_cast<int64_t>(q) * p.q_ss + 16 * k + 8 * hf);
+  }
+  // Q^T pre-scaled by scale * log2(e) (rounded back to bf16), so the MFMAs produce the
+  // exponent of exp2 directly, and one more k-step adds the row's running base: K is
+  // extended by a column of ones (kone: A operand, k = 0 of the lanes < 32) and Q^T by
+  // the row of -base (qneg[b]: B operand, k = 0 of lane = query < 32).  The softmax
+  // then needs one v_exp per score and no multiply-add.
+  const float c = p.scale_log2;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int k = 0; k < NKS; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[b][k][e] = static_cast<bf16>(static_cast<float>(qf[b][k][e]) * c);
+  bf16x8 kone, qneg[2];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    kone[e] = static_cast<bf16>(e == 0 && hf == 0 ? 1.0f : 0.0f);
+    qneg[0][e] = static_cast<bf16>(0.0f);
+    qneg[1][e] = static_cast<bf16>(0.0f);
   }
   __syncthreads();
 
@@ -399,16 +422,17 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
     for (int d = 0; d < DT; ++d)
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[b][d][e] = 0.f;
-  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.f, 0.f};
-  const float c = p.scale_log2;
+  // base[b]: the bf16 value subtracted from this row's exponents (0 until the first block sets it)
+  float base[2] = {0.f, 0.f}, lrun[2] = {0.f, 0.f};
   int nkb = skvp / 32;
   if (CAUSAL) {
-    const int last = (q0 + 63 < p.sq ? q0 + 63 : p.sq - 1) / 32 + 1;
+    const int qmax = qrow[1] + 31;                  // qrow[1] >= qrow[0]
+    const int last = (qmax < p.sq ? qmax : p.sq - 1) / 32 + 1;
     nkb = last < nkb ? last : nkb;
   }
   // one 32-key block: both query blocks' scores first (their MFMA latency hides
   // behind the first block's softmax), then per query block softmax and P V
-  auto key_block = [&](int kbk, auto mask_tag) {
+  auto key_block = [&](int kbk, auto mask_tag, bool first) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int key0 = kbk * 32;
     bf16x8 kf[NKS];
@@ -432,15 +456,18 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
     f32x16 s[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
+      if (CAUSAL && key0 > qrow[b] + 31) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[b][e] = 0.f;
 #pragma unroll
       for (int k = 0; k < NKS; ++k) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], qf[b][k], s[b], 0, 0, 0);
+      s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, qneg[b], s[b], 0, 0, 0);
     }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
+      if (CAUSAL && key0 > qrow[b] + 31) continue;
       if constexpr (MASK) {
-        const int q = q0 + b * 32 + l32;
+        const int q = qrow[b] + l32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = key0 + (r >> 2) * 8 + 4 * hf + (r & 3);
@@ -455,20 +482,25 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
       const float m4 = __builtin_fmaxf(__builtin_fmaxf(s[b][12], s[b][13]), s[b][14]);
       float bm = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(m0, m1), m2),
                                  __builtin_fmaxf(__builtin_fmaxf(m3, m4), s[b][15]));
-      bm = other_half_max(bm) * c;
-      const bool up = bm > mrun[b] + kLazyRescale;
+      bm = other_half_max(bm);                        // block max relative to base[b]
+      const bool up = first || bm > kLazyRescale;
       if (__builtin_amdgcn_ballot_w64(up)) {
-        const float mnew = up ? bm : mrun[b];
-        const float alpha = mnew == mrun[b] ? 1.0f : __builtin_amdgcn_exp2f(mrun[b] - mnew);
+        // new base (a bf16 value, so -base is exact in qneg); this block's exponents
+        // are moved by the same shift d and earlier blocks rescaled by 2^-d
+        const float nbase = up && bm > -INFINITY ? static_cast<float>(static_cast<bf16>(base[b] + bm)) : base[b];
+        const float d = nbase - base[b];
+        const float alpha = d == 0.f ? 1.0f : __builtin_amdgcn_exp2f(-d);
 #pragma unroll
-        for (int d = 0; d < DT; ++d) oacc[b][d] *= alpha;
+        for (int dd = 0; dd < DT; ++dd) oacc[b][dd] *= alpha;
         lrun[b] *= alpha;
-        mrun[b] = mnew;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[b][r] -= d;
+        base[b] = nbase;
+        qneg[b][0] = static_cast<bf16>(hf == 0 ? -nbase : 0.0f);
       }
-      const float base = mrun[b] == -INFINITY ? 0.f : mrun[b];
       float pv[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(s[b][r], c, -base));
+      for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(s[b][r]);
       bf16x8 pf[2];
 #pragma unroll
       for (int r = 0; r < 16; ++r) pf[r >> 3][r & 7] = static_cast<bf16>(pv[r]);
@@ -494,18 +526,18 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
   using masked = std::integral_constant<bool, true>;
   using unmasked = std::integral_constant<bool, false>;
   if (CAUSAL) {
-    for (int kbk = 0; kbk < nkb; ++kbk) key_block(kbk, masked{});
+    for (int kbk = 0; kbk < nkb; ++kbk) key_block(kbk, masked{}, kbk == 0);
   } else {
     const int nfull = p.skv / 32;                    // blocks with 32 valid keys
-    for (int kbk = 0; kbk < nfull; ++kbk) key_block(kbk, unmasked{});
-    if (nfull < nkb) key_block(nfull, masked{});
+    for (int kbk = 0; kbk < nfull; ++kbk) key_block(kbk, unmasked{}, kbk == 0);
+    if (nfull < nkb) key_block(nfull, masked{}, nfull == 0);
   }
 
   // ---- O = (O^T / l)^T: lane holds query l%32, dh rows 8 (r/4) + 4 (l/32) + r%4 (+32 d) ----
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     const float lt = other_half_sum(lrun[b]);
-    const int q = q0 + b * 32 + l32;
+    const int q = qrow[b] + l32;
     if (q >= p.sq) continue;
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
 #pragma unroll
