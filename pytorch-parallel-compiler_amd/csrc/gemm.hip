@@ -420,13 +420,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmParams p) {
 // each 128 x 128 as 8 x 8 MFMA 16x16x32 tiles (one wave per SIMD, the 256
 // accumulators per lane in AGPRs).  MFMA roles are swapped with respect to C:
 // the A operand is a W row (o), the B operand an activation row (m), so a
-// lane's 4 accumulators are 4 consecutive output columns of one row, and the
-// bias is folded in by starting the accumulators at it.
+// lane's 4 accumulators are 4 consecutive output columns of one row.  The
+// accumulators of a tile start at zero (the first MFMA takes a zero C operand)
+// and the epilogue adds the bias.
 //
 // K advances in stages of 64 (128-byte row segments: whole cache lines)
-// through 2 LDS slots of 64 KB; the stage sequence runs on across tile
-// boundaries, so the next tile's operands load during the current tile's
-// last stage and epilogue.  Operands move global -> LDS with
+// through 2 LDS slots of 64 KB, in a rotated order per tile (see tile_of); the
+// stage sequence runs on across tile boundaries, so the next tile's operands
+// load during the current tile's last stage and epilogue.  Operands move
+// global -> LDS with
 // global_load_lds_dwordx4: one instruction moves 8 rows x 128 bytes into a
 // contiguous 1 KB; the 16-byte chunk c of row r sits at position c ^ (r & 7),
 // so the 8 rows a fragment read serves per pass hit 8 distinct bank groups.
@@ -605,7 +607,6 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
     for (int g = 0; g < 16; ++g) read_frag(stage, fpos, g, wf, af);
   };
 
-  // ---- bias of a tile, in accumulator layout: columns o0 + ow + 16 i + 4 (lane >> 4) + e ----
   // ---- bias of a tile: wave w moves the tile's columns [64 w, 64 w + 64) into LDS slot
   // (tile index & 1) with one LDS-DMA load (columns past o read a valid column; the
   // stores of those columns are dropped).  The epilogue adds it; the accumulators of
