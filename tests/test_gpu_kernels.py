@@ -217,6 +217,27 @@ def test_grouped_gemm_large_tiles(hip, out_dtype, m, o, k, rows_inner):
     assert rel_err(c.cpu(), exact) <= TOL_BF16
 
 
+@pytest.mark.parametrize("m,o,k", [(256, 272, 64), (512, 256, 512), (272, 512, 128)])
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, None])
+def test_grouped_gemm_large_tiles_plain(hip, m, o, k, bias_dtype):
+    """The large-tile kernel without residual or ReLU: one K stage per tile (k = 64), rotated K
+    orders over 2-8 stages, bias in bf16, fp32 or absent."""
+    from wide_compiler import _hip
+    n = 128
+    g = gen(114)
+    a = _rand((n, m, k), g, torch.bfloat16)
+    w = (_rand((n, o, k), g) * k ** -0.5).to(torch.bfloat16)
+    bias = _rand((n, o), g, bias_dtype) if bias_dtype is not None else None
+    c = torch.empty((n, m, o), dtype=torch.bfloat16, device=DEV)
+    _hip.grouped_gemm(n=n, m=m, o=o, k=k, a=a.to(DEV), a_sn=m * k, a_so=0, a_si=k, a_rows_inner=m,
+                      w=w.to(DEV), w_sn=o * k, c=c, c_sn=m * o, c_so=0, c_si=o, c_rows_inner=m,
+                      bias=bias.to(DEV) if bias is not None else None, bias_sn=o)
+    exact = torch.bmm(a.double(), w.double().transpose(1, 2).contiguous())
+    if bias is not None:
+        exact = exact + bias.double().unsqueeze(1)
+    assert rel_err(c.cpu(), exact) <= TOL_BF16
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_linear_strided_boundary_view_and_relu(hip, dtype):
     import wide_compiler as wc
