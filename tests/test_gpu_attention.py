@@ -36,7 +36,7 @@ def _oracle(wide, q, k, v, causal, double=True):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n,b,t,d,h", [(3, 2, 64, 64, 2), (2, 2, 50, 128, 4), (2, 1, 200, 256, 2),
                                        (4, 3, 17, 32, 1), (2, 2, 130, 256, 8), (2, 1, 300, 128, 2),
-                                       (2, 2, 333, 64, 2)])
+                                       (2, 2, 333, 64, 2), (1, 2, 600, 64, 2)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_self_attention(hip, dtype, n, b, t, d, h, causal):
     import wide_compiler as wc
