@@ -343,8 +343,13 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hf = lane >> 5;
-  const int qt = blockIdx.x % p.q_tiles;
-  const int bh = blockIdx.x / p.q_tiles;
+  // Workgroups are dispatched round-robin over the 8 XCDs; XCD x takes the contiguous
+  // range [x G / 8, (x + 1) G / 8) of (batch, head, query tile) ids, so the heads of one
+  // row, whose 64-byte slices share cache lines, are read through one L2.
+  const int G = gridDim.x;
+  const int bid = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int qt = bid % p.q_tiles;
+  const int bh = bid / p.q_tiles;
   const int nb = bh / p.heads, h = bh - (bh / p.heads) * p.heads;
   const bf16* qb = static_cast<const bf16*>(p.q) + nb * p.q_sb + h * DH;
   const bf16* kb = static_cast<const bf16*>(p.k) + nb * p.k_sb + h * DH;
