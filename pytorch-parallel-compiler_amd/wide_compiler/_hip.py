@@ -148,6 +148,7 @@ SIGNATURES = {
     "wc_bn_eval": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P]),
     "wc_group_norm": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F, _I32, _I32, _I32, _P]),
     "wc_rnn_workspace_bytes": (_I64, [ctypes.POINTER(_RnnArgs)]),
+    "wc_rnn_status_offset": (_I64, [ctypes.POINTER(_RnnArgs)]),
     "wc_rnn_forward": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_recurrence": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
@@ -347,9 +348,47 @@ def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional
     return a, ws
 
 
+# Status words of recent partitioned-LSTM launches: (event, pinned host copy).  A launch
+# whose cross-workgroup wait timed out leaves 1 there; the next recurrent call (or
+# rnn_sync_check) raises once the copy has landed, without ever blocking the stream.
+_rnn_pending: List = []
+
+
+def _rnn_watch(a: _RnnArgs, ws: Tensor) -> None:
+    off = int(lib().wc_rnn_status_offset(ctypes.byref(a)))
+    if off < 0 or torch.cuda.is_current_stream_capturing():
+        return
+    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    host.copy_(ws[off:off + 4].view(torch.int32), non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(ws.device))
+    _rnn_pending.append((ev, host))
+
+
+def rnn_sync_check(block: bool = False) -> None:
+    """Raise WideKernelError if a finished partitioned-LSTM launch reported a timed-out
+    cross-workgroup wait (its outputs are then invalid).  block=True waits for every
+    launch still in flight."""
+    global _rnn_pending
+    keep, failed = [], 0
+    for ev, host in _rnn_pending:
+        if block:
+            ev.synchronize()
+        if ev.query():
+            failed += int(host[0]) != 0
+        else:
+            keep.append((ev, host))
+    _rnn_pending = keep
+    if failed:
+        raise WideKernelError("wc_rnn_recurrence: a cross-workgroup wait of the partitioned LSTM timed out; "
+                              "the outputs of that launch are invalid")
+
+
 def rnn_forward(**kw) -> None:
+    rnn_sync_check()
     a, ws = rnn_args(**kw)
     _check(lib().wc_rnn_forward(ctypes.byref(a), stream_of(kw["x"])), "wc_rnn_forward")
+    _rnn_watch(a, ws)
 
 
 def rnn_phase(a: _RnnArgs, phase: str, like: Tensor) -> None:

@@ -303,10 +303,15 @@ def test_gru(hip, dtype, n, b, t, i, h, with_h0):
 @pytest.mark.parametrize("n,b,t,i,h", [(32, 8, 32, 64, 128), (3, 2, 5, 8, 16), (2, 3, 7, 12, 100),
                                        (2, 3, 21, 64, 32),   # fused projection, partial last chunk
                                        # streamed (one launch per step): W_hh beyond one workgroup
-                                       (2, 18, 5, 16, 512), (3, 3, 4, 8, 320)])
+                                       (2, 18, 5, 16, 512), (3, 3, 4, 8, 320),
+                                       # bf16: partitioned on-chip recurrence (hidden / 128
+                                       # workgroups per model); fp32: streamed
+                                       (3, 16, 9, 32, 512), (2, 5, 7, 16, 256), (2, 1, 6, 24, 384),
+                                       (2, 16, 130, 32, 512)])
 @pytest.mark.parametrize("with_state", [False, True])
 def test_lstm(hip, dtype, n, b, t, i, h, with_state):
     import wide_compiler as wc
+    from wide_compiler import _hip
     g = gen(111)
     mods = _rnn_modules(nn.LSTM, n, i, h, 111, torch.float32)
     wide = wc.WideLSTM.from_modules(mods).to(DEV, dtype)
@@ -314,13 +319,21 @@ def test_lstm(hip, dtype, n, b, t, i, h, with_state):
     hx = (_rand((n, b, h), g, dtype), _rand((n, b, h), g, dtype)) if with_state else None
     with torch.no_grad():
         out, (hn, cn) = wide(x.to(DEV), None if hx is None else (hx[0].to(DEV), hx[1].to(DEV)))
+    _hip.rnn_sync_check(block=True)
+    out, hn, cn = out.cpu(), hn.cpu(), cn.cpu()
     p = [getattr(wide, k).detach().cpu() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
     eo, (eh, ec) = wide_ref.lstm(x.double(), *(q.double() for q in p),
                                  hx=None if hx is None else (hx[0].double(), hx[1].double()))
-    errs = _per_step_err(out.cpu(), eo)
+    errs = _per_step_err(out, eo)
     assert max(errs) <= tol(dtype), errs
-    assert rel_err(hn.cpu(), eh) <= tol(dtype)
-    assert rel_err(cn.cpu(), ec) <= tol(dtype)
+    assert rel_err(hn, eh) <= tol(dtype)
+    assert rel_err(cn, ec) <= tol(dtype)
+    if dtype == torch.bfloat16:
+        # the reference's own bf16 path (bf16 gates and bf16 cell state, wide_lstm.py:205-229):
+        # the same bar at every timestep
+        ro, (rh, rc) = wide_ref.lstm(x, *p, hx=hx)
+        assert max(_per_step_err(out, ro)) <= TOL_BF16, _per_step_err(out, ro)
+        assert rel_err(cn, rc) <= TOL_BF16
 
 
 def test_gru_matches_nn_gru_per_model(hip):
