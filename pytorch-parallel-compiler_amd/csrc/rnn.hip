@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "wc_gemm.h"
+#include "wc_rnn.h"
 
 namespace wc {
 namespace {
@@ -51,18 +52,6 @@ struct RnnParams {
   void* hn;
   void* cn;
 };
-
-// v_exp_f32 / v_rcp_f32 based activations, branch-free.  sigmoid has ~1e-7
-// relative error; tanh(x) = 1 - 2 / (e^2x + 1) has ~1e-7 absolute error
-// (its relative error grows only where |tanh| itself is below ~1e-3), both
-// far inside the parity bars.
-__device__ __forceinline__ float sigmoid_f(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
-}
-
-__device__ __forceinline__ float tanh_f(float x) {
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__expf(2.0f * x) + 1.0f);
-}
 
 // DPP lane permutations inside a 16-lane row (register-to-register, no LDS)
 template <int CTRL>
@@ -517,258 +506,6 @@ size_t step_lds_bytes(int hid) {
   return sizeof(float) * 16 * (C::R + 4) + sizeof(T) * 16 * static_cast<size_t>(hid + 16 / sizeof(T));
 }
 
-// ---------------------------------------------------------------------------
-// Partitioned persistent LSTM recurrence (bf16; hidden 256, 384 or 512; batch <= 16).
-//
-// W_hh of one model (4H x H bf16: 2 MB at H = 512) exceeds one compute unit's
-// registers and LDS, so P = H / 128 workgroups share a model, one per compute unit,
-// for all T steps.  Workgroup `part` owns hidden units [128 part, 128 part + 128) and
-// the 512 gate rows (i, f, g, o of each unit) of W_hh that feed them, held on-chip for
-// the whole sequence: the first SL k-steps (32 columns each) in LDS, the rest in
-// registers.  Per step it forms its gate pre-activations for all batch rows as MFMA
-// tiles (A = W_hh rows, B = h_{t-1}^T read from LDS), applies the cell update in
-// registers (the fp32 cell state never leaves the chip), writes h_t to the output,
-// and publishes a per-(model, part) step counter; it then waits for the counters of
-// the model's other parts and copies their slices of h_t into its LDS.
-//
-// Lane layout (v_mfma_f32_16x16x32_bf16, wave w of 4, lane = 16 g + fr): row tile j
-// (0..7) of wave w holds A row rho = gate (rho & 3) of unit 32 w + 8 (rho >> 2) + j,
-// so the accumulator of lane (g, fr) holds all four gates of unit 32 w + 8 g + j for
-// batch row fr.  A lane therefore owns 8 consecutive units of one batch row: its
-// gates_x of a gate, its h_t and its cell state are 16-byte vectors, and the cell
-// update needs no data exchange between lanes.
-//
-// Cross-workgroup exchange.  h_t and the counters are written and read with
-// device-scope (sc1) vector accesses, which are coherent across the XCDs' L2s; a
-// part's h_t stores complete (vmcnt(0), then a barrier) before its counter is
-// stored.  Counters sit in the caller's workspace: the input projection zeroes them,
-// and the last workgroup of a model to finish resets them, so every launch starts
-// from zero.  Every wait is bounded: past the limit the workgroup records 1 in the
-// status word and leaves (the outputs are then invalid).  The host launches the grid
-// cooperatively, so all workgroups are co-resident, or the launch fails.
-// ---------------------------------------------------------------------------
-constexpr int kPartUnits = 128;                      // hidden units per workgroup
-constexpr int kPartThreads = 256;                    // 4 waves
-constexpr int kPartSyncInts = 32;                    // one 128-byte block of counters per model
-constexpr int kPartDone = 16;                        // index of the finished-parts counter
-constexpr int kPartSpinLimit = 1 << 22;              // polls (each ~0.5 us) before giving up
-
-struct PartParams {
-  int n, batch, steps, remap;
-  const bf16* gx;     // [n, batch, steps, 4H]: x W_ih^T + b_ih + b_hh, rounded to bf16
-  const bf16* w_hh;   // [n, 4H, H]
-  const bf16* h0;     // [n, batch, H] or null
-  const bf16* c0;     // [n, batch, H] or null
-  bf16* out;          // [n, batch, steps, H]
-  bf16* hn;           // [n, batch, H] or null
-  bf16* cn;           // [n, batch, H] or null
-  int* sync;          // [n][kPartSyncInts] step counters and finished-parts counter
-  int* status;        // set to 1 when a wait timed out
-};
-
-// k-steps of W_hh kept in LDS (the rest live in registers: 8 (16 - SL) fragments of
-// 4 registers per lane at H = 512)
-template <int H> struct PartCfg;
-template <> struct PartCfg<256> { static constexpr int SL = 0; };
-template <> struct PartCfg<384> { static constexpr int SL = 1; };
-template <> struct PartCfg<512> { static constexpr int SL = 4; };
-
-template <int H>
-constexpr size_t part_lds_bytes() {
-  return static_cast<size_t>(PartCfg<H>::SL) * 4 * 8 * 1024 + 16 * static_cast<size_t>(H + 8) * 2 + 16;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
-
-constexpr int kSc1 = 16;   // buffer-op cache policy: device scope (sc1)
-
-__device__ __forceinline__ int sync_load(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void sync_store(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-template <int H>
-__global__ __launch_bounds__(kPartThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void lstm_part_kernel(PartParams p) {
-  constexpr int NT = 8, KS = H / 32, P = H / kPartUnits, SL = PartCfg<H>::SL, RS = KS - SL;
-  constexpr int HP = H + 8;                          // LDS pitch of an h row (elements)
-  constexpr int G = 4 * H;
-  extern __shared__ __attribute__((aligned(16))) char part_smem[];
-  bf16x8* wl = reinterpret_cast<bf16x8*>(part_smem);                          // [SL][4][NT][64]
-  bf16* hs = reinterpret_cast<bf16*>(part_smem + SL * 4 * NT * 1024);         // [16][HP] h_{t-1}
-  int* abort_flag = reinterpret_cast<int*>(hs + 16 * HP);
-
-  const int nwg = p.n * P;
-  int id = blockIdx.x;
-  if (p.remap) id = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);   // a model's parts share an XCD
-  const int mdl = id / P, part = id - mdl * P;
-  const int u0 = part * kPartUnits;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, fr = lane & 15;
-  const int ucol = u0 + w * 32 + g * 8;              // first of the lane's 8 units (model column)
-  const bool brow = fr < p.batch;
-  const int64_t mb = static_cast<int64_t>(mdl) * p.batch;
-
-  // ---- W_hh rows of this part: registers and LDS, loaded once ----
-  bf16x8 wr[RS > 0 ? RS : 1][NT];
-  {
-    const bf16* wb = p.w_hh + static_cast<int64_t>(mdl) * G * H;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const bf16* row = wb + static_cast<int64_t>((fr & 3) * H + u0 + w * 32 + (fr >> 2) * 8 + j) * H + g * 8;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + s * 32);
-        if (s < SL) wl[((s * 4 + w) * NT + j) * 64 + lane] = v;
-        else wr[s - SL][j] = v;
-      }
-    }
-  }
-  // ---- h_{-1} into LDS (rows >= batch stay zero), c_{-1} and gates_x of step 0 in registers ----
-  for (int e = tid; e < 16 * (HP / 8); e += kPartThreads) {
-    const int b = e / (HP / 8), col = (e - b * (HP / 8)) * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (p.h0 && b < p.batch && col < H)
-      v = *reinterpret_cast<const uint4*>(p.h0 + (mb + b) * H + col);
-    *reinterpret_cast<uint4*>(hs + b * HP + col) = v;
-  }
-  if (tid == 0) *abort_flag = 0;
-  float c[NT];
-  {
-    bf16x8 cv = {};
-    if (p.c0 && brow) cv = *reinterpret_cast<const bf16x8*>(p.c0 + (mb + fr) * H + ucol);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) c[j] = static_cast<float>(cv[j]);
-  }
-  const uint32_t out_bytes = static_cast<uint32_t>(p.batch) * p.steps * H * 2;   // this model's out block
-  const __amdgpu_buffer_rsrc_t ors = part_rsrc(p.out + mb * p.steps * H, out_bytes);
-  const __amdgpu_buffer_rsrc_t grs =
-      part_rsrc(p.gx + mb * p.steps * G, static_cast<uint32_t>(p.batch) * p.steps * G * 2);
-  const uint32_t lane_row = static_cast<uint32_t>(brow ? fr : 0) * p.steps;   // (b * steps) for this lane
-  bf16x8 gxn[4];
-  auto load_gx = [&](int t) {
-    const uint32_t off = ((lane_row + t) * G + ucol) * 2;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      gxn[q] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(grs, off + q * H * 2, 0, 0));
-  };
-  load_gx(0);
-  int* my_sync = p.sync + static_cast<int64_t>(mdl) * kPartSyncInts;
-  __syncthreads();
-
-  bool aborted = false;
-  bf16x8 hv = {};
-  for (int t = 0; t < p.steps; ++t) {
-    // gates = gates_x (incl. both biases) + h_{t-1} W_hh^T
-    f32x4 acc[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[j][e] = static_cast<float>(gxn[e][j]);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const bf16x8 hb = *reinterpret_cast<const bf16x8*>(hs + fr * HP + s * 32 + g * 8);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const bf16x8 a = (s < SL) ? wl[((s * 4 + w) * NT + j) * 64 + lane] : wr[s < SL ? 0 : s - SL][j];
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hb, acc[j], 0, 0, 0);
-      }
-    }
-    // cell update of the lane's 8 units (i, f, g, o in acc[j][0..3])
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const float ig = sigmoid_f(acc[j][0]);
-      const float fg = sigmoid_f(acc[j][1]);
-      const float gg = tanh_f(acc[j][2]);
-      const float og = sigmoid_f(acc[j][3]);
-      c[j] = fg * c[j] + ig * gg;
-      hv[j] = static_cast<bf16>(og * tanh_f(c[j]));
-    }
-    if (brow)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, hv), ors,
-                                             ((lane_row + t) * H + ucol) * 2, 0, kSc1);
-    if (t + 1 == p.steps) break;
-    __syncthreads();                                   // every wave has read h_{t-1}
-    *reinterpret_cast<bf16x8*>(hs + fr * HP + ucol) = hv;
-    if (P > 1) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's h_t stores are performed
-      __syncthreads();
-      if (tid == 0) sync_store(my_sync + part, t + 1);
-    }
-    load_gx(t + 1);
-    if (P > 1) {
-      if (w == 0) {
-        bool ok = true;
-        if (lane < P && lane != part) {
-          int spins = 0;
-          while (sync_load(my_sync + lane) < t + 1) {
-            if (++spins > kPartSpinLimit) {
-              ok = false;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-          }
-        }
-        if (!ok) *abort_flag = 1;
-      }
-      __syncthreads();
-      if (*abort_flag) {
-        aborted = true;
-        break;
-      }
-      // the other parts' slices of h_t: rows < batch, 128-unit slices != part
-      constexpr int CH = (P - 1) * (kPartUnits / 8);   // 16-byte chunks per row
-      for (int e = tid; e < p.batch * CH; e += kPartThreads) {
-        const int b = e / CH, r = e - b * CH;
-        int q = r / (kPartUnits / 8);
-        q += (q >= part) ? 1 : 0;
-        const int col = q * kPartUnits + (r % (kPartUnits / 8)) * 8;
-        const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-            ors, ((static_cast<uint32_t>(b) * p.steps + t) * H + col) * 2, 0, kSc1);
-        *reinterpret_cast<i32x4*>(hs + b * HP + col) = v;
-      }
-    }
-    __syncthreads();
-  }
-
-  if (!aborted && brow) {
-    const int64_t so = (mb + fr) * H + ucol;
-    if (p.hn) *reinterpret_cast<bf16x8*>(p.hn + so) = hv;
-    if (p.cn) {
-      bf16x8 cv;
-#pragma unroll
-      for (int j = 0; j < NT; ++j) cv[j] = static_cast<bf16>(c[j]);
-      *reinterpret_cast<bf16x8*>(p.cn + so) = cv;
-    }
-  }
-  if (P > 1) {
-    // the last part of the model to finish resets the counters for the next launch
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-      if (aborted) sync_store(p.status, 1);
-      const int before = __hip_atomic_fetch_add(my_sync + kPartDone, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (before == P - 1) {
-#pragma unroll
-        for (int q = 0; q < P; ++q) sync_store(my_sync + q, 0);
-        sync_store(my_sync + kPartDone, 0);
-      }
-    }
-  }
-}
-
-// counters and status zeroed; bias = b_ih + b_hh in fp32 (either may be null)
-__global__ void part_prep_kernel(int* sync, int nsync, const bf16* b_ih, const bf16* b_hh, float* bias,
-                                 int64_t nbias) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < nsync) sync_store(sync + i, 0);
-  if (bias && i < nbias)
-    bias[i] = (b_ih ? static_cast<float>(b_ih[i]) : 0.f) + (b_hh ? static_cast<float>(b_hh[i]) : 0.f);
-}
-
 }  // namespace
 }  // namespace wc
 
@@ -812,57 +549,8 @@ static bool rnn_plan(int gates, int hid, RnnParams& p) {
   return best >= 0;
 }
 
-// ---- partitioned LSTM: when it applies, and its workspace layout ----
-template <int H>
-static bool part_kernel_fits(size_t& lds) {
-  lds = part_lds_bytes<H>();
-  const void* fn = reinterpret_cast<const void*>(lstm_part_kernel<H>);
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
-    return false;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPartThreads, lds) != hipSuccess) return false;
-  return per_cu >= 1;
-}
-
-// The partitioned kernel runs bf16 LSTMs with hidden 256 / 384 / 512 and batch <= 16 when
-// every (model, part) workgroup can hold a compute unit of its own.
-static bool part_plan(const wc_rnn_args* a) {
-  if (a->cell != WC_CELL_LSTM || a->dtype != WC_BF16 || a->batch < 1 || a->batch > 16 || a->steps < 1)
-    return false;
-  if (a->hidden != 256 && a->hidden != 384 && a->hidden != 512) return false;
-  const int64_t parts = a->hidden / kPartUnits;
-  const int cus = device_cu_count();
-  if (cus <= 0 || a->n * parts > cus) return false;
-  // per-model blocks of gates_x and out are addressed with 32-bit byte offsets
-  if (a->batch * a->steps * 4 * a->hidden * 2 >= 0x7fffffffll) return false;
-  for (const void* q : {a->w_hh, a->h0, a->c0, static_cast<const void*>(a->out),
-                        static_cast<const void*>(a->h_n), static_cast<const void*>(a->c_n)})
-    if (q && !aligned(q, 16)) return false;
-  size_t lds = 0;
-  if (a->hidden == 256) return part_kernel_fits<256>(lds);
-  if (a->hidden == 384) return part_kernel_fits<384>(lds);
-  return part_kernel_fits<512>(lds);
-}
-
-inline int64_t round256(int64_t v) { return (v + 255) & ~static_cast<int64_t>(255); }
-
-struct PartLayout {
-  int64_t gx, bias, sync, status, total;   // byte offsets into the workspace
-};
-
-static PartLayout part_layout(const wc_rnn_args* a) {
-  const int64_t g = 4 * a->hidden;
-  PartLayout l;
-  l.gx = 0;
-  l.bias = round256(a->n * a->batch * a->steps * g * 2);
-  l.sync = l.bias + round256(a->n * g * 4);
-  l.status = l.sync + round256(a->n * kPartSyncInts * 4);
-  l.total = l.status + 256;
-  return l;
-}
-
 static int64_t rnn_ws_bytes(const wc_rnn_args* a) {
-  if (part_plan(a)) return part_layout(a).total;
+  if (part_plan(a)) return part_workspace_bytes(a);
   const int64_t gates = a->cell == WC_CELL_GRU ? 3 : 4;
   // fp32 input projection [n, batch, steps, G] + fp32 cell state [n, batch, hidden]
   return (a->n * a->batch * a->steps * gates * a->hidden + a->n * a->batch * a->hidden) *
@@ -923,7 +611,7 @@ extern "C" int64_t wc_rnn_workspace_bytes(const wc_rnn_args* a) {
 
 extern "C" int64_t wc_rnn_status_offset(const wc_rnn_args* a) {
   if (!a || a->n < 0 || a->batch < 0 || a->steps < 0 || a->hidden < 0) return -1;
-  return part_plan(a) ? part_layout(a).status : -1;
+  return part_plan(a) ? part_status_offset(a) : -1;
 }
 
 static int32_t rnn_check(const wc_rnn_args* a, const char* what, RnnParams& p, int& gates) {
@@ -963,17 +651,7 @@ extern "C" int32_t wc_rnn_input_projection(const wc_rnn_args* a, void* stream) {
   const bool part = part_plan(a);
   void* bias_f32 = nullptr;
   if (part) {
-    // zero the step counters and status word; bias = b_ih + b_hh (fp32) for the projection
-    const PartLayout l = part_layout(a);
-    char* ws = static_cast<char*>(a->workspace);
-    const int nsync = static_cast<int>((l.total - l.sync) / 4);
-    const int64_t nbias = (a->b_ih || a->b_hh) ? static_cast<int64_t>(p.n) * G : 0;
-    if (nbias) bias_f32 = ws + l.bias;
-    const int64_t items = nbias > nsync ? nbias : nsync;
-    part_prep_kernel<<<static_cast<uint32_t>(cdiv(items, 256)), 256, 0, as_stream(stream)>>>(
-        reinterpret_cast<int*>(ws + l.sync), nsync, static_cast<const bf16*>(a->b_ih),
-        static_cast<const bf16*>(a->b_hh), static_cast<float*>(bias_f32), nbias);
-    rc = check_launch("wc_rnn_input_projection(prep)");
+    rc = part_prepare(a, as_stream(stream), &bias_f32);
     if (rc) return rc;
   }
   // gates_x = x W_ih^T + b_ih  ->  workspace [N, B*T, G]: fp32, or bf16 with b_ih + b_hh
@@ -1005,46 +683,6 @@ extern "C" int32_t wc_rnn_input_projection(const wc_rnn_args* a, void* stream) {
     return grouped_gemm(g, a->dtype, a->dtype, WC_F32, as_stream(stream));
   }
   return grouped_gemm(g, a->dtype, WC_F32, a->dtype, as_stream(stream));
-}
-
-template <int H>
-static int32_t launch_part(const wc_rnn_args* a, hipStream_t st) {
-  const PartLayout l = part_layout(a);
-  char* ws = static_cast<char*>(a->workspace);
-  PartParams p;
-  p.n = static_cast<int>(a->n);
-  p.batch = static_cast<int>(a->batch);
-  p.steps = static_cast<int>(a->steps);
-  const int nwg = p.n * (H / kPartUnits);
-  p.remap = (nwg % 8 == 0 && (nwg / 8) % (H / kPartUnits) == 0) ? 1 : 0;
-  p.gx = reinterpret_cast<const bf16*>(ws + l.gx);
-  p.w_hh = static_cast<const bf16*>(a->w_hh);
-  p.h0 = static_cast<const bf16*>(a->h0);
-  p.c0 = static_cast<const bf16*>(a->c0);
-  p.out = static_cast<bf16*>(a->out);
-  p.hn = static_cast<bf16*>(a->h_n);
-  p.cn = static_cast<bf16*>(a->c_n);
-  p.sync = reinterpret_cast<int*>(ws + l.sync);
-  p.status = reinterpret_cast<int*>(ws + l.status);
-  const size_t lds = part_lds_bytes<H>();
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cap) != hipSuccess)
-    return set_error(WC_ERR_ARG, "wc_rnn_recurrence: stream capture status unavailable");
-  if (cap == hipStreamCaptureStatusNone) {
-    // co-residency of the whole grid is guaranteed, or the launch fails here
-    void* args[] = {&p};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(lstm_part_kernel<H>),
-                                                    dim3(nwg), dim3(kPartThreads), args,
-                                                    static_cast<unsigned>(lds), st);
-    if (e != hipSuccess)
-      return set_error(static_cast<int32_t>(e), "wc_rnn_recurrence: cooperative launch of %d workgroups "
-                       "failed: %s", nwg, hipGetErrorString(e));
-    return WC_OK;
-  }
-  // under graph capture: an ordinary kernel node (the host checked that the grid fits the
-  // device one workgroup per compute unit)
-  lstm_part_kernel<H><<<dim3(nwg), dim3(kPartThreads), lds, st>>>(p);
-  return check_launch("wc_rnn_recurrence(partitioned)");
 }
 
 // Launch the persistent kernel with the lane shape already in p (lg, kl, upg).
@@ -1087,12 +725,7 @@ extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
   if (rc) return rc;
   if (p.n == 0 || p.batch == 0 || p.steps == 0) return WC_OK;
   WC_REQUIRE(a->w_hh && a->out, WC_ERR_NULL, "wc_rnn_recurrence: null pointer");
-  if (part_plan(a)) {
-    hipStream_t st = as_stream(stream);
-    if (p.hid == 256) return launch_part<256>(a, st);
-    if (p.hid == 384) return launch_part<384>(a, st);
-    return launch_part<512>(a, st);
-  }
+  if (part_plan(a)) return part_recurrence(a, as_stream(stream));
   if (!rnn_plan(gates, p.hid, p)) {
     // W_hh of one model does not fit a workgroup's registers: one launch per step
     const int es = dtype_size(a->dtype);
