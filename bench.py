@@ -2,25 +2,33 @@
 Wide-forward throughput of the MI355X build on one GPU.  Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--mode best|graph|eager]
-                  [--no-cpu] [--cpu-seconds S]
+                  [--no-cpu] [--cpu-seconds S] [--no-extra]
 
-Default workload (the configuration the headline metric is quoted on): WideGRU over N=32
-nn.GRU(64 -> 128, batch_first) models, x [32, 4, 32, 64] ~ N(0, 1) fp32, h0 = 0.  The other
-configurations are selectable with --config (mlp, resblock, attention, seq, groupnorm).
+Default workload (the largest single-GPU configuration): N=64 sequence models, each
+Embedding(8192, 256) - LayerNorm(256) - LSTM(256 -> 512) - Linear(512 -> 8192), bf16 weights,
+ids [64, 16, 128] uniform in [0, 8192).  --config selects another configuration as the headline
+(mlp, gru, resblock, attention, groupnorm); the others are reported under "configs".
 
 * step  = one wide forward over one batch, inputs already resident in HBM.
 * value = samples/s = N*B*K / wall time of K steps, bracketed by torch.cuda.synchronize().
   Two ways to run a step are timed: graph replays the forward as one captured HIP graph per
   step; eager calls the module from Python (kernel launches queue asynchronously).  --mode
   best (default) reports the faster of the two as value; both rates are in the line.
-* roofline = the dominant kernel: algorithmic flops (or bytes) per launch divided by its
-  average duration, timed with HIP events on the stream it is launched on; peaks are MI355X
-  datasheet values (dense MFMA fp32 157.3 TFLOP/s, bf16 2516.6 TFLOP/s; HBM 8 TB/s).
+* roofline = the kernel with the largest share of the step's GPU time: algorithmic flops (or
+  bytes) per launch divided by its average duration, timed with HIP events around a graph of
+  back-to-back launches on the stream they run on; "kernels" lists every kernel of the step
+  with its own fraction.  Peaks are MI355X datasheet values (dense MFMA fp32 157.3 TFLOP/s,
+  bf16 2516.6 TFLOP/s; HBM 8 TB/s).  "traffic" is the counter-measured HBM bytes per launch
+  of that kernel (profiles/traffic_<config>.json) when one was recorded for it.
+* configs = the other configurations (value, ms per step, dominant kernel and its fraction),
+  plus "pack": the boundary pack and transpose kernels in GB/s.
 * cache regimes: per-step GPU times (HIP events around each step, in the mode used) over K
   steps, median reported hot (steps back to back) and cold (a 512 MiB buffer rewritten before
   every step, so the 256 MB Infinity Cache and the L2s hold none of the step's data).
 * cpu_baseline = the oracle (op-for-op CPU restatement of the reference wide path, torch CPU
-  ops) on the host cores over a bounded sample, scaled to samples/s.
+  ops) on the host cores over a bounded sample, scaled to samples/s.  Threads = the CPUs this
+  process may use (affinity, capped by the cgroup CPU quota); the CPU model, core counts,
+  thread count and BLAS / oneDNN build are recorded beside it.
 """
 
 from __future__ import annotations
@@ -30,7 +38,7 @@ import json
 import os
 import sys
 import time
-from typing import Callable, Dict, Optional
+from typing import Callable, Dict, List, Optional
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "pytorch-parallel-compiler_amd"))
@@ -100,9 +108,95 @@ def _cpu_loop(fn: Callable[[], None], seconds: float, min_iters: int = 2):
             return iters, el
 
 
+def _kernel(name: str, bound: str, sec: float, launches: int = 1, flops: float = 0.0,
+            byts: float = 0.0, peak: Optional[float] = None) -> Dict:
+    """One kernel of a step: algorithmic work per launch over its measured average duration."""
+    if bound == "hbm":
+        peak = PEAK["hbm"] if peak is None else peak
+        achieved, unit, scale, work = byts / sec, "GB/s", 1e9, {"bytes_per_launch": byts}
+    else:
+        achieved, unit, scale, work = flops / sec, "TFLOP/s", 1e12, {"flops_per_launch": flops}
+    return {"kernel": name, "bound": "hbm" if bound == "hbm" else "mfma", "us_per_launch": sec * 1e6,
+            "launches_per_step": launches, "achieved": achieved / scale, "peak": peak / scale, "unit": unit,
+            "frac": achieved / peak, **work}
+
+
 # ---------------------------------------------------------------------------------------
-# configurations
+# configurations: each returns the step, a parity check against the oracle, the step's
+# kernels (measured), and a bounded CPU sample of the oracle
 # ---------------------------------------------------------------------------------------
+
+def cfg_seq(dev, steps, warmup) -> Dict:
+    import torch
+    from wide_compiler import _hip, workloads
+    from oracle import wide_ref
+
+    work = workloads.seq_n64()
+    n, b = work.n, work.batch
+    ids_cpu = work.inputs["ids"]
+    _, _, t = ids_cpu.shape
+    wide = workloads.WideSeqModel([m.to(dev) for m in work.models]).eval()
+    ids = ids_cpu.to(dev)
+    hdim, v, d = wide.lstm.hidden_size, wide.fc.out_features, wide.lstm.input_size
+    logits = torch.empty((n, b, t, v), device=dev, dtype=torch.bfloat16)
+
+    def step():
+        return wide(ids, logits)
+
+    def parity():
+        with torch.inference_mode():
+            y = step()
+        errs = []
+        for k in (0, n - 1):
+            p = {kk: (vv.double() if torch.is_tensor(vv) else vv)
+                 for kk, vv in workloads.seq_params([work.models[k]]).items()}
+            errs.append(_rel(y[k:k + 1], wide_ref.seq_model(ids_cpu[k:k + 1], p)))
+        return max(errs)
+
+    def kernels():
+        with torch.inference_mode():
+            x = wide.ln(wide.emb(ids, per_model=True))
+            hs, _ = wide.lstm(x)
+            lstm = wide.lstm
+            a, ws = _hip.rnn_args(cell=_hip.CELL_LSTM, x=x, w_ih=lstm.weight_ih, w_hh=lstm.weight_hh,
+                                  b_ih=lstm.bias_ih, b_hh=lstm.bias_hh, h0=None, c0=None, out=hs,
+                                  h_n=None, c_n=None)
+            t_emb = _event_time(lambda: wide.emb(ids, per_model=True), 20, 2)
+            t_ln = _event_time(lambda: wide.ln(x), 20, 2)
+            t_proj = _event_time(lambda: _hip.rnn_phase(a, "input_projection", x), 10, 2)
+            t_rec = _event_time(lambda: _hip.rnn_phase(a, "recurrence", x), 10, 2)
+            t_fc = _event_time(lambda: wide.fc.forward_into(hs, logits), 10, 2)
+        rows = n * b * t
+        g = 4 * hdim
+        return [
+            _kernel("seg_copy_kernel<GatherMap> (per-model embedding gather, bf16)", "hbm", t_emb,
+                    byts=rows * (8 + 2 * d * 2)),
+            _kernel("layernorm_kernel (256-wide rows, bf16, fp32 statistics)", "hbm", t_ln,
+                    byts=2 * rows * d * 2 + 2 * n * d * 2),
+            _kernel("LSTM input projection (part_prep_kernel + gemm_xlp_kernel, 256 -> 2048, bf16 out)",
+                    "mfma", t_proj, flops=2.0 * rows * g * d, peak=PEAK["bf16_mfma"]),
+            _kernel("lstm_part_kernel (LSTM recurrence, 128 steps, W_hh on-chip, 4 CUs per model)", "mfma",
+                    t_rec, flops=2.0 * rows * g * hdim, peak=PEAK["bf16_mfma"]),
+            _kernel("gemm_xlp_kernel (vocab projection 512 -> 8192 + bias, bf16)", "mfma", t_fc,
+                    flops=2.0 * rows * v * hdim, peak=PEAK["bf16_mfma"]),
+        ]
+
+    n_cpu = 1
+    p_cpu = {kk: (vv.float() if torch.is_tensor(vv) and vv.is_floating_point() else vv)
+             for kk, vv in workloads.seq_params(work.models[:n_cpu]).items()}
+    p_cpu = {kk: (vv.to(torch.bfloat16) if torch.is_tensor(vv) and vv.is_floating_point() else vv)
+             for kk, vv in p_cpu.items()}
+    ids_sub = ids_cpu[:n_cpu, :4].contiguous()
+
+    def cpu_run():
+        wide_ref.seq_model(ids_sub, p_cpu)
+
+    return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": step, "parity": parity,
+            "kernels": kernels, "cpu": cpu_run, "cpu_samples": n_cpu * 4,
+            "cpu_sample": f"{n_cpu} of the {n} models, 4 of the {b} sequences (no cross-model or cross-sequence "
+                          f"terms), bf16",
+            "extra": {"seq_len": t, "vocab": v, "embed": d, "hidden": hdim}}
+
 
 def cfg_gru(dev, steps, warmup) -> Dict:
     import torch
@@ -130,16 +224,12 @@ def cfg_gru(dev, steps, warmup) -> Dict:
         hn = torch.empty((n, b, h), device=dev)
         a, ws = _hip.rnn_args(cell=_hip.CELL_GRU, x=x, w_ih=wide.weight_ih, w_hh=wide.weight_hh, b_ih=wide.bias_ih,
                               b_hh=wide.bias_hh, h0=None, c0=None, out=o, h_n=hn, c_n=None)
-        kt = {ph: _event_time(lambda ph=ph: _hip.rnn_phase(a, ph, x), steps, warmup)
-              for ph in ("input_projection", "recurrence")}
-        return kt, ws
-
-    def roofline():
-        kt, _ = kernels()
-        flops = 2.0 * n * b * t * 3 * h * h
-        return {"bound": "mfma", "kernel": "rnn_seq_kernel (GRU recurrence, fp32)", "flops_per_launch": flops,
-                "sec": kt["recurrence"], "peak": PEAK["fp32_mfma"],
-                "other_kernels_us": {"input_projection_gemm": kt["input_projection"] * 1e6}}
+        t_proj = _event_time(lambda: _hip.rnn_phase(a, "input_projection", x), steps, warmup)
+        t_rec = _event_time(lambda: _hip.rnn_phase(a, "recurrence", x), steps, warmup)
+        return [_kernel("gemm_kernel (GRU input projection 64 -> 384, fp32)", "mfma", t_proj,
+                        flops=2.0 * n * b * t * 3 * h * i, peak=PEAK["fp32_mfma"]),
+                _kernel("rnn_seq_kernel (GRU recurrence, fp32)", "mfma", t_rec,
+                        flops=2.0 * n * b * t * 3 * h * h, peak=PEAK["fp32_mfma"])]
 
     mods = work.models
     p32 = [torch.stack([getattr(m, k).detach().float() for m in mods])
@@ -149,7 +239,7 @@ def cfg_gru(dev, steps, warmup) -> Dict:
         wide_ref.gru(x_cpu, *p32)
 
     return {"name": work.name, "n": n, "batch": b, "dtype": "fp32", "step": lambda: wide(x), "parity": parity,
-            "roofline": roofline, "cpu": cpu_run, "cpu_samples": n * b, "cpu_sample": "full workload",
+            "kernels": kernels, "cpu": cpu_run, "cpu_samples": n * b, "cpu_sample": "full workload",
             "extra": {"seq_len": t, "input_size": i, "hidden": h}}
 
 
@@ -176,25 +266,23 @@ def cfg_mlp(dev, steps, warmup) -> Dict:
         return _rel(y, wide_ref.mlp_wide(packed_cpu.double(), n, w1.double(), b1.double(), w2.double(),
                                          b2.double()))
 
-    def roofline():
+    def kernels():
         xn = packed.view(b, n, 64).movedim(1, 0)
         fused = getattr(wide, "_mlp2", {}).get("fc2")
         if fused is not None:
             sec = _event_time(lambda: fused(xn), steps, warmup)
             byts = 4.0 * (n * 128 * 64 + n * 128 + n * 64 * 128 + n * 64 + n * b * 64 + n * b * 64)
-            return {"bound": "hbm", "kernel": "mlp2_kernel (fc1 + bias + ReLU + fc2 + bias, fp32)",
-                    "bytes_per_launch": byts, "sec": sec, "peak": PEAK["hbm"]}
+            return [_kernel("mlp2_kernel (fc1 + bias + ReLU + fc2 + bias, fp32)", "hbm", sec, byts=byts)]
         fc1 = wide.stages["fc1"]
         sec = _event_time(lambda: fc1(xn), steps, warmup)
         byts = 4.0 * (n * 128 * 64 + n * 128 + n * b * 64 + n * b * 128)
-        return {"bound": "hbm", "kernel": "gemm_kernel (fc1 + bias + ReLU, fp32)", "bytes_per_launch": byts,
-                "sec": sec, "peak": PEAK["hbm"]}
+        return [_kernel("gemm_kernel (fc1 + bias + ReLU, fp32)", "hbm", sec, byts=byts)]
 
     def cpu_run():
         wide_ref.mlp_wide(packed_cpu, n, w1, b1, w2, b2)
 
     return {"name": work.name, "n": n, "batch": b, "dtype": "fp32", "step": lambda: wide(packed),
-            "parity": parity, "roofline": roofline, "cpu": cpu_run, "cpu_samples": n * b,
+            "parity": parity, "kernels": kernels, "cpu": cpu_run, "cpu_samples": n * b,
             "cpu_sample": "full workload", "extra": {"layers": "Linear(64,128)-ReLU-Linear(128,64)"}}
 
 
@@ -221,13 +309,13 @@ def cfg_resblock(dev, steps, warmup) -> Dict:
                              wide_ref.resblock_wide(x_cpu[:, k * c:(k + 1) * c].double(), 1, pk)))
         return max(errs)
 
-    def roofline():
+    def kernels():
         conv1 = wide.stages["conv1"]
         xn = x.view(b, n, c, hw, hw).movedim(1, 0)
         sec = _event_time(lambda: conv1(xn), steps, warmup)
         flops = 2.0 * n * b * hw * hw * c * c * 9
-        return {"bound": "mfma", "kernel": "conv_res_kernel (resident-weight conv3x3 + BN + ReLU, bf16)", "flops_per_launch": flops,
-                "sec": sec, "peak": PEAK["bf16_mfma"]}
+        return [_kernel("conv_res_kernel (resident-weight conv3x3 + BN + ReLU, bf16)", "mfma", sec, launches=2,
+                        flops=flops, peak=PEAK["bf16_mfma"])]
 
     n_cpu = 4
     pk_cpu = workloads.resblock_params([m for m in models[:n_cpu]], torch.bfloat16)
@@ -237,7 +325,7 @@ def cfg_resblock(dev, steps, warmup) -> Dict:
         wide_ref.resblock_wide(x_sub, n_cpu, pk_cpu)
 
     return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": lambda: wide(x), "parity": parity,
-            "roofline": roofline, "cpu": cpu_run, "cpu_samples": n_cpu * b,
+            "kernels": kernels, "cpu": cpu_run, "cpu_samples": n_cpu * b,
             "cpu_sample": f"{n_cpu} of the {n} models (the wide path has no cross-model terms), bf16",
             "extra": {"channels": c, "hw": hw}}
 
@@ -270,7 +358,7 @@ def cfg_attention(dev, steps, warmup) -> Dict:
             errs.append(_rel(y[k:k + 1], ref))
         return max(errs)
 
-    def roofline():
+    def kernels():
         qkv = torch.empty((n, b, s, 3 * d), device=dev, dtype=x.dtype)
         o = torch.empty((n, b, s, d), device=dev, dtype=x.dtype)
         wqkv, bqkv = wide._qkv_params()
@@ -283,11 +371,13 @@ def cfg_attention(dev, steps, warmup) -> Dict:
         t_attn = _event_time(attn, steps, warmup)
         t_qkv = _event_time(lambda: wide._project(x, wqkv, 3 * d * d, bqkv, 3 * d, 3 * d), steps, warmup)
         t_out = _event_time(lambda: wide._project(o, wide.out_weight, d * d, wide.out_bias, d, d), steps, warmup)
-        flops = 4.0 * n * b * hh * s * s * dh
-        return {"bound": "mfma", "kernel": "attn_res_kernel (fused softmax(QK^T)V, bf16, head_dim 32, K/V resident "
-                                           "in LDS)",
-                "flops_per_launch": flops, "sec": t_attn, "peak": PEAK["bf16_mfma"],
-                "other_kernels_us": {"qkv_projection_gemm": t_qkv * 1e6, "out_projection_gemm": t_out * 1e6}}
+        rows = n * b * s
+        return [_kernel("gemm_xlp_kernel (Q|K|V projection 256 -> 768, bf16)", "mfma", t_qkv,
+                        flops=2.0 * rows * 3 * d * d, peak=PEAK["bf16_mfma"]),
+                _kernel("attn_res_kernel (fused softmax(QK^T)V, bf16, head_dim 32, K/V resident in LDS)", "mfma",
+                        t_attn, flops=4.0 * n * b * hh * s * s * dh, peak=PEAK["bf16_mfma"]),
+                _kernel("gemm_xlp_kernel (output projection 256 -> 256, bf16)", "mfma", t_out,
+                        flops=2.0 * rows * d * d, peak=PEAK["bf16_mfma"])]
 
     n_cpu = 1
     xs_cpu = x_cpu[:n_cpu].contiguous()
@@ -298,70 +388,9 @@ def cfg_attention(dev, steps, warmup) -> Dict:
         wide_ref.attention(xs_cpu, xs_cpu, xs_cpu, *pc, hh)
 
     return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": lambda: wide(x), "parity": parity,
-            "roofline": roofline, "cpu": cpu_run, "cpu_samples": n_cpu * b,
+            "kernels": kernels, "cpu": cpu_run, "cpu_samples": n_cpu * b,
             "cpu_sample": f"{n_cpu} of the {n} models (the wide path has no cross-model terms), bf16",
             "extra": {"seq_len": s, "embed": d, "heads": hh}}
-
-
-def cfg_seq(dev, steps, warmup) -> Dict:
-    import torch
-    from wide_compiler import _hip, workloads
-    from oracle import wide_ref
-
-    work = workloads.seq_n64()
-    n, b = work.n, work.batch
-    ids_cpu = work.inputs["ids"]
-    _, _, t = ids_cpu.shape
-    wide = workloads.WideSeqModel([m.to(dev) for m in work.models]).eval()
-    ids = ids_cpu.to(dev)
-    hdim, v = wide.lstm.hidden_size, wide.fc.out_features
-    logits = torch.empty((n, b, t, v), device=dev, dtype=torch.bfloat16)
-
-    def parity():
-        with torch.inference_mode():
-            y = wide(ids)
-        errs = []
-        for k in (0, n - 1):
-            p = {kk: (vv.double() if torch.is_tensor(vv) else vv)
-                 for kk, vv in workloads.seq_params([work.models[k]]).items()}
-            errs.append(_rel(y[k:k + 1], wide_ref.seq_model(ids_cpu[k:k + 1], p)))
-        return max(errs)
-
-    def roofline():
-        with torch.inference_mode():
-            x = wide.ln(wide.emb(ids, per_model=True))
-            hs, _ = wide.lstm(x)
-            lstm = wide.lstm
-            a, ws = _hip.rnn_args(cell=_hip.CELL_LSTM, x=x, w_ih=lstm.weight_ih, w_hh=lstm.weight_hh,
-                                  b_ih=lstm.bias_ih, b_hh=lstm.bias_hh, h0=None, c0=None, out=hs,
-                                  h_n=None, c_n=None)
-            t_fc = _event_time(lambda: wide.fc.forward_into(hs, logits), steps // 10 + 1, 2)
-            t_rec = _event_time(lambda: _hip.rnn_phase(a, "recurrence", x), 3, 1)
-            t_proj = _event_time(lambda: _hip.rnn_phase(a, "input_projection", x), 5, 1)
-            t_emb = _event_time(lambda: wide.emb(ids, per_model=True), 10, 2)
-            t_ln = _event_time(lambda: wide.ln(x), 10, 2)
-        flops = 2.0 * n * b * t * hdim * v
-        return {"bound": "mfma", "kernel": "gemm_xlp_kernel (vocab projection 512 -> 8192 + bias, bf16)",
-                "flops_per_launch": flops, "sec": t_fc, "peak": PEAK["bf16_mfma"],
-                "other_kernels_us": {"lstm_recurrence_128_steps": t_rec * 1e6,
-                                     "lstm_input_projection_gemm": t_proj * 1e6,
-                                     "embedding_gather": t_emb * 1e6, "layernorm": t_ln * 1e6}}
-
-    n_cpu = 1
-    p_cpu = {kk: (vv.float() if torch.is_tensor(vv) and vv.is_floating_point() else vv)
-             for kk, vv in workloads.seq_params(work.models[:n_cpu]).items()}
-    p_cpu = {kk: (vv.to(torch.bfloat16) if torch.is_tensor(vv) and vv.is_floating_point() else vv)
-             for kk, vv in p_cpu.items()}
-    ids_sub = ids_cpu[:n_cpu, :4].contiguous()
-
-    def cpu_run():
-        wide_ref.seq_model(ids_sub, p_cpu)
-
-    return {"name": work.name, "n": n, "batch": b, "dtype": "bf16", "step": lambda: wide(ids),
-            "parity": parity, "roofline": roofline, "cpu": cpu_run, "cpu_samples": n_cpu * 4,
-            "cpu_sample": f"{n_cpu} of the {n} models, 4 of the {b} sequences (no cross-model or cross-sequence "
-                          f"terms), bf16",
-            "extra": {"seq_len": t, "vocab": v, "embed": 256, "hidden": hdim}}
 
 
 def cfg_groupnorm(dev, steps, warmup) -> Dict:
@@ -390,11 +419,10 @@ def cfg_groupnorm(dev, steps, warmup) -> Dict:
             y = wide(x)
         return _rel(y, wide_ref.group_norm(x_cpu.double(), w_cpu.double(), b_cpu.double(), groups, 1e-5))
 
-    def roofline():
+    def kernels():
         sec = _event_time(lambda: wide(x), steps, warmup)
-        byts = 2.0 * x.numel() * 4 + 2 * n * c * 4
-        return {"bound": "hbm", "kernel": "groupnorm_kernel (8192-element rows, fp32)", "bytes_per_launch": byts,
-                "sec": sec, "peak": PEAK["hbm"]}
+        return [_kernel("groupnorm_kernel (8192-element rows, fp32)", "hbm", sec,
+                        byts=2.0 * x.numel() * 4 + 2 * n * c * 4)]
 
     n_cpu = 8
 
@@ -402,23 +430,145 @@ def cfg_groupnorm(dev, steps, warmup) -> Dict:
         wide_ref.group_norm(x_cpu[:n_cpu], w_cpu[:n_cpu * c], b_cpu[:n_cpu * c], groups, 1e-5)
 
     return {"name": f"WideGroupNorm N={n} B={b} C={c} G={groups} {hw}x{hw} fp32", "n": n, "batch": b,
-            "dtype": "fp32", "step": lambda: wide(x), "parity": parity, "roofline": roofline, "cpu": cpu_run,
+            "dtype": "fp32", "step": lambda: wide(x), "parity": parity, "kernels": kernels, "cpu": cpu_run,
             "cpu_samples": n_cpu * b, "cpu_sample": f"{n_cpu} of the {n} models (no cross-model terms)",
             "extra": {"channels": c, "groups": groups, "spatial": [hw, hw]}}
 
 
-CONFIGS = {"gru": cfg_gru, "mlp": cfg_mlp, "resblock": cfg_resblock, "attention": cfg_attention,
-           "seq": cfg_seq, "groupnorm": cfg_groupnorm}
+CONFIGS = {"seq": cfg_seq, "gru": cfg_gru, "mlp": cfg_mlp, "resblock": cfg_resblock, "attention": cfg_attention,
+           "groupnorm": cfg_groupnorm}
+EXTRA = ("mlp", "gru", "resblock", "attention")
+
+
+# ---------------------------------------------------------------------------------------
+# measurement
+# ---------------------------------------------------------------------------------------
+
+def _timed(step, k: int, w: int) -> float:
+    import torch
+    with torch.inference_mode():
+        for _ in range(w):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(k):
+            step()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+
+def _first(out):
+    return out[0] if isinstance(out, tuple) else out
+
+
+def _graph_of(step):
+    """The step captured as one HIP graph (after warm-up on a side stream), and whether a
+    replay's output equals an eager forward's bit for bit.  The replay's output is copied
+    before the eager forward runs, since a step may write into a persistent buffer."""
+    import torch
+    with torch.inference_mode():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                step()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_out = step()
+        graph.replay()
+        replayed = _first(static_out).clone()
+        eager = _first(step())
+        torch.cuda.synchronize()
+        same = torch.equal(replayed, eager)
+    return graph, same
+
+
+def _run_config(cfg: Dict, steps: int, warmup: int, mode: str) -> Dict:
+    """value / mode / parity / kernels of one configuration."""
+    import torch
+    n, b = cfg["n"], cfg["batch"]
+    step = cfg["step"]
+    parity = cfg["parity"]()
+    eager_s = _timed(step, steps, warmup)
+    graph_s, graph = None, None
+    if mode in ("graph", "best"):
+        graph, same = _graph_of(step)
+        if not same:
+            raise RuntimeError("graph replay differs from the eager forward")
+        graph_s = _timed(graph.replay, steps, warmup)
+    if mode == "eager" or graph_s is None:
+        wall, used = eager_s, "eager"
+    elif mode == "graph":
+        wall, used = graph_s, "graph"
+    else:
+        wall, used = (graph_s, "graph") if graph_s <= eager_s else (eager_s, "eager")
+    with torch.inference_mode():
+        kernels = cfg["kernels"]()
+    dom = max(kernels, key=lambda k: k["us_per_launch"] * k["launches_per_step"])
+    return {"wall": wall, "mode": used, "eager_s": eager_s, "graph_s": graph_s, "graph": graph,
+            "parity": parity, "kernels": kernels, "dominant": dom,
+            "samples_per_s": n * b * steps / wall, "ms_per_step": wall / steps * 1e3}
+
+
+def _pack_leg(dev) -> Dict:
+    """The boundary byte-movement kernels at the ResBlock configuration's size (100 tensors of
+    [8, 64, 32, 32] bf16, 104.9 MB): wc_pack_rows (pack from N separate tensors) and wc_swap01
+    (channel-packed -> N-first transpose).  Bytes = 2 * numel * sizeof (read + write)."""
+    import torch
+    from wide_compiler import _hip
+    n, b, c, hw = 100, 8, 64, 32
+    srcs = [torch.randn(b, c, hw, hw, device=dev).to(torch.bfloat16) for _ in range(n)]
+    packed = torch.empty(b, n * c, hw, hw, device=dev, dtype=torch.bfloat16)
+    row = c * hw * hw * 2
+    nfirst = torch.empty(n, b, c, hw, hw, device=dev, dtype=torch.bfloat16)
+    t_pack = _event_time(lambda: _hip.pack_rows(srcs, packed, b, row, [row] * n), 10, 2)
+    t_swap = _event_time(lambda: _hip.swap01(packed, b, n, n * row, row, row, nfirst), 10, 2)
+    byts = 2.0 * n * b * c * hw * hw * 2
+    return {"pack_rows": _kernel("seg_copy_kernel<PackMap> (wc_pack_rows, 100 x [8,64,32,32] bf16)", "hbm",
+                                 t_pack, byts=byts),
+            "boundary_transpose": _kernel("seg_copy_kernel (wc_swap01, [8,6400,32,32] -> [100,8,64,32,32] bf16)",
+                                          "hbm", t_swap, byts=byts)}
+
+
+def _cpu_info() -> Dict:
+    import torch
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()
+            if q != "max":
+                quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    cfg = torch.__config__.show()
+    blas = [ln.strip() for ln in cfg.split("\n") if "MKL" in ln or "LAPACK" in ln]
+    build = [ln for ln in cfg.split(",") if "BLAS_INFO" in ln or "USE_MKLDNN" in ln]
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "cgroup_cpu_quota": quota, "threads": threads, "torch": torch.__version__,
+            "blas": "; ".join(blas + [b.strip() for b in build])}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", choices=sorted(CONFIGS), default="gru")
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="seq")
     ap.add_argument("--mode", choices=("best", "graph", "eager"), default="best")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configurations and the pack leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the reference kernel whose "
@@ -441,53 +591,15 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 5}))
         return 0
+
     cfg = CONFIGS[args.config](dev, args.steps, args.warmup)
     n, b = cfg["n"], cfg["batch"]
-    step = cfg["step"]
-    parity = cfg["parity"]()
-
-    def timed(fn, k, w):
-        with torch.inference_mode():
-            for _ in range(w):
-                fn()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(k):
-                fn()
-            torch.cuda.synchronize()
-            return time.perf_counter() - t0
-
-    eager_s = timed(step, args.steps, args.warmup)
-    graph_s = None
-    if args.mode in ("graph", "best"):
-        with torch.inference_mode():
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                for _ in range(3):
-                    step()
-            torch.cuda.current_stream().wait_stream(s)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                static_out = step()
-            eager_out = step()
-        graph_s = timed(graph.replay, args.steps, args.warmup)
-        with torch.inference_mode():
-            torch.cuda.synchronize()
-            go = static_out[0] if isinstance(static_out, tuple) else static_out
-            eo = eager_out[0] if isinstance(eager_out, tuple) else eager_out
-            if not torch.equal(go, eo):
-                print("bench.py: graph replay differs from the eager forward", file=sys.stderr)
-                return 3
-    if args.mode == "eager" or graph_s is None:
-        wall, used = eager_s, "eager"
-    elif args.mode == "graph":
-        wall, used = graph_s, "graph"
-    else:
-        wall, used = (graph_s, "graph") if graph_s <= eager_s else (eager_s, "eager")
+    r = _run_config(cfg, args.steps, args.warmup, args.mode)
+    print(f"bench: {args.config} {r['samples_per_s']:.4g} samples/s ({r['mode']}), parity {r['parity']:.3e}",
+          file=sys.stderr, flush=True)
 
     # hot / cold cache regimes: per-step GPU times in the mode used
-    run_step = graph.replay if used == "graph" else step
+    run_step = r["graph"].replay if r["mode"] == "graph" else cfg["step"]
     with torch.inference_mode():
         hot = _step_times(run_step, args.steps)
         flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
@@ -495,58 +607,81 @@ def main() -> int:
         del flush
     hot_med, cold_med = _median(hot), _median(cold)
 
-    with torch.inference_mode():
-        rf = cfg["roofline"]()
-    if "flops_per_launch" in rf:
-        achieved = rf["flops_per_launch"] / rf["sec"]
-        unit, scale = "TFLOP/s", 1e12
-    else:
-        achieved = rf["bytes_per_launch"] / rf["sec"]
-        unit, scale = "GB/s", 1e9
-    roofline = {"bound": rf["bound"], "achieved": achieved / scale, "peak": rf["peak"] / scale, "unit": unit,
-                "frac": achieved / rf["peak"], "traffic": None, "kernel": rf["kernel"],
-                "us_per_launch": rf["sec"] * 1e6}
-    for key in ("flops_per_launch", "bytes_per_launch", "other_kernels_us"):
-        if key in rf:
-            roofline[key] = rf[key]
+    dom = dict(r["dominant"])
+    step_gpu_us = sum(k["us_per_launch"] * k["launches_per_step"] for k in r["kernels"])
+    roofline = {"bound": dom["bound"], "achieved": dom["achieved"], "peak": dom["peak"], "unit": dom["unit"],
+                "frac": dom["frac"], "traffic": None, "kernel": dom["kernel"], "us_per_launch": dom["us_per_launch"],
+                "share_of_step_kernel_time": dom["us_per_launch"] * dom["launches_per_step"] / step_gpu_us}
+    for key in ("flops_per_launch", "bytes_per_launch"):
+        if key in dom:
+            roofline[key] = dom[key]
     traffic_file = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
-            roofline["traffic"] = json.load(f).get("bytes_per_launch")
-
-    cpu = None
-    if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        torch.set_num_threads(threads)
-        with torch.inference_mode():
-            iters, el = _cpu_loop(cfg["cpu"], args.cpu_seconds)
-        cpu = {"value": cfg["cpu_samples"] * iters / el, "unit": "samples/s", "cores": threads, "kind": "port",
-               "sample": f"{iters} forwards of the oracle ({cfg['cpu_sample']}; torch CPU ops, {threads} threads) "
-                         f"in {el:.1f} s"}
+            tr = json.load(f)
+        if tr.get("kernel") == dom["kernel"]:
+            roofline["traffic"] = tr.get("bytes_per_launch")
+    roofline["kernels"] = r["kernels"]
 
     line = {
         "metric": METRIC,
-        "value": n * b * args.steps / wall,
+        "value": r["samples_per_s"],
         "unit": "samples/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": wall / args.steps * 1e3,
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": cfg["dtype"],
-        "data": "synthetic (seeded torch.nn default init, inputs ~ N(0,1))",
-        "config": {"workload": cfg["name"], "n_models": n, "batch": b, "mode": used, **cfg["extra"]},
+        "data": "synthetic (seeded torch.nn default init, inputs ~ N(0,1) / uniform ids)",
+        "config": {"workload": cfg["name"], "n_models": n, "batch": b, "mode": r["mode"], **cfg["extra"]},
         "roofline": roofline,
-        "eager_samples_per_s": n * b * args.steps / eager_s,
-        "cache_regimes": {"mode": used, "steps": args.steps, "flush_bytes": 512 << 20,
+        "eager_samples_per_s": n * b * args.steps / r["eager_s"],
+        "graph_samples_per_s": None if r["graph_s"] is None else n * b * args.steps / r["graph_s"],
+        "cache_regimes": {"mode": r["mode"], "steps": args.steps, "flush_bytes": 512 << 20,
                           "hot_median_ms": hot_med * 1e3, "hot_samples_per_s": n * b / hot_med,
                           "cold_median_ms": cold_med * 1e3, "cold_samples_per_s": n * b / cold_med},
-        "graph_samples_per_s": None if graph_s is None else n * b * args.steps / graph_s,
-        "parity_rel_err_vs_oracle": parity,
-        "cpu_baseline": cpu,
+        "parity_rel_err_vs_oracle": r["parity"],
     }
+    del r["graph"]
+
+    if not args.no_extra:
+        extra: Dict[str, Dict] = {}
+        for name in EXTRA:
+            if name == args.config:
+                continue
+            c = CONFIGS[name](dev, args.steps, args.warmup)
+            rc = _run_config(c, args.steps, args.warmup, args.mode)
+            d = rc["dominant"]
+            extra[name] = {"workload": c["name"], "value": rc["samples_per_s"], "unit": "samples/s",
+                           "ms_per_step": rc["ms_per_step"], "mode": rc["mode"], "dtype": c["dtype"],
+                           "parity_rel_err_vs_oracle": rc["parity"],
+                           "roofline": {"kernel": d["kernel"], "bound": d["bound"], "achieved": d["achieved"],
+                                        "peak": d["peak"], "unit": d["unit"], "frac": d["frac"],
+                                        "us_per_launch": d["us_per_launch"]},
+                           "kernels": rc["kernels"]}
+            print(f"bench: {name} {rc['samples_per_s']:.4g} samples/s ({rc['mode']}), {d['kernel'].split()[0]} "
+                  f"{d['frac']:.3f}", file=sys.stderr, flush=True)
+            del c, rc
+            torch.cuda.empty_cache()
+        with torch.inference_mode():
+            extra["pack"] = _pack_leg(dev)
+        line["configs"] = extra
+
+    cpu = None
+    if not args.no_cpu:
+        info = _cpu_info()
+        torch.set_num_threads(info["threads"])
+        with torch.inference_mode():
+            iters, el = _cpu_loop(cfg["cpu"], args.cpu_seconds)
+        cpu = {"value": cfg["cpu_samples"] * iters / el, "unit": "samples/s", "cores": info["threads"],
+               "kind": "port",
+               "sample": f"{iters} forwards of the oracle ({cfg['cpu_sample']}; torch CPU ops, "
+                         f"{torch.get_num_threads()} threads) in {el:.1f} s",
+               **info, "torch_threads": torch.get_num_threads()}
+    line["cpu_baseline"] = cpu
     print(json.dumps(line))
     return 0
 

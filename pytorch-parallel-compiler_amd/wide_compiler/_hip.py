@@ -370,6 +370,8 @@ def rnn_sync_check(block: bool = False) -> None:
     cross-workgroup wait (its outputs are then invalid).  block=True waits for every
     launch still in flight."""
     global _rnn_pending
+    if not _rnn_pending or torch.cuda.is_current_stream_capturing():
+        return                       # events cannot be queried while a graph is captured
     keep, failed = [], 0
     for ev, host in _rnn_pending:
         if block:
