@@ -224,6 +224,19 @@ int32_t wc_rnn_input_projection(const wc_rnn_args* args, void* stream);
 int32_t wc_rnn_recurrence(const wc_rnn_args* args, void* stream);
 
 /*
+ * wc_rnn_forward without a caller-provided workspace: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid allocation).  The workspace is a file-scope
+ * device array of wc_rnn_noalloc_scratch_bytes() bytes (64 MiB), one per device,
+ * held from the first call on a device until the process ends; args->workspace and
+ * args->workspace_bytes are ignored.  Sizes whose wc_rnn_workspace_bytes exceeds it
+ * return WC_ERR_LIMIT.  The call allocates and frees nothing.  All calls on one device
+ * share its array: calls that overlap in time on one device race.
+ */
+int64_t wc_rnn_noalloc_scratch_bytes(void);
+int32_t wc_rnn_forward_noalloc(const wc_rnn_args* args, void* stream);
+
+/*
  * Grouped GEMM with fused epilogue -- replaces torch.einsum('noi,nbi->nbo')
  * + bias of WideLinear._forward_einsum (wide_compiler/core/primitives/
  * wide_linear.py:161-171), the projection einsums of WideAttention

@@ -149,6 +149,8 @@ SIGNATURES = {
     "wc_group_norm": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F, _I32, _I32, _I32, _P]),
     "wc_rnn_workspace_bytes": (_I64, [ctypes.POINTER(_RnnArgs)]),
     "wc_rnn_status_offset": (_I64, [ctypes.POINTER(_RnnArgs)]),
+    "wc_rnn_noalloc_scratch_bytes": (_I64, []),
+    "wc_rnn_forward_noalloc": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_forward": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_recurrence": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
@@ -326,9 +328,10 @@ def mlp2(*, n: int, m: int, in_features: int, hidden: int, out_features: int,
 
 def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional[Tensor],
              b_hh: Optional[Tensor], h0: Optional[Tensor], c0: Optional[Tensor], out: Tensor,
-             h_n: Optional[Tensor], c_n: Optional[Tensor], workspace: Optional[Tensor] = None):
-    """Fill the wc_rnn_args struct; allocates the fp32 workspace unless one is given.
-    Returns (args, workspace)."""
+             h_n: Optional[Tensor], c_n: Optional[Tensor], workspace: Optional[Tensor] = None,
+             allocate: bool = True):
+    """Fill the wc_rnn_args struct; allocates the workspace unless one is given or
+    allocate is False (then the struct carries no workspace).  Returns (args, workspace)."""
     n, batch, steps, in_size = x.shape
     hidden = w_hh.shape[-1]
     a = _RnnArgs()
@@ -340,6 +343,9 @@ def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional
     a.w_ih, a.w_hh, a.b_ih, a.b_hh = w_ih.data_ptr(), w_hh.data_ptr(), ptr(b_ih), ptr(b_hh)
     a.h0, a.c0 = ptr(h0), ptr(c0)
     a.out, a.h_n, a.c_n = out.data_ptr(), ptr(h_n), ptr(c_n)
+    if not allocate and workspace is None:
+        a.workspace, a.workspace_bytes = None, 0
+        return a, None
     need = int(lib().wc_rnn_workspace_bytes(ctypes.byref(a)))
     ws = workspace
     if ws is None or ws.numel() * ws.element_size() < need:
@@ -391,6 +397,13 @@ def rnn_forward(**kw) -> None:
     a, ws = rnn_args(**kw)
     _check(lib().wc_rnn_forward(ctypes.byref(a), stream_of(kw["x"])), "wc_rnn_forward")
     _rnn_watch(a, ws)
+
+
+def rnn_forward_noalloc(**kw) -> None:
+    """wc_rnn_forward_noalloc: the same forward with the workspace in the library's static
+    per-device scratch; nothing is allocated for the call."""
+    a, _ = rnn_args(allocate=False, **kw)
+    _check(lib().wc_rnn_forward_noalloc(ctypes.byref(a), stream_of(kw["x"])), "wc_rnn_forward_noalloc")
 
 
 def rnn_phase(a: _RnnArgs, phase: str, like: Tensor) -> None:
