@@ -342,9 +342,18 @@ typedef struct wc_conv_args {
   int64_t r_stride_n, r_stride_b;
   void* y;
   int64_t y_stride_n, y_stride_b;
+  const void* weight;          /* the grouped filter bank [n*c_out, c_in, kh, kw] itself (contiguous,
+                                  16-byte aligned), read when packed_weight is NULL: allowed when
+                                  wc_conv2d_direct_weights returns 1 */
 } wc_conv_args;
 
 int32_t wc_conv2d(const wc_conv_args* args, void* stream);
+
+/* 1 when wc_conv2d runs these sizes from args->weight directly (packed_weight NULL):
+ * the resident-weight kernel (bf16 'same' convolution, stride 1, C_in 32 or 64, C_out a
+ * multiple of 64, the input widths it is built for) reads the module's filter bank in
+ * its own layout, so no packing pass precedes it; 0 otherwise (pack, then call). */
+int32_t wc_conv2d_direct_weights(const wc_conv_args* args);
 
 /*
  * Grouped 3-D convolution -- replaces the permute/reshape + grouped nn.Conv3d +

@@ -39,6 +39,7 @@ struct ConvParams {
   const void* x;
   int64_t x_sn, x_sb;
   const void* wp;           // packed weights [n][co][kh][kw][ci32]
+  const void* wn;           // or (resident-weight kernel only) the filter bank [n*co][ci][kh][kw]
   const void* bias;         // [n*co] or null
   const void* bn_w;         // eval BN params [n*co] (bn_mean null: no BN)
   const void* bn_b;
@@ -766,16 +767,19 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
     return it;
   };
 
-  // ---- zero the halo columns of both input buffers (never written again) ----
-  for (int e = tid; e < 2 * IR * (KW - 1) * NCH; e += 512) {
-    const int chunk = e % NCH;
-    int r = e / NCH;
-    const int hc = r % (KW - 1);
-    r /= (KW - 1);
-    const int row = r % IR, buf = r / IR;
-    const int col = hc < C::PW ? hc : W + hc;
-    *reinterpret_cast<u32x4*>(ilds + buf * C::IN_BYTES + (row * IC + col) * PXB + chunk * 16) = z4;
-  }
+  // ---- zero the halo columns of input buffers b0..b1-1 (staging never writes them) ----
+  auto zero_halo = [&](int b0, int b1) {
+    for (int e = tid; e < (b1 - b0) * IR * (KW - 1) * NCH; e += 512) {
+      const int chunk = e % NCH;
+      int r = e / NCH;
+      const int hc = r % (KW - 1);
+      r /= (KW - 1);
+      const int row = r % IR, buf = b0 + r / IR;
+      const int col = hc < C::PW ? hc : W + hc;
+      *reinterpret_cast<u32x4*>(ilds + buf * C::IN_BYTES + (row * IC + col) * PXB + chunk * 16) = z4;
+    }
+  };
+  zero_halo(0, 2);
 
   // ---- staging: NCHW 16-byte vectors -> registers -> channels-last LDS ----
   // unit u = (channel group cg fastest, 16-byte column vector v, staged row ir)
@@ -817,7 +821,7 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
 #pragma unroll
     for (int k = 0; k < C::UPT; ++k) {
       const int u = g_op + k * 256;
-      if (k == 0 || u < C::UNITS) {                    // (only a partial last round branches)
+      if (k + 1 < C::UPT || C::UNITS % 256 == 0 || u < C::UNITS) {   // (only a partial last round branches)
         const int cg = u % NCH, rest = u / NCH;
         const int v = rest % C::VPR, ir = rest / C::VPR;
         u32x4 t[8];
@@ -833,26 +837,65 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
 
   // ---- resident weights (all 512 threads) ----
   auto load_weights = [&](const ResItem& it) {
-    const bf16* wb = static_cast<const bf16*>(p.wp) +
-                     (static_cast<int64_t>(it.mdl) * p.co + it.tco * 64) * TAPS * CI;
-    // 16-byte pieces, ordered (co, tap, chunk) as in global memory; all loads are
-    // issued before the LDS stores so their latencies overlap
+    // 16-byte pieces in global order; all loads are issued before the LDS stores so
+    // their latencies overlap
     constexpr int PIECES = TAPS * 64 * NCH;
     constexpr int PPT = (PIECES + 511) / 512;
     u32x4 v[PPT];
+    // addresses are recomputed from an opaque copy of the thread index at every call, so
+    // the compiler does not keep them live (in registers the K loop needs) between calls
+    int t_op = tid;
+    asm volatile("" : "+v"(t_op));
+    if (p.wn) {
+      // the filter bank as the module holds it, [n*co][ci][kh][kw]: input channels
+      // chunk*8 .. chunk*8+7 of output channel co are 8 * TAPS contiguous elements
+      // ([ci][tap]), which thread (co, chunk) loads as TAPS 16-byte vectors and transposes in
+      // registers into one 16-byte piece per tap (channel k of tap t is element k*TAPS + t)
+      constexpr int PAIRS = 64 * NCH;
+      static_assert(PAIRS <= 512, "one (co, chunk) pair per thread");
+      if (t_op < PAIRS) {
+        const int chunk = t_op % NCH, co = t_op / NCH;
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            static_cast<const bf16*>(p.wn) +
+            ((static_cast<int64_t>(it.mdl) * p.co + it.tco * 64 + co) * CI + chunk * 8) * TAPS);
+        uint32_t in[TAPS * 4];
 #pragma unroll
-    for (int q = 0; q < PPT; ++q) {
-      const int e = tid + q * 512;
-      v[q] = e < PIECES ? *reinterpret_cast<const u32x4*>(wb + static_cast<int64_t>(e) * 8) : z4;
-    }
+        for (int t = 0; t < TAPS; ++t) {
+          const u32x4 a = src[t];
 #pragma unroll
-    for (int q = 0; q < PPT; ++q) {
-      const int e = tid + q * 512;
-      if (e < PIECES) {
-        const int chunk = e % NCH;
-        const int rest = e / NCH;
-        const int tap = rest % TAPS, co = rest / TAPS;
-        *reinterpret_cast<u32x4*>(wlds + (tap * 64 + co) * PXB + C::swz(chunk, co) * 16) = v[q];
+          for (int w = 0; w < 4; ++w) in[t * 4 + w] = a[w];
+        }
+        char* const dst = wlds + co * PXB + C::swz(chunk, co) * 16;
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t) {
+          uint32_t o[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const int m0 = 2 * w * TAPS + t, m1 = m0 + TAPS;   // low and high halves of word w
+            const uint32_t sel = ((m0 & 1) ? 0x0302u : 0x0100u) | ((m1 & 1) ? 0x07060000u : 0x05040000u);
+            o[w] = __builtin_amdgcn_perm(in[m1 >> 1], in[m0 >> 1], sel);
+          }
+          *reinterpret_cast<u32x4*>(dst + t * 64 * PXB) = u32x4{o[0], o[1], o[2], o[3]};
+        }
+      }
+    } else {
+      // packed [n][co][tap][ci]: pieces ordered (co, tap, chunk)
+      const bf16* wb = static_cast<const bf16*>(p.wp) +
+                       (static_cast<int64_t>(it.mdl) * p.co + it.tco * 64) * TAPS * CI;
+#pragma unroll
+      for (int q = 0; q < PPT; ++q) {
+        const int e = t_op + q * 512;
+        v[q] = e < PIECES ? *reinterpret_cast<const u32x4*>(wb + static_cast<int64_t>(e) * 8) : z4;
+      }
+#pragma unroll
+      for (int q = 0; q < PPT; ++q) {
+        const int e = t_op + q * 512;
+        if (e < PIECES) {
+          const int chunk = e % NCH;
+          const int rest = e / NCH;
+          const int tap = rest % TAPS, co = rest / TAPS;
+          *reinterpret_cast<u32x4*>(wlds + (tap * 64 + co) * PXB + C::swz(chunk, co) * 16) = v[q];
+        }
       }
     }
     // folded per-channel affine of the epilogue: y = acc * alpha + beta
@@ -1201,17 +1244,29 @@ int32_t conv_res_launch(ConvParams p, hipStream_t st) {
   return check_launch("wc_conv2d");
 }
 
-// Launches the resident-weight kernel when the geometry is one it is built
-// for; returns 1 (nothing launched) otherwise.
-int32_t conv_res_dispatch(ConvParams p, hipStream_t st) {
+// The (kh, kw, C_in, W) shapes the resident-weight kernel is instantiated for.
+bool res_shape(int kh, int kw, int ci, int w) {
+  return (kh == 3 && kw == 3 && ((ci == 64 && (w == 32 || w == 16)) || (ci == 32 && (w == 32 || w == 64)))) ||
+         (kh == 1 && kw == 3 && (ci == 64 || ci == 32) && w == 256);
+}
+
+// True when the resident-weight kernel runs these sizes (bf16 'same' convolution, stride
+// 1, C_in 32 / 64, C_out % 64 == 0, the vector alignments its loads and stores need).
+bool conv_res_ok(const ConvParams& p) {
   const bool same = p.sh == 1 && p.sw == 1 && p.dh == 1 && p.dw == 1 && p.ph == p.kh / 2 && p.pw == p.kw / 2 &&
                     (p.kh % 2) == 1 && (p.kw % 2) == 1 && p.ho == p.h && p.wo == p.w;
-  if (!same || p.co % 64 != 0 || !(p.ci == 32 || p.ci == 64)) return 1;
-  // 16-byte input vectors, 8-byte output / residual vectors
+  if (!same || p.co % 64 != 0 || !(p.ci == 32 || p.ci == 64) || !res_shape(p.kh, p.kw, p.ci, p.w)) return false;
+  // 16-byte input and weight vectors, 8-byte output / residual vectors
   if (!aligned(p.x, 16) || (p.x_sn % 8) || (p.x_sb % 8) || !aligned(p.y, 8) || (p.y_sn % 4) || (p.y_sb % 4) ||
-      !aligned(p.wp, 16))
-    return 1;
-  if (p.res && (!aligned(p.res, 8) || (p.r_sn % 4) || (p.r_sb % 4))) return 1;
+      !aligned(p.wn ? p.wn : p.wp, 16))
+    return false;
+  return !p.res || (aligned(p.res, 8) && (p.r_sn % 4) == 0 && (p.r_sb % 4) == 0);
+}
+
+// Launches the resident-weight kernel when conv_res_ok; returns 1 (nothing launched)
+// otherwise.
+int32_t conv_res_dispatch(ConvParams p, hipStream_t st) {
+  if (!conv_res_ok(p)) return 1;
   p.tiles_co = p.co / 64;
   const bool pf = p.pdt == WC_F32;
 #define WC_RES(KH, KW, CI, W)                                                                        \
@@ -1253,6 +1308,39 @@ extern "C" int64_t wc_conv_packed_weight_elems(int64_t n, int64_t c_out, int64_t
   return n * c_out * kh * kw * round32(static_cast<int>(c_in));
 }
 
+extern "C" int32_t wc_conv2d_direct_weights(const wc_conv_args* a) {
+  if (!a || a->dtype != WC_BF16 || !a->weight || a->n <= 0 || a->batch <= 0 || a->c_out <= 0 || a->h <= 0 ||
+      a->w <= 0 || a->stride_h <= 0 || a->stride_w <= 0 || a->dil_h <= 0 || a->dil_w <= 0)
+    return 0;
+  if (a->c_in * a->h * a->w >= 0x7fffffffll || a->n * a->c_out >= 0x7fffffffll) return 0;
+  ConvParams p = {};
+  p.ci = (int)a->c_in;
+  p.co = (int)a->c_out;
+  p.h = (int)a->h;
+  p.w = (int)a->w;
+  p.kh = (int)a->kh;
+  p.kw = (int)a->kw;
+  p.sh = (int)a->stride_h;
+  p.sw = (int)a->stride_w;
+  p.ph = (int)a->pad_h;
+  p.pw = (int)a->pad_w;
+  p.dh = (int)a->dil_h;
+  p.dw = (int)a->dil_w;
+  p.ho = (int)a->h_out;
+  p.wo = (int)a->w_out;
+  p.x = a->x;
+  p.x_sn = a->x_stride_n;
+  p.x_sb = a->x_stride_b;
+  p.wn = a->weight;
+  p.res = a->residual;
+  p.r_sn = a->r_stride_n;
+  p.r_sb = a->r_stride_b;
+  p.y = a->y;
+  p.y_sn = a->y_stride_n;
+  p.y_sb = a->y_stride_b;
+  return conv_res_ok(p) ? 1 : 0;
+}
+
 extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   clear_error();
   WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_conv2d: null args");
@@ -1270,7 +1358,7 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
              "wc_conv2d: output %lldx%lld does not match the geometry (%lldx%lld)", (long long)a->h_out,
              (long long)a->w_out, (long long)ho, (long long)wo);
   if (a->n == 0 || a->batch == 0 || a->c_out == 0 || ho <= 0 || wo <= 0) return WC_OK;
-  WC_REQUIRE(a->x && a->packed_weight && a->y, WC_ERR_NULL, "wc_conv2d: null pointer");
+  WC_REQUIRE(a->x && a->y && (a->packed_weight || a->weight), WC_ERR_NULL, "wc_conv2d: null pointer");
   WC_REQUIRE(a->c_in * a->h * a->w < 0x7fffffffll && a->c_out * ho * wo < 0x7fffffffll &&
                  a->n * a->c_out < 0x7fffffffll,
              WC_ERR_LIMIT, "wc_conv2d: sizes too large");
@@ -1296,6 +1384,7 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   p.x_sn = a->x_stride_n;
   p.x_sb = a->x_stride_b;
   p.wp = a->packed_weight;
+  p.wn = a->packed_weight ? nullptr : a->weight;
   p.bias = a->bias;
   p.bn_w = a->bn_weight;
   p.bn_b = a->bn_bias;
@@ -1327,6 +1416,13 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   const bool yal = aligned(p.y, 16) && (p.y_sn * es) % 16 == 0 && (p.y_sb * es) % 16 == 0;
   const bool ral = !p.res || (aligned(p.res, 16) && (p.r_sn * es) % 16 == 0 && (p.r_sb * es) % 16 == 0);
   p.vec_out = (yal && ral && p.tc % ve == 0 && p.wo % ve == 0) ? 1 : 0;
+  if (p.wn) {
+    // the filter bank itself: only the resident-weight kernel reads that layout
+    WC_REQUIRE(!f32 && conv_res_ok(p), WC_ERR_ARG,
+               "wc_conv2d: these sizes need packed weights (wc_conv_pack_weights); "
+               "wc_conv2d_direct_weights tells when the filter bank itself will do");
+    return conv_res_dispatch(p, as_stream(stream));
+  }
   WC_REQUIRE(aligned(p.wp, 16), WC_ERR_ALIGN, "wc_conv2d: packed weights not 16-byte aligned");
   const int64_t nblk = static_cast<int64_t>(p.n) * p.batch * p.tiles_r * p.tiles_c * p.tiles_co;
   WC_REQUIRE(nblk < 0x7fffffffll, WC_ERR_LIMIT, "wc_conv2d: too many tiles");
@@ -1427,6 +1523,7 @@ extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
   p.x_sn = a->x_stride_n;
   p.x_sb = a->x_stride_b;
   p.wp = a->packed_weight;
+  p.wn = nullptr;
   p.bias = a->bias;
   p.bn_w = p.bn_b = p.bn_mean = p.bn_var = nullptr;
   p.bn_eps = 0.f;

@@ -1,12 +1,13 @@
 """
 Build configuration of a wide model (mirror of wide_compiler/core/config.py:16-128).
 
-Only ``validate``, ``validate_rtol`` and ``debug`` change what this build does.  The
-``compile*`` fields are accepted for API compatibility: with ``compile=True`` the result is
-wrapped in ``torch.compile`` exactly as the reference does (api.py:138-147), and every HIP
-primitive is registered with torch.compiler as an opaque call, so inductor never generates
-code for the hot path.  ``precision``/``allow_tf32``/``validate_atol``/``fallback_passthrough``/
-``strict_architecture``/``profile``/``n`` are carried but unused, as in the reference.
+Only ``validate``, ``validate_rtol``, ``debug`` and the ``compile*`` fields change what this
+build does.  With ``compile=True`` the result is wrapped in ``torch.compile`` exactly as the
+reference does (api.py:138-147).  The HIP primitives are ctypes calls that dynamo does not
+trace into: each one ends a compiled region (a graph break) and runs as is, so inductor
+generates code only for the torch operations between them, never for the hot path.
+``precision``/``allow_tf32``/``validate_atol``/``fallback_passthrough``/``strict_architecture``/
+``profile``/``n`` are carried but unused, as in the reference.
 """
 
 from __future__ import annotations

@@ -1,11 +1,13 @@
 """
 Host side of the implicit-GEMM convolution shared by WideConv1d / WideConv2d.
 
-The filters are packed once into the kernel's K-contiguous layout [N, C_out, kh, kw, Ci32]
-by wc_conv_pack_weights and cached on the module; the cache is rebuilt whenever the filter
-tensor changes (new storage or an in-place update bumps its version counter).  A following
-eval BatchNorm, residual add and ReLU are applied in the conv epilogue when TracedWideModel
-has fused them (``fused_bn`` / ``fused_activation`` / the ``residual`` argument).
+The filters are read from the module's own parameter on every call, as the reference does:
+writes through ``.data`` do not bump a tensor's version counter, so no cache of a derived
+layout keyed on it could see them.  The resident-weight kernel stages the filter bank in its
+natural [N*C_out, C_in, kh, kw] layout; the other kernels take it packed into a K-contiguous
+layout [N, C_out, kh, kw, Ci32] by one small bandwidth kernel per call.  A following eval BatchNorm, residual add and ReLU
+are applied in the conv epilogue when TracedWideModel has fused them (``fused_bn`` /
+``fused_activation`` / the ``residual`` argument).
 """
 
 from __future__ import annotations
@@ -17,16 +19,6 @@ from torch import Tensor
 
 from ... import _hip
 from .._layout import inner_block_contiguous
-
-
-def _packed(mod, w: Tensor, kh: int, kw: int) -> Tensor:
-    key = (w.data_ptr(), w._version, w.dtype, w.device, tuple(w.shape))
-    cache = getattr(mod, "_wcache", None)
-    if cache is None or cache[0] != key:
-        wc = w if w.is_contiguous() else w.contiguous()
-        packed = _hip.conv_pack_weights(wc, mod.n, mod.out_channels, mod.in_channels, kh, kw)
-        mod._wcache = (key, packed)
-    return mod._wcache[1]
 
 
 def conv_forward(mod, x: Tensor, one_d: bool = False, residual: Optional[Tensor] = None,
@@ -79,8 +71,9 @@ def conv_forward(mod, x: Tensor, one_d: bool = False, residual: Optional[Tensor]
             residual = residual.contiguous()
     if y.numel() == 0:
         return y
-    packed = _packed(mod, w, kh, kw)
-    _hip.conv2d(x=x, packed_w=packed, n=n, c_in=ci, c_out=co, kernel=(kh, kw), stride=stride, padding=padding,
+    if not w.is_contiguous():
+        w = w.contiguous()
+    _hip.conv2d(x=x, weight=w, n=n, c_in=ci, c_out=co, kernel=(kh, kw), stride=stride, padding=padding,
                 dilation=dilation, y=y, bias=bias, bn=bn_args, residual=residual,
                 relu=mod.fused_activation == "relu")
     return y

@@ -89,19 +89,15 @@ class WideAttention(nn.Module):
         return (out, None) if mha_mode else out
 
     def _qkv_params(self) -> Tuple[Tensor, Optional[Tensor]]:
-        """[q_weight; kv_weight] as one [N, 3D, D] weight (and [N, 3D] bias), rebuilt only when a
-        parameter changes (keyed by storage and version counter)."""
-        ps = (self.q_weight, self.kv_weight, self.q_bias, self.kv_bias)
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) if t is not None else None for t in ps)
-        cache = getattr(self, "_qkv_cache", None)
-        if cache is None or cache[0] != key:
-            with torch.no_grad():
-                w = torch.cat([self.q_weight, self.kv_weight], dim=1).contiguous()
-                bias = None
-                if self.q_bias is not None:
-                    bias = torch.cat([self.q_bias, self.kv_bias], dim=1).contiguous()
-            self._qkv_cache = (key, w, bias)
-        return self._qkv_cache[1], self._qkv_cache[2]
+        """[q_weight; kv_weight] as one [N, 3D, D] weight (and [N, 3D] bias), built on every call
+        (no cache: writes through ``.data`` do not bump the version counter a cache could key
+        on, and the reference reads its parameters on every call)."""
+        with torch.no_grad():
+            w = torch.cat([self.q_weight, self.kv_weight], dim=1)
+            bias = None
+            if self.q_bias is not None:
+                bias = torch.cat([self.q_bias, self.kv_bias], dim=1)
+        return w, bias
 
     def _project(self, x: Tensor, w: Tensor, w_sn: int, bias: Optional[Tensor], b_sn: int, o: int) -> Tensor:
         """[N, B, T, D] @ W[n]^T + b -> [N, B, T, o] via the grouped GEMM (x read in place)."""

@@ -62,7 +62,24 @@ class WideConv1d(nn.Module):
                     nn.init.uniform_(self.bias[i], -bound, bound)
         self.fused_bn = None
         self.fused_activation = None
-        self._wcache = None
+        self._register_load_state_dict_pre_hook(self._load_any_layout)
+
+    def _load_any_layout(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                         error_msgs):
+        """Accept either of the reference's layouts, whichever strategy this module uses: the
+        reference picks ``op.*`` (grouped, N >= 10) or ``weight`` / ``bias`` (sequential) from N
+        (wide_conv1d.py:80-105), so a checkpoint of one strategy loads into the other here."""
+        n, co, ci, k = self.n, self.out_channels, self.in_channels, self.kernel_size
+        grouped = self.strategy == Conv1dStrategy.GROUPED
+        src, dst = (("weight", "bias"), ("op.weight", "op.bias")) if grouped else \
+            (("op.weight", "op.bias"), ("weight", "bias"))
+        if prefix + src[0] not in state_dict or prefix + dst[0] in state_dict:
+            return
+        w = state_dict.pop(prefix + src[0])
+        state_dict[prefix + dst[0]] = w.reshape(n * co, ci, k) if grouped else w.reshape(n, co, ci, k)
+        if prefix + src[1] in state_dict:
+            b = state_dict.pop(prefix + src[1])
+            state_dict[prefix + dst[1]] = b.reshape(-1) if grouped else b.reshape(n, co)
 
     # uniform view of the filters for the kernel: [N*C_out, C_in, 1, k] and [N*C_out]
     def _filters(self):

@@ -80,7 +80,6 @@ class WideConv2d(nn.Module):
         # epilogue fused in by TracedWideModel: a following eval BatchNorm, ReLU, residual add
         self.fused_bn = None
         self.fused_activation = None
-        self._wcache = None
 
     @property
     def strategy(self) -> ConvStrategy:

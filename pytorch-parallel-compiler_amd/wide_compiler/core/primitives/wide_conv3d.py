@@ -81,14 +81,10 @@ class WideConv3d(nn.Module):
         return self.convs[0], w, b
 
     def _packed(self, w: Tensor, kd: int, kh: int, kw: int) -> Tensor:
-        parts = [self.conv.weight] if self._use_grouped else [c.weight for c in self.convs]
-        key = tuple((t.data_ptr(), t._version) for t in parts) + (w.dtype, w.device, tuple(w.shape))
-        cache = getattr(self, "_wcache", None)
-        if cache is None or cache[0] != key:
-            wc = w if w.is_contiguous() else w.contiguous()
-            packed = _hip.conv_pack_weights(wc, self.n, self.out_channels, self.in_channels, kd * kh, kw)
-            self._wcache = (key, packed)
-        return self._wcache[1]
+        """The filters in the kernel's layout, packed on every call (no cache: writes through
+        ``.data`` do not bump the version counter a cache could key on)."""
+        wc = w if w.is_contiguous() else w.contiguous()
+        return _hip.conv_pack_weights(wc, self.n, self.out_channels, self.in_channels, kd * kh, kw)
 
     def forward(self, x: Tensor) -> Tensor:
         what = "WideConv3d"

@@ -162,6 +162,20 @@ def _method_caller(name: str):
     return caller
 
 
+class _WideTracer(fx.Tracer):
+    """fx's default tracer (what the reference's fx.symbolic_trace uses, traced_wide.py:306),
+    except that a module whose type name is in the registry stays one call_module node, so
+    that the wide primitive registered for it replaces it; fx would otherwise trace through a
+    user-defined module and the registration could never apply."""
+
+    def __init__(self, registered):
+        super().__init__()
+        self._registered = registered
+
+    def is_leaf_module(self, m: nn.Module, module_qualified_name: str) -> bool:
+        return type(m).__name__ in self._registered or super().is_leaf_module(m, module_qualified_name)
+
+
 class TracedWideModel(nn.Module):
     def __init__(self, n: int):
         super().__init__()
@@ -193,7 +207,8 @@ class TracedWideModel(nn.Module):
         wide = cls(n)
         template = models[0]
         try:
-            traced = fx.symbolic_trace(template)
+            tracer = _WideTracer(set(get_registry().list_registered()))
+            traced = fx.GraphModule(template, tracer.trace(template))
         except Exception as e:  # noqa: BLE001 - reported as in the reference
             raise RuntimeError(f"FX tracing failed: {e}. Model may have dynamic control flow.")
         wide._graph = traced.graph
@@ -343,7 +358,10 @@ class TracedWideModel(nn.Module):
                     if isinstance(prod, (WideConv2d, WideConv1d)) and prod.fused_activation is None and \
                             src not in self._residual_of and sole_user(main, name) and \
                             order.get(other_src, -1) < order[src] and other_src != src:
-                        self._residual_of[src] = other
+                        # the residual is read from the stage that computes it: an alias of
+                        # it (a ReLU folded into that stage) may come after the conv in fx
+                        # order, and its value would not exist yet when the conv runs
+                        self._residual_of[src] = other_src
                         self._aliases[name] = main
                         break
                 continue

@@ -117,7 +117,7 @@ def test_conv_fused_bn_residual_relu(hip, dtype):
     (3, 2, 64, 64, 32, 32, False),     # one 64-channel tile, 8-row blocks
     (5, 3, 64, 128, 20, 32, True),     # two channel tiles, partial last row block
     (7, 2, 32, 64, 9, 64, True),       # C_in 32, 4-row blocks
-    (40, 4, 64, 64, 16, 16, True),     # more items than workgroups, model changes inside a range
+    (100, 3, 64, 64, 16, 16, True),    # more items than workgroups, model changes inside a range
     (2, 1, 32, 64, 32, 32, False),
 ])
 def test_conv2d_resident_weights(hip, n, b, ci, co, h, w, fused):
@@ -145,6 +145,41 @@ def test_conv2d_resident_weights(hip, n, b, ci, co, h, w, fused):
     with torch.no_grad():
         y = conv(x.to(DEV), **kw).cpu()
     assert rel_err(y, ref) <= TOL_BF16
+
+
+@pytest.mark.parametrize("kh,n,b,ci,w,h", [
+    (3, 40, 4, 64, 32, 32),            # 640 items over 256 workgroups: 2-3 items each, model changes inside
+    (3, 100, 6, 64, 16, 16),
+    (3, 40, 4, 32, 32, 32),            # C_in 32: fewer staging units than threads in a group
+    (3, 30, 4, 32, 64, 20),            # partial last row block
+    (1, 100, 8, 64, 256, 1),           # the 1x3 kernel (Conv1d over L = 256)
+    (1, 100, 8, 32, 256, 1),
+])
+def test_resident_kernel_weight_layouts_agree(hip, monkeypatch, kh, n, b, ci, w, h):
+    """The resident-weight kernel staging the module's filter bank directly (through a free
+    input buffer, whose zero halo columns must survive) and staging the packed copy give
+    bit-identical outputs matching the oracle, with several items per workgroup so that both
+    groups of a workgroup stage inputs and weights are reloaded at model boundaries."""
+    from wide_compiler import _hip
+    g = gen(215)
+    co = 64
+    x = _rand((n, b, ci, h, w), g, torch.bfloat16).to(DEV)
+    wt = (_rand((n * co, ci, kh, 3), g) * 0.1).to(torch.bfloat16).to(DEV)
+    bias = _rand((n * co,), g).to(DEV)
+    packs = []
+    real_pack = _hip.conv_pack_weights
+    monkeypatch.setattr(_hip, "conv_pack_weights", lambda *a: packs.append(1) or real_pack(*a))
+    outs = []
+    for packed in (False, True):
+        y = torch.full((n, b, co, h, w), float("nan"), dtype=torch.bfloat16, device=DEV)
+        _hip.conv2d(x=x, weight=wt, n=n, c_in=ci, c_out=co, kernel=(kh, 3), stride=(1, 1),
+                    padding=(kh // 2, 1), dilation=(1, 1), y=y, bias=bias, relu=True, packed=packed)
+        outs.append(y.cpu())
+    assert len(packs) == 1                              # only the packed=True call packed
+    assert torch.equal(outs[0], outs[1])
+    ref = F.relu(wide_ref.conv2d(x.cpu().double(), wt.cpu().double(), bias.cpu().double(), n,
+                                 padding=(kh // 2, 1)))
+    assert rel_err(outs[0], ref) <= TOL_BF16
 
 
 def test_conv1d_resident_weights(hip):
