@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define WC_ABI_VERSION 1
+#define WC_ABI_VERSION 2
 
 /* element types */
 enum {
@@ -401,6 +401,12 @@ typedef struct wc_attn_args {
   int64_t v_stride_nb, v_stride_s;
   void* o;
   int64_t o_stride_nb, o_stride_s;
+  const void* mask;            /* optional additive fp32 mask (NULL = none; not with causal):
+                                  element (nb, head, query, key) at mask + nb*mask_stride_nb +
+                                  head*mask_stride_head + query*mask_stride_q + key, added to the
+                                  scaled score (a boolean mask: 0 / -inf).  Strides may be 0
+                                  (broadcast).  A query row whose keys are all -inf gets zeros. */
+  int64_t mask_stride_nb, mask_stride_head, mask_stride_q;
 } wc_attn_args;
 
 int32_t wc_attention(const wc_attn_args* args, void* stream);

@@ -35,6 +35,10 @@ struct AttnParams {
   int64_t v_sb, v_ss;
   void* o;
   int64_t o_sb, o_ss;
+  // additive fp32 mask, element (nb, head, query, key) at nb*m_sb + head*m_sh + query*m_sq + key
+  // (general kernel only; NULL = none)
+  const float* mask;
+  int64_t m_sb, m_sh, m_sq;
 };
 
 constexpr int kAttnThreads = 256;
@@ -180,6 +184,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int q = q0 + nt * 16 + fr;
+      const float* mrow = (p.mask && q < p.sq) ? p.mask + nb * p.m_sb + h * p.m_sh + q * p.m_sq : nullptr;
       float tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -187,7 +192,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
         for (int e = 0; e < 4; ++e) {
           const int key = k0 + mt * 16 + g * 4 + e;
           float sv = sacc[mt][nt][e] * p.scale_log2;
-          if (key >= p.skv || (p.causal && key > q)) sv = -INFINITY;
+          if (key >= p.skv || (p.causal && key > q))
+            sv = -INFINITY;
+          else if (mrow)
+            sv += mrow[key] * 1.4426950408889634f;        // natural-log mask -> the exp2 domain
           sacc[mt][nt][e] = sv;
           tmax = fmaxf(tmax, sv);
         }
@@ -649,7 +657,16 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
   p.o = a->o;
   p.o_sb = a->o_stride_nb;
   p.o_ss = a->o_stride_s;
-  if (a->dtype == WC_BF16 && (a->head_dim == 32 || a->head_dim == 64)) {
+  p.mask = static_cast<const float*>(a->mask);
+  p.m_sb = a->mask_stride_nb;
+  p.m_sh = a->mask_stride_head;
+  p.m_sq = a->mask_stride_q;
+  if (p.mask) {
+    WC_REQUIRE(a->mask_stride_nb >= 0 && a->mask_stride_head >= 0 && a->mask_stride_q >= 0, WC_ERR_ARG,
+               "wc_attention: negative mask stride");
+    WC_REQUIRE(!a->causal, WC_ERR_ARG, "wc_attention: a mask and causal masking are exclusive");
+  }
+  if (!p.mask && a->dtype == WC_BF16 && (a->head_dim == 32 || a->head_dim == 64)) {
     // resident-KV kernel: K and V of one head in LDS, 8-byte aligned output rows
     const int skvp = static_cast<int>(cdiv(a->skv, 32) * 32);
     const bool o_al = aligned(a->o, 8) && (a->o_stride_nb * es) % 8 == 0 && (a->o_stride_s * es) % 8 == 0;

@@ -716,8 +716,10 @@ struct ResItem {
 
 constexpr uint32_t kResOob = 0x80000000u;            // buffer offset of a dropped / zero lane
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t res_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+// A buffer descriptor over one (model, batch row) block of `bytes` bytes: offsets past it
+// (kResOob included) read zero / store nothing.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t res_rsrc(const void* base, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
 // 8x8 bf16 transpose with v_perm_b32: in[q] = 8 pixels of channel q -> out[x] =
@@ -799,7 +801,7 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
     const bool valid = t < count;
     const ResItem it = decode(valid ? t : 0);
     const __amdgpu_buffer_rsrc_t rs =
-        res_rsrc(static_cast<const bf16*>(p.x) + it.mdl * p.x_sn + it.b * p.x_sb);
+        res_rsrc(static_cast<const bf16*>(p.x) + it.mdl * p.x_sn + it.b * p.x_sb, CI * p.h * W * 2);
     const int r0 = it.th * TR - C::PH;
 #pragma unroll
     for (int k = 0; k < C::UPT; ++k) {
@@ -1005,7 +1007,7 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
   //
   // Regrouping of tile j.  After the MFMAs lane (fr, kq) holds channel j*16 + fr at
   // pixels i*16 + kq*4 + [0, 4) of the wave's 64 (row tiles i = 0..3), packed to bf16
-  // pairs: X = tiles 0, 2 and Y = tiles 1, 3.  (1) v_permlane16_swap exchanges X of
+  // pairs: X = tiles 0, 2 and Y = tiles 1, 3.  (1) a 16-lane-row swap exchanges X of
   // the odd 16-lane rows (kq = 1, 3) with Y of the even rows, so every lane holds two
   // 8-pixel chunks of its channel, chunk s = {X[2s], X[2s+1], Y[2s], Y[2s+1]} at
   // pixels 8 (4 s + 2 (kq & 1) + (kq >> 1)).  (2) Lanes fr and fr ^ 1 (a DPP quad
@@ -1016,7 +1018,7 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
   auto res_issue = [&](int j0) {
     const ResItem& it = fin_it;
     const __amdgpu_buffer_rsrc_t rrs =
-        res_rsrc(static_cast<const bf16*>(p.res) + it.mdl * p.r_sn + it.b * p.r_sb);
+        res_rsrc(static_cast<const bf16*>(p.res) + it.mdl * p.r_sn + it.b * p.r_sb, p.co * how * 2);
     const uint32_t obase = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
     const int left = p.ho - it.th * TR;
     const uint32_t off = lane_orow < (left < TR ? left : TR) ? lane_off : kResOob;
@@ -1030,7 +1032,8 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
   auto finish = [&](auto res, int j0) {
     constexpr bool kRes = decltype(res)::value;
     const ResItem& it = fin_it;
-    const __amdgpu_buffer_rsrc_t yrs = res_rsrc(static_cast<bf16*>(p.y) + it.mdl * p.y_sn + it.b * p.y_sb);
+    const __amdgpu_buffer_rsrc_t yrs =
+        res_rsrc(static_cast<bf16*>(p.y) + it.mdl * p.y_sn + it.b * p.y_sb, p.co * how * 2);
     const uint32_t obase = static_cast<uint32_t>(it.tco * 64 * how + it.th * TR * W) * 2u;
     const int left = p.ho - it.th * TR;
     const uint32_t off = lane_orow < (left < TR ? left : TR) ? lane_off : kResOob;
@@ -1050,11 +1053,16 @@ __global__ __launch_bounds__(512, 1) void conv_res_kernel(ConvParams p, int per_
           }
           xy[i & 1][(i >> 1) * 2 + h] = pack_bf16x2(v0, v1);
         }
+      // (1) as a lane-crossbar shuffle: v_permlane16_swap here gave wrong words now and then
+      // (timing-dependent; the compiler's wait states around it did not cover it)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const auto sw = __builtin_amdgcn_permlane16_swap(xy[0][k], xy[1][k], false, false);
-        xy[0][k] = sw[0];
-        xy[1][k] = sw[1];
+        const bool odd_row = (kq & 1) != 0;
+        const uint32_t recv = static_cast<uint32_t>(__shfl_xor(static_cast<int>(odd_row ? xy[0][k] : xy[1][k]), 16, 64));
+        if (odd_row)
+          xy[0][k] = recv;
+        else
+          xy[1][k] = recv;
       }
       uint32_t va[4], vb[4];
 #pragma unroll
@@ -1256,6 +1264,10 @@ bool conv_res_ok(const ConvParams& p) {
   const bool same = p.sh == 1 && p.sw == 1 && p.dh == 1 && p.dw == 1 && p.ph == p.kh / 2 && p.pw == p.kw / 2 &&
                     (p.kh % 2) == 1 && (p.kw % 2) == 1 && p.ho == p.h && p.wo == p.w;
   if (!same || p.co % 64 != 0 || !(p.ci == 32 || p.ci == 64) || !res_shape(p.kh, p.kw, p.ci, p.w)) return false;
+  // one (model, batch row) block of x and of y / residual in bytes: a buffer descriptor's range
+  if (static_cast<int64_t>(p.ci) * p.h * p.w * 2 >= 0x7fffffffll ||
+      static_cast<int64_t>(p.co) * p.ho * p.wo * 2 >= 0x7fffffffll)
+    return false;
   // 16-byte input and weight vectors, 8-byte output / residual vectors
   if (!aligned(p.x, 16) || (p.x_sn % 8) || (p.x_sb % 8) || !aligned(p.y, 8) || (p.y_sn % 4) || (p.y_sb % 4) ||
       !aligned(p.wn ? p.wn : p.wp, 16))

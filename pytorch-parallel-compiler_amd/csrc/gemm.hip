@@ -459,8 +459,8 @@ typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void* base, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
 // VMEM instructions one wave issues per tile epilogue: 32 stores (+ 32 residual
@@ -640,9 +640,10 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   // from 8 (lane & 15) ----
   lds_char* strip = smem + 2 * kXlStageBytes + wave * kXlStripBytes;
   auto epilogue = [&](const Tile& t, int ti_parity) {
-    const __amdgpu_buffer_rsrc_t crs = xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn);
+    const __amdgpu_buffer_rsrc_t crs =
+        xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn, p.c_bytes);
     const __amdgpu_buffer_rsrc_t rrs =
-        xl_rsrc(RES ? static_cast<const bf16*>(p.r) + static_cast<int64_t>(t.mdl) * p.r_sn : p.c);
+        xl_rsrc(RES ? static_cast<const bf16*>(p.r) + static_cast<int64_t>(t.mdl) * p.r_sn : p.c, p.r_bytes);
     constexpr bool relu = RELU;
     const int lane = lane_now();
     const int fr = lane & 15;
@@ -808,6 +809,14 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
     read_frags((ti + 1) * KS, fp0, w0, a0);
   }
 }
+// Elements from one model's base to the end of the last of its m rows (of `width`
+// columns) addressed as (m / ri) * so + (m % ri) * si.
+inline int64_t xl_span(const GemmParams& p, int64_t so, int64_t si, int64_t ri, int64_t width) {
+  const int64_t outer = (p.m - 1) / ri;
+  const int64_t inner = p.m - 1 < ri ? p.m - 1 : ri - 1;
+  return outer * so + inner * si + width;
+}
+
 
 template <typename TB>
 int32_t launch_xl(GemmParams p, hipStream_t st) {
@@ -824,6 +833,9 @@ int32_t launch_xl(GemmParams p, hipStream_t st) {
     cus = v;
   }
   const int grid = static_cast<int>(tiles < cus ? tiles : cus);
+  // bf16 C / R (the only XL output type); xl_shape_ok has bounded both below 2^31
+  p.c_bytes = static_cast<int32_t>(xl_span(p, p.c_so, p.c_si, p.c_ri.d, p.o) * 2);
+  p.r_bytes = p.r ? static_cast<int32_t>(xl_span(p, p.r_so, p.r_si, p.c_ri.d, p.o) * 2) : p.c_bytes;
   p.fd_ks = make_fastdiv(static_cast<uint32_t>(p.k / kXlBK));
   p.fd_tpm = make_fastdiv(static_cast<uint32_t>(p.tiles_m * p.tiles_o));
   p.fd_tm = make_fastdiv(static_cast<uint32_t>(p.tiles_m));
@@ -886,15 +898,10 @@ bool xl_shape_ok(const GemmParams& p) {
                                               static_cast<uint64_t>(p.r_si * es)}) >= 16;
   if (!c_ok || !r_ok) return false;
   const int64_t lim = 0x7fffffffll;
-  auto span = [&](int64_t so, int64_t si, int64_t ri, int64_t width) {
-    const int64_t outer = (p.m - 1) / ri;
-    const int64_t inner = p.m - 1 < ri ? p.m - 1 : ri - 1;
-    return outer * so + inner * si + width;
-  };
-  const int64_t a_end = span(p.a_so, p.a_si, p.a_ri.d, p.k) * 2;
+  const int64_t a_end = xl_span(p, p.a_so, p.a_si, p.a_ri.d, p.k) * 2;
   const int64_t w_end = static_cast<int64_t>(p.o) * p.k * 2;
-  const int64_t c_end = span(p.c_so, p.c_si, p.c_ri.d, p.o) * es;
-  const int64_t r_end = p.r ? span(p.r_so, p.r_si, p.c_ri.d, p.o) * es : 0;
+  const int64_t c_end = xl_span(p, p.c_so, p.c_si, p.c_ri.d, p.o) * es;
+  const int64_t r_end = p.r ? xl_span(p, p.r_so, p.r_si, p.c_ri.d, p.o) * es : 0;
   return a_end < lim && w_end < lim && c_end < lim && r_end < lim;
 }
 

@@ -25,8 +25,11 @@ struct GemmParams {
   void* c;
   int64_t c_sn, c_so, c_si;
   FastDiv c_ri;
-  // persistent XL kernel only: dividers of the stage -> tile -> (model, column tile) map
+  // persistent XL kernel only: dividers of the stage -> tile -> (model, column tile) map,
+  // and the byte extents of one model's C and R regions (their buffer descriptors' range,
+  // so a stray offset is dropped by the hardware instead of reaching other memory)
   FastDiv fd_ks, fd_tpm, fd_tm;
+  int32_t c_bytes, r_bytes;
 };
 
 // dtype: A/W element type; out_dtype: WC_F32 or dtype; bias_dtype: WC_F32 or dtype.

@@ -23,7 +23,7 @@ from typing import List, Optional, Sequence
 import torch
 from torch import Tensor
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16 = 0, 1, 2
 ACT_NONE, ACT_RELU = 0, 1
@@ -129,6 +129,8 @@ class _AttnArgs(ctypes.Structure):
         ("k", ctypes.c_void_p), ("k_stride_nb", ctypes.c_int64), ("k_stride_s", ctypes.c_int64),
         ("v", ctypes.c_void_p), ("v_stride_nb", ctypes.c_int64), ("v_stride_s", ctypes.c_int64),
         ("o", ctypes.c_void_p), ("o_stride_nb", ctypes.c_int64), ("o_stride_s", ctypes.c_int64),
+        ("mask", ctypes.c_void_p), ("mask_stride_nb", ctypes.c_int64), ("mask_stride_head", ctypes.c_int64),
+        ("mask_stride_q", ctypes.c_int64),
     ]
 
 
@@ -479,9 +481,11 @@ def conv3d(*, x: Tensor, packed_w: Tensor, n: int, c_in: int, c_out: int, kernel
 
 
 def attention(*, q: Tensor, k: Tensor, v: Tensor, o: Tensor, nb: int, heads: int, sq: int, skv: int,
-              head_dim: int, q_strides, k_strides, v_strides, o_strides, scale: float, causal: bool) -> None:
+              head_dim: int, q_strides, k_strides, v_strides, o_strides, scale: float, causal: bool,
+              mask: Optional[Tensor] = None) -> None:
     """q/k/v/o are base pointers (views) of [nb, S, heads*head_dim]-shaped data with the given
-    (stride_nb, stride_s) element strides."""
+    (stride_nb, stride_s) element strides; ``mask`` is an additive fp32 [nb, heads, sq, skv]
+    view with a unit key stride (other strides may be 0)."""
     a = _AttnArgs()
     a.dtype = dtype_code(q.dtype, "attention")
     a.causal = 1 if causal else 0
@@ -491,6 +495,13 @@ def attention(*, q: Tensor, k: Tensor, v: Tensor, o: Tensor, nb: int, heads: int
     a.k, (a.k_stride_nb, a.k_stride_s) = k.data_ptr(), k_strides
     a.v, (a.v_stride_nb, a.v_stride_s) = v.data_ptr(), v_strides
     a.o, (a.o_stride_nb, a.o_stride_s) = o.data_ptr(), o_strides
+    if mask is not None:
+        if mask.dtype != torch.float32 or tuple(mask.shape) != (nb, heads, sq, skv) or \
+                (skv > 1 and mask.stride(3) != 1) or mask.device != q.device:
+            raise ValueError("attention mask must be an fp32 [nb, heads, sq, skv] view with unit key stride "
+                             "on the query's device")
+        a.mask = mask.data_ptr()
+        a.mask_stride_nb, a.mask_stride_head, a.mask_stride_q = mask.stride(0), mask.stride(1), mask.stride(2)
     _check(lib().wc_attention(ctypes.byref(a), stream_of(q)), "wc_attention")
 
 

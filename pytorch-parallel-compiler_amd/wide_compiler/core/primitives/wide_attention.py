@@ -12,7 +12,10 @@ Execution (every strategy): the Q and K/V projections are grouped MFMA GEMMs wit
 in the epilogue (one K|V GEMM over kv_weight when key is value), the attention core is the
 fused flash-style kernel wc_attention reading Q/K/V in place in the projections' [N*B, S,
 heads*Dh] layout, and the output projection is a third grouped GEMM.  Inference only:
-dropout in training mode and explicit attention masks raise (``is_causal`` is supported).
+dropout in training mode raises.  ``attn_mask`` follows scaled_dot_product_attention over the
+[N*B, heads, Tq, Tkv] scores (wide_attention.py:222-228): boolean (True = attend) or additive,
+broadcastable to that shape, not together with ``is_causal``; a query whose keys are all masked
+gets zeros, as torch's SDPA gives.
 """
 
 from __future__ import annotations
@@ -110,6 +113,33 @@ class WideAttention(nn.Module):
                           c_sn=m * o, c_so=0, c_si=o, c_rows_inner=max(m, 1), bias=bias, bias_sn=b_sn)
         return out
 
+    @staticmethod
+    def _mask(attn_mask: Tensor, is_causal: bool, nb: int, hh: int, tq: int, tkv: int, dev) -> Tensor:
+        """attn_mask (SDPA semantics over [N*B, heads, Tq, Tkv]) as the kernel's additive fp32 view:
+        broadcast dimensions keep stride 0, so a [Tq, Tkv] mask is read, not copied N*B*heads times."""
+        what = "WideAttention"
+        if is_causal:
+            raise RuntimeError(f"{what}: attn_mask and is_causal cannot both be set (as in "
+                               "scaled_dot_product_attention)")
+        if attn_mask.device != dev:
+            raise RuntimeError(f"{what}: attn_mask is on {attn_mask.device}, the inputs on {dev}")
+        if attn_mask.dim() > 4:
+            raise RuntimeError(f"{what}: attn_mask must have at most 4 dims, got {list(attn_mask.shape)}")
+        if attn_mask.dtype == torch.bool:
+            m = torch.zeros(attn_mask.shape, dtype=torch.float32, device=dev).masked_fill_(~attn_mask, float("-inf"))
+        elif attn_mask.is_floating_point():
+            m = attn_mask.float()
+        else:
+            raise RuntimeError(f"{what}: attn_mask must be bool or floating point, got {attn_mask.dtype}")
+        if m.dim() > 0 and m.shape[-1] > 1 and m.stride(-1) != 1:
+            m = m.contiguous()
+        m = m.reshape((1,) * (4 - m.dim()) + tuple(m.shape))
+        try:
+            return m.expand(nb, hh, tq, tkv)
+        except RuntimeError:
+            raise RuntimeError(f"{what}: attn_mask {list(attn_mask.shape)} does not broadcast to "
+                               f"[N*B={nb}, heads={hh}, Tq={tq}, Tkv={tkv}]") from None
+
     def _attend(self, query: Tensor, key: Tensor, value: Tensor, attn_mask: Optional[Tensor],
                 is_causal: bool) -> Tensor:
         what = "WideAttention"
@@ -117,8 +147,6 @@ class WideAttention(nn.Module):
         params = (self.q_weight, self.kv_weight, self.out_weight, self.q_bias, self.kv_bias, self.out_bias)
         _hip.require_device(what, query, key, value, *params)
         _hip.require_forward_only(what, query, key, value, *params)
-        if attn_mask is not None:
-            raise NotImplementedError(f"{what}: explicit attention masks are not supported (is_causal is)")
         if self.training and self.dropout > 0:
             raise RuntimeError(f"{what}: attention dropout in training mode is not supported (forward-only "
                                "inference kernels); call .eval()")
@@ -130,6 +158,7 @@ class WideAttention(nn.Module):
         b, tq, tkv = query.shape[1], query.shape[2], key.shape[2]
         if key.shape[1] != b or value.shape[1] != b or value.shape[2] != tkv:
             raise RuntimeError(f"{what}: key/value must be [N, B={b}, Tkv, D] with matching Tkv")
+        mask = self._mask(attn_mask, is_causal, n * b, hh, tq, tkv, query.device) if attn_mask is not None else None
         kvw = self.kv_weight if self.kv_weight.is_contiguous() else self.kv_weight.contiguous()
         qw = self.q_weight if self.q_weight.is_contiguous() else self.q_weight.contiguous()
         ow = self.out_weight if self.out_weight.is_contiguous() else self.out_weight.contiguous()
@@ -144,7 +173,7 @@ class WideAttention(nn.Module):
             if tq > 0:
                 _hip.attention(q=q, k=k_t, v=v_t, o=attn, nb=n * b, heads=hh, sq=tq, skv=tkv, head_dim=dh,
                                q_strides=q_strides, k_strides=k_strides, v_strides=v_strides,
-                               o_strides=(tq * d, d), scale=dh ** -0.5, causal=is_causal)
+                               o_strides=(tq * d, d), scale=dh ** -0.5, causal=is_causal, mask=mask)
             return self._project(attn, ow, d * d, self.out_bias, d, d)
         q = self._project(query, qw, d * d, self.q_bias, d, d)
         if key is value:
@@ -161,7 +190,7 @@ class WideAttention(nn.Module):
         if tq > 0 and tkv > 0:
             _hip.attention(q=q, k=k_t, v=v_t, o=attn, nb=n * b, heads=hh, sq=tq, skv=tkv, head_dim=dh,
                            q_strides=(tq * d, d), k_strides=k_strides, v_strides=v_strides, o_strides=(tq * d, d),
-                           scale=dh ** -0.5, causal=is_causal)
+                           scale=dh ** -0.5, causal=is_causal, mask=mask)
         return self._project(attn, ow, d * d, self.out_bias, d, d)
 
     @classmethod

@@ -81,20 +81,64 @@ def test_attention_matches_nn_mha_per_model(hip):
             assert rel_err(y[k], e) <= TOL_F32
 
 
-def test_attention_mask_and_dropout_raise(hip):
+def test_attention_dropout_and_mask_with_causal_raise(hip):
     import wide_compiler as wc
     wide = wc.WideAttention(2, 32, 2, dropout=0.1).to(DEV)
     x = torch.zeros(2, 1, 4, 32, device=DEV)
     with torch.no_grad():
         with pytest.raises(RuntimeError, match="dropout"):
             wide.train()(x)
-        with pytest.raises(NotImplementedError, match="mask"):
-            wide.eval()(x, attn_mask=torch.zeros(4, 4, device=DEV))
+        with pytest.raises(RuntimeError, match="is_causal"):
+            wide.eval()(x, attn_mask=torch.zeros(4, 4, device=DEV), is_causal=True)
+        with pytest.raises(RuntimeError, match="broadcast"):
+            wide.eval()(x, attn_mask=torch.zeros(3, 4, device=DEV))
+
+
+def _masks(kind, nb, h, tq, tkv, g):
+    """(the mask given to the wide module, the same mask as the oracle's SDPA takes it)"""
+    if kind == "bool2d":                     # [Tq, Tkv] boolean, two query rows fully masked
+        m = torch.rand(tq, tkv, generator=g) > 0.4
+        m[3] = False
+        m[tq - 1] = False
+        return m, m
+    if kind == "add_nb":                     # additive [N*B, 1, Tq, Tkv], some -inf
+        m = torch.randn(nb, 1, tq, tkv, generator=g)
+        m[torch.rand(nb, 1, tq, tkv, generator=g) > 0.8] = float("-inf")
+        return m, m
+    m = torch.randn(nb, h, tq, tkv, generator=g) * 2           # additive per head
+    return m, m
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("kind", ["bool2d", "add_nb", "add_heads"])
+@pytest.mark.parametrize("n,b,tq,tkv,d,h", [(2, 2, 37, 37, 64, 2), (3, 1, 20, 70, 128, 4)])
+def test_attention_mask(hip, dtype, kind, n, b, tq, tkv, d, h):
+    """attn_mask with scaled_dot_product_attention semantics (wide_attention.py:222-228):
+    boolean (True = attend) or additive, broadcast over [N*B, heads, Tq, Tkv]; a fully masked
+    query row gives zeros, as torch's SDPA does."""
+    import wide_compiler as wc
+    g = gen(404)
+    wide = wc.WideAttention.from_modules(_mha(n, d, h, 404, torch.float32)).to(DEV, dtype).eval()
+    q = torch.randn(n, b, tq, d, generator=g).to(dtype)
+    kv = q if tq == tkv else torch.randn(n, b, tkv, d, generator=g).to(dtype)
+    m, m_ref = _masks(kind, n * b, h, tq, tkv, g)
+    with torch.no_grad():
+        if tq == tkv:
+            y = wide(q.to(DEV), attn_mask=m.to(DEV)).cpu()
+        else:
+            y, _ = wide(q.to(DEV), kv.to(DEV), kv.to(DEV), attn_mask=m.to(DEV))
+            y = y.cpu()
+    c = lambda t: None if t is None else t.detach().cpu().double()  # noqa: E731
+    exact = wide_ref.attention(q.double(), kv.double(), kv.double(), c(wide.q_weight), c(wide.kv_weight),
+                               c(wide.out_weight), c(wide.q_bias), c(wide.kv_bias), c(wide.out_bias), h,
+                               attn_mask=m_ref if m_ref.dtype == torch.bool else m_ref.double())
+    assert torch.isfinite(y).all()
+    assert rel_err(y, exact) <= tol(dtype)
 
 
 def test_attention_config_n16(hip):
-    """The attention configuration at full size: N=16 MHA(256, 8 heads), B=8, S=512, bf16;
-    checked model-by-model on three models (no cross-model terms in the wide path)."""
+    """The attention configuration at full size: N=16 MHA(256, 8 heads), B=8, S=512, bf16.
+    Every model against the fp32 oracle, three spread models against fp64."""
     import wide_compiler as wc
     g = gen(403)
     n, b, t, d, h = 16, 8, 512, 256, 8
@@ -102,6 +146,12 @@ def test_attention_config_n16(hip):
     x = torch.randn(n, b, t, d, generator=g).to(torch.bfloat16)
     with torch.no_grad():
         y = wide.eval()(x.to(DEV)).cpu()
+    names = ("q_weight", "kv_weight", "out_weight", "q_bias", "kv_bias", "out_bias")
+    w32 = [None if getattr(wide, a) is None else getattr(wide, a).detach().cpu().float() for a in names]
+    xf = x.float()
+    exact32 = wide_ref.attention(xf, xf, xf, *w32, h)
+    errs = [rel_err(y[k], exact32[k]) for k in range(n)]
+    assert max(errs) <= TOL_BF16, max(errs)
     for k in (0, 7, 15):
         c = lambda w: None if w is None else w.detach().cpu()[k:k + 1].double()  # noqa: E731
         exact = wide_ref.attention(x[k:k + 1].double(), x[k:k + 1].double(), x[k:k + 1].double(),
