@@ -37,6 +37,7 @@
 // and leaves (the outputs are then invalid).  The host launches the grid
 // cooperatively, so all workgroups are co-resident or the launch fails.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "wc_rnn.h"
@@ -509,7 +510,13 @@ int32_t launch_part(const wc_rnn_args* a, hipStream_t st) {
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cap) != hipSuccess)
     return set_error(WC_ERR_ARG, "wc_rnn_recurrence: stream capture status unavailable");
-  if (cap == hipStreamCaptureStatusNone) {
+  // WC_RNN_COOPERATIVE=0 makes the eager launch an ordinary one too, like the one under
+  // capture (rocprofv3 7.2 crashes at exit after a cooperative launch and writes no trace)
+  static const bool cooperative = [] {
+    const char* v = getenv("WC_RNN_COOPERATIVE");
+    return !(v && v[0] == '0' && v[1] == '\0');
+  }();
+  if (cap == hipStreamCaptureStatusNone && cooperative) {
     // co-residency of the whole grid is guaranteed, or the launch fails here
     void* args[] = {&p};
     const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(lstm_part_kernel<H>),
@@ -520,8 +527,8 @@ int32_t launch_part(const wc_rnn_args* a, hipStream_t st) {
                        "failed: %s", nwg, hipGetErrorString(e));
     return WC_OK;
   }
-  // under graph capture: an ordinary kernel node (part_plan checked that the grid fits
-  // the device one workgroup per compute unit)
+  // under graph capture (or WC_RNN_COOPERATIVE=0): an ordinary launch (part_plan checked
+  // that the grid fits the device one workgroup per compute unit)
   lstm_part_kernel<H><<<dim3(nwg), dim3(kPartThreads), lds, st>>>(p);
   return check_launch("wc_rnn_recurrence(partitioned)");
 }

@@ -91,26 +91,19 @@ class WideAttention(nn.Module):
         out = self._attend(query, key, value, attn_mask, is_causal)
         return (out, None) if mha_mode else out
 
-    def _qkv_params(self) -> Tuple[Tensor, Optional[Tensor]]:
-        """[q_weight; kv_weight] as one [N, 3D, D] weight (and [N, 3D] bias), built on every call
-        (no cache: writes through ``.data`` do not bump the version counter a cache could key
-        on, and the reference reads its parameters on every call)."""
-        with torch.no_grad():
-            w = torch.cat([self.q_weight, self.kv_weight], dim=1)
-            bias = None
-            if self.q_bias is not None:
-                bias = torch.cat([self.q_bias, self.kv_bias], dim=1)
-        return w, bias
-
-    def _project(self, x: Tensor, w: Tensor, w_sn: int, bias: Optional[Tensor], b_sn: int, o: int) -> Tensor:
-        """[N, B, T, D] @ W[n]^T + b -> [N, B, T, o] via the grouped GEMM (x read in place)."""
+    def _project(self, x: Tensor, w: Tensor, w_sn: int, bias: Optional[Tensor], b_sn: int, o: int,
+                 out: Optional[Tensor] = None, col0: int = 0) -> Tensor:
+        """[N, B, T, D] @ W[n]^T + b -> [N, B, T, o] via the grouped GEMM (x read in place), or into
+        columns [col0, col0 + o) of ``out`` [N, B, T, C] when given."""
         from .._layout import rows_or_contiguous
         x, r = rows_or_contiguous(x)
-        out = torch.empty((*x.shape[:-1], o), dtype=x.dtype, device=x.device)
         m = r.rows
+        if out is None:
+            out = torch.empty((*x.shape[:-1], o), dtype=x.dtype, device=x.device)
+        width = out.shape[-1]
         _hip.grouped_gemm(n=self.n, m=m, o=o, k=self.d_model, a=x, a_sn=r.stride_n, a_so=r.stride_outer,
-                          a_si=r.stride_inner, a_rows_inner=r.rows_inner, w=w, w_sn=w_sn, c=out,
-                          c_sn=m * o, c_so=0, c_si=o, c_rows_inner=max(m, 1), bias=bias, bias_sn=b_sn)
+                          a_si=r.stride_inner, a_rows_inner=r.rows_inner, w=w, w_sn=w_sn, c=out[..., col0:],
+                          c_sn=m * width, c_so=0, c_si=width, c_rows_inner=max(m, 1), bias=bias, bias_sn=b_sn)
         return out
 
     @staticmethod
@@ -164,9 +157,12 @@ class WideAttention(nn.Module):
         ow = self.out_weight if self.out_weight.is_contiguous() else self.out_weight.contiguous()
         kvb = self.kv_bias
         if query is key and key is value:
-            # self-attention: one GEMM over [q_weight; kv_weight] reads x once -> [N, B, T, 3D] = Q | K | V
-            wqkv, bqkv = self._qkv_params()
-            qkv = self._project(query, wqkv, 3 * d * d, bqkv, 3 * d, 3 * d)
+            # self-attention: the Q and K|V GEMMs write columns [0, D) and [D, 3D) of one
+            # [N, B, T, 3D] = Q | K | V buffer, which the attention kernel reads in place; the
+            # parameters are read as they are on every call (no concatenated copy to go stale)
+            qkv = torch.empty((n, b, tq, 3 * d), dtype=query.dtype, device=query.device)
+            self._project(query, qw, d * d, self.q_bias, d, d, out=qkv, col0=0)
+            self._project(query, kvw, 2 * d * d, kvb, 2 * d, 2 * d, out=qkv, col0=d)
             q, k_t, v_t = qkv, qkv[..., d:], qkv[..., 2 * d:]
             q_strides = k_strides = v_strides = (tq * 3 * d, 3 * d)
             attn = torch.empty((n, b, tq, d), dtype=query.dtype, device=query.device)

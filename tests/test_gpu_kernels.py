@@ -217,25 +217,36 @@ def test_grouped_gemm_large_tiles(hip, out_dtype, m, o, k, rows_inner):
     assert rel_err(c.cpu(), exact) <= TOL_BF16
 
 
-@pytest.mark.parametrize("m,o,k", [(256, 272, 64), (512, 256, 512), (272, 512, 128)])
+@pytest.mark.parametrize("m,o,k,c_ri", [(256, 272, 64, None), (512, 256, 512, None), (272, 512, 128, None),
+                                        (272, 512, 128, 48), (2048, 512, 512, 128)])
 @pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, None])
-def test_grouped_gemm_large_tiles_plain(hip, m, o, k, bias_dtype):
+def test_grouped_gemm_large_tiles_plain(hip, m, o, k, c_ri, bias_dtype):
     """The large-tile kernel without residual or ReLU: one K stage per tile (k = 64), rotated K
-    orders over 2-8 stages, bias in bf16, fp32 or absent."""
+    orders over 2-8 stages, bias in bf16, fp32 or absent, output rows in one run or in groups
+    of c_ri rows two rows apart (two-level output addressing)."""
     from wide_compiler import _hip
-    n = 128
+    n = 128 if m < 1024 else 32
     g = gen(114)
     a = _rand((n, m, k), g, torch.bfloat16)
     w = (_rand((n, o, k), g) * k ** -0.5).to(torch.bfloat16)
     bias = _rand((n, o), g, bias_dtype) if bias_dtype is not None else None
-    c = torch.empty((n, m, o), dtype=torch.bfloat16, device=DEV)
+    ri = c_ri or m
+    outer = (m + ri - 1) // ri
+    pitch = (ri + 2) * o if c_ri else 0
+    c = torch.full((n, outer * (ri + 2) if c_ri else m, o), float("nan"), dtype=torch.bfloat16, device=DEV)
     _hip.grouped_gemm(n=n, m=m, o=o, k=k, a=a.to(DEV), a_sn=m * k, a_so=0, a_si=k, a_rows_inner=m,
-                      w=w.to(DEV), w_sn=o * k, c=c, c_sn=m * o, c_so=0, c_si=o, c_rows_inner=m,
+                      w=w.to(DEV), w_sn=o * k, c=c, c_sn=c.shape[1] * o, c_so=pitch, c_si=o, c_rows_inner=ri,
                       bias=bias.to(DEV) if bias is not None else None, bias_sn=o)
+    c = c.cpu()
+    rows = [(r // ri) * (ri + 2) + r % ri for r in range(m)] if c_ri else list(range(m))
+    got = c[:, rows]
     exact = torch.bmm(a.double(), w.double().transpose(1, 2).contiguous())
     if bias is not None:
         exact = exact + bias.double().unsqueeze(1)
-    assert rel_err(c.cpu(), exact) <= TOL_BF16
+    assert rel_err(got, exact) <= TOL_BF16
+    if c_ri:                                 # the gap rows between groups are never written
+        gaps = [r for r in range(c.shape[1]) if r not in set(rows)]
+        assert torch.isnan(c[:, gaps]).all()
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
