@@ -349,10 +349,12 @@ typedef struct wc_conv_args {
 
 int32_t wc_conv2d(const wc_conv_args* args, void* stream);
 
-/* 1 when wc_conv2d runs these sizes from args->weight directly (packed_weight NULL):
- * the resident-weight kernel (bf16 'same' convolution, stride 1, C_in 32 or 64, C_out a
- * multiple of 64, the input widths it is built for) reads the module's filter bank in
- * its own layout, so no packing pass precedes it; 0 otherwise (pack, then call). */
+/* Part of the replacement of self.grouped_conv(x) (wide_compiler/core/primitives/
+ * wide_conv2d.py:169-194), which reads grouped_conv.weight on every call: 1 when wc_conv2d
+ * runs these sizes from args->weight directly (packed_weight NULL) -- the resident-weight
+ * kernel (bf16 'same' convolution, stride 1, C_in 32 or 64, C_out a multiple of 64, the
+ * input widths it is built for) stages the module's filter bank in its own layout, so no
+ * packing pass precedes it; 0 otherwise (wc_conv_pack_weights, then wc_conv2d). */
 int32_t wc_conv2d_direct_weights(const wc_conv_args* args);
 
 /*

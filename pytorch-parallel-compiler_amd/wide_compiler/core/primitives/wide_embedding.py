@@ -10,7 +10,9 @@ strategy; the second is the per-model lookup a stack of independent sequence mod
 (each model embeds its own tokens), which ``weight[:, ids]`` cannot express.  Both are the
 same bit-exact row-gather kernel (wc_embedding_gather).  An out-of-range id reads nothing:
 its output row is zero and the module's device-side error flag is raised; call
-``index_error()`` (synchronises) to turn that into an IndexError.
+``index_error()`` (synchronises) to turn that into an IndexError.  With ``strict_ids = True``
+every forward does that check itself (one host synchronisation per call, skipped under graph
+capture) and raises as the reference's ``weight[:, ids]`` does.
 """
 
 from __future__ import annotations
@@ -46,6 +48,7 @@ class WideEmbedding(nn.Module):
         self.weight = nn.Parameter(torch.empty(n, num_embeddings, embedding_dim))
         nn.init.normal_(self.weight)
         self._err = None
+        self.strict_ids = False
 
     @property
     def strategy(self) -> EmbeddingStrategy:
@@ -73,6 +76,8 @@ class WideEmbedding(nn.Module):
             out = torch.empty((self.n, *x.shape, self.embedding_dim), dtype=w.dtype, device=w.device)
         if out.numel():
             _hip.embedding_gather(w, ids, out, shared=not per_model, err_flag=self._flag(w.device))
+            if self.strict_ids and not torch.cuda.is_current_stream_capturing():
+                self.index_error()
         return out
 
     def index_error(self) -> None:

@@ -46,6 +46,22 @@ def test_seq_model(hip, dtype, n, b, t, v, d, h):
     assert rel_err(y, exact) <= tol(dtype)
 
 
+def test_embedding_strict_ids_raise_at_the_call(hip):
+    """strict_ids = True: an out-of-range id raises IndexError from the forward itself, as the
+    reference's weight[:, ids] does; in-range ids pass and the flag starts clear."""
+    import wide_compiler as wc
+    emb = wc.WideEmbedding.from_modules([torch.nn.Embedding(10, 8) for _ in range(3)]).to(DEV)
+    emb.strict_ids = True
+    with torch.no_grad():
+        emb(torch.tensor([[1, 9], [0, 3]], device=DEV))
+        with pytest.raises(IndexError):
+            emb(torch.tensor([[1, 10], [0, 3]], device=DEV))
+        with pytest.raises(IndexError):
+            emb(torch.tensor([[-1, 2], [0, 3], [4, 5]], device=DEV), per_model=True)
+        y = emb(torch.tensor([[2, 3]], device=DEV))      # the flag was cleared by the raise
+    assert y.shape == (3, 1, 2, 8)
+
+
 def test_seq_model_out_of_range_id_raises(hip):
     from wide_compiler.workloads import WideSeqModel
     mods = _models(2, 16, 8, 32, torch.float32)
