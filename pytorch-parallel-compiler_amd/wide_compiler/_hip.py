@@ -226,8 +226,15 @@ def require_forward_only(what: str, *tensors: Optional[Tensor]) -> None:
         )
 
 
-def stream_of(t: Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_of(t: Tensor) -> int:
+    """The current HIP stream of t's device as an address (what the ABI's void* stream takes).
+    torch's raw accessor costs a tenth of building a torch.cuda.Stream object per launch."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def ptr(t: Optional[Tensor]) -> Optional[int]:
@@ -314,11 +321,13 @@ def mlp2_supported(dtype: torch.dtype, in_features: int, hidden: int, out_featur
     return bool(lib().wc_mlp2_supported(dtype_code(dtype, "mlp2"), in_features, hidden, out_features))
 
 
-def mlp2(*, n: int, m: int, in_features: int, hidden: int, out_features: int,
-         x: Tensor, x_sn: int, x_so: int, x_si: int, x_rows_inner: int,
-         w1: Tensor, b1: Optional[Tensor], w2: Tensor, b2: Optional[Tensor],
-         y: Tensor, y_sn: int, y_so: int, y_si: int, y_rows_inner: int,
-         relu1: bool, relu2: bool) -> None:
+def mlp2_args(*, n: int, m: int, in_features: int, hidden: int, out_features: int,
+              x: Tensor, x_sn: int, x_so: int, x_si: int, x_rows_inner: int,
+              w1: Tensor, b1: Optional[Tensor], w2: Tensor, b2: Optional[Tensor],
+              y: Tensor, y_sn: int, y_so: int, y_si: int, y_rows_inner: int,
+              relu1: bool, relu2: bool) -> "_Mlp2Args":
+    """The filled argument block of wc_mlp2 (launch with mlp2_launch; a caller may keep it and
+    change only the x / y addresses between launches)."""
     a = _Mlp2Args()
     a.dtype = dtype_code(x.dtype, "mlp2")
     a.act1 = ACT_RELU if relu1 else ACT_NONE
@@ -327,7 +336,16 @@ def mlp2(*, n: int, m: int, in_features: int, hidden: int, out_features: int,
     a.x, a.x_stride_n, a.x_stride_outer, a.x_stride_inner, a.x_rows_inner = x.data_ptr(), x_sn, x_so, x_si, x_rows_inner
     a.w1, a.b1, a.w2, a.b2 = w1.data_ptr(), ptr(b1), w2.data_ptr(), ptr(b2)
     a.y, a.y_stride_n, a.y_stride_outer, a.y_stride_inner, a.y_rows_inner = y.data_ptr(), y_sn, y_so, y_si, y_rows_inner
-    _check(lib().wc_mlp2(ctypes.byref(a), stream_of(x)), "wc_mlp2")
+    return a
+
+
+def mlp2_launch(a: "_Mlp2Args", stream: int) -> None:
+    _check(lib().wc_mlp2(ctypes.byref(a), stream), "wc_mlp2")
+
+
+def mlp2(**kw) -> None:
+    """wc_mlp2 with the arguments of mlp2_args, on x's current stream."""
+    mlp2_launch(mlp2_args(**kw), stream_of(kw["x"]))
 
 
 def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional[Tensor],
@@ -514,7 +532,7 @@ def exported_symbols() -> List[str]:
 # but ends the compiled region there and runs the call as is, so inductor never generates
 # code for the hot path.
 for _name in ("pack_rows", "swap01", "embedding_gather", "layernorm", "bn_eval", "group_norm", "grouped_gemm",
-              "mlp2", "rnn_forward", "rnn_forward_noalloc", "rnn_phase", "conv_pack_weights", "conv2d", "conv3d",
+              "mlp2", "mlp2_args", "mlp2_launch", "rnn_forward", "rnn_forward_noalloc", "rnn_phase", "conv_pack_weights", "conv2d", "conv3d",
               "attention", "rnn_sync_check"):
     globals()[_name] = torch.compiler.disable(globals()[_name])
 del _name

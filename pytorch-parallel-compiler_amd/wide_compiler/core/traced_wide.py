@@ -413,38 +413,67 @@ class TracedWideModel(nn.Module):
             self._skipped[src] = name
 
     # ----------------------------------------------------------------------------------
+    def _make_plan(self) -> list:
+        """The forward's work as a flat list, built once from the traced graph and the fusion
+        bookkeeping (all fixed after construction): ("alias", name, source) or ("run", name, op,
+        args, kwargs, residual, is_output), where args / kwargs entries are (True, value name) or
+        (False, constant).  forward() then does no per-stage bookkeeping."""
+        out_name = self._resolve(self._output_name) if self._output_name else ""
+        plan = []
+        for name in self._execution_order:
+            if name in self._attr_names or name not in self.stage_info or name in self._skipped:
+                continue
+            if name in self._aliases:
+                if self._resolve(name) not in self._skipped:
+                    plan.append(("alias", name, self._aliases[name]))
+                continue
+            op = self.stages[name.replace(".", "_")]
+            args = [(True, a) if isinstance(a, str) else (False, a) for a in self._node_args[name]]
+            if name in self._mlp2:
+                op = self._mlp2[name]
+                args = [(True, self._chain_input[name])]
+            kwargs = [(k, (True, v) if isinstance(v, str) else (False, v))
+                      for k, v in self._node_kwargs.get(name, {}).items()]
+            plan.append(("run", name, op, args, kwargs, self._residual_of.get(name), name == out_name))
+        self.__dict__["_fwd_plan"] = plan
+        return plan
+
     def forward(self, x: Tensor) -> Tensor:
+        # a model that is one fused MLP launch writing the packed output: replay its kept
+        # launch arguments for an input of the form seen before (the whole forward is then
+        # one allocation and one launch on the host)
+        direct = self.__dict__.get("_direct")
+        if direct is not None and direct[0] == (x.shape, x.stride(), x.dtype, x.device):
+            _, op, args, param_ptrs, packed_shape, relu = direct
+            if relu == (op.fused_activation == "relu"):
+                packed = torch.empty(packed_shape, dtype=x.dtype, device=x.device)
+                if op.launch_with(args, param_ptrs, x, packed):
+                    return packed
         b = x.shape[0]
         c = x.shape[1] // self.n
-        spatial = tuple(x.shape[2:])
-        xn = x.view(b, self.n, c, *spatial).movedim(1, 0)  # N-first view, read in place
+        xn = x.view(b, self.n, c, *x.shape[2:]).movedim(1, 0)  # N-first view, read in place
         values: Dict[str, Any] = {self._input_name: xn}
         for attr in self._attr_names:
             buf = f"_attr_{attr.replace('.', '_')}"
             if hasattr(self, buf):
                 values[attr] = getattr(self, buf)
+        plan = self.__dict__.get("_fwd_plan")
+        if plan is None:
+            plan = self._make_plan()
 
-        out_name = self._resolve(self._output_name) if self._output_name else ""
         packed_out: Optional[Tensor] = None
-        for name in self._execution_order:
-            if name in self._attr_names or name not in self.stage_info:
+        for step in plan:
+            if step[0] == "alias":
+                values[step[1]] = values[step[2]]
                 continue
-            if name in self._skipped:
-                continue
-            if name in self._aliases:
-                if self._resolve(name) not in self._skipped:
-                    values[name] = values[self._aliases[name]]
-                continue
-            op = self.stages[name.replace(".", "_")]
-            args = [values[a] if isinstance(a, str) and a in values else a for a in self._node_args[name]]
-            if name in self._mlp2:
-                op = self._mlp2[name]
-                args = [values[self._chain_input[name]]]
-            kwargs = {k: (values[v] if isinstance(v, str) and v in values else v)
-                      for k, v in self._node_kwargs.get(name, {}).items()}
-            if name in self._residual_of:
-                kwargs["residual"] = values[self._residual_of[name]]
-            if name == out_name and len(args) == 1 and isinstance(args[0], Tensor):
+            _, name, op, arg_spec, kw_spec, res, is_out = step
+            # a name that no stage produced (e.g. a module attribute) passes through as text,
+            # as the traced call's own argument
+            args = [values.get(v, v) if is_name else v for is_name, v in arg_spec]
+            kwargs = {k: (values.get(v, v) if is_name else v) for k, (is_name, v) in kw_spec}
+            if res is not None:
+                kwargs["residual"] = values[res]
+            if is_out and len(args) == 1 and isinstance(args[0], Tensor):
                 direct = self._into_packed(op, args[0], kwargs)
                 if direct is not None:
                     packed_out, values[name] = direct
@@ -457,11 +486,23 @@ class TracedWideModel(nn.Module):
                 values[name] = op(*args)
 
         if packed_out is not None:
+            if len(plan) == 1 and isinstance(plan[0][2], WideMLP2):
+                self._keep_direct(x, plan[0][2], xn, values[plan[0][1]], packed_out)
             return packed_out
         out = values[self._output_name]
         if isinstance(out, tuple):
             out = out[0]
         return self._to_packed(out)
+
+    def _keep_direct(self, x: Tensor, op: "WideMLP2", xn: Tensor, view: Tensor, packed: Tensor) -> None:
+        """Record the fused MLP's kept launch arguments for inputs of x's form, if the launch that
+        just ran kept them for exactly this (N-first input view, packed output view) pair."""
+        plan = op.__dict__.get("_plan")
+        relu = op.fused_activation == "relu"
+        if plan is not None and plan[0] == op.plan_key(xn, view, relu, op._params()) and \
+                xn.data_ptr() == x.data_ptr() and view.data_ptr() == packed.data_ptr():
+            self.__dict__["_direct"] = ((x.shape, x.stride(), x.dtype, x.device), op, plan[1], plan[0][-1],
+                                        tuple(packed.shape), relu)
 
     def _into_packed(self, op: nn.Module, x: Tensor, kwargs: Dict[str, Any]) -> Optional[Tuple[Tensor, Tensor]]:
         """Run the output stage writing straight into the packed [B, N*C, *S] layout when it
