@@ -218,12 +218,16 @@ def test_grouped_gemm_large_tiles(hip, out_dtype, m, o, k, rows_inner):
 
 
 @pytest.mark.parametrize("m,o,k,c_ri", [(256, 272, 64, None), (512, 256, 512, None), (272, 512, 128, None),
-                                        (272, 512, 128, 48), (2048, 512, 512, 128)])
+                                        (272, 512, 128, 48), (2048, 512, 512, 128), (512, 256, 64, None),
+                                        (512, 512, 128, 64), (512, 256, 256, None), (544, 320, 512, 32),
+                                        (512, 256, 1024, None)])
 @pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, None])
-def test_grouped_gemm_large_tiles_plain(hip, m, o, k, c_ri, bias_dtype):
-    """The large-tile kernel without residual or ReLU: one K stage per tile (k = 64), rotated K
-    orders over 2-8 stages, bias in bf16, fp32 or absent, output rows in one run or in groups
-    of c_ri rows two rows apart (two-level output addressing)."""
+@pytest.mark.parametrize("relu", [False, True])
+def test_grouped_gemm_large_tiles_plain(hip, m, o, k, c_ri, bias_dtype, relu):
+    """The large-tile kernel without residual: one K stage per tile (k = 64), rotated K orders
+    over 2-16 stages, bias in bf16, fp32 or absent, with or without ReLU, output rows in one run
+    or in groups of c_ri rows two rows apart (two-level output addressing), partial edge tiles
+    (m = 544, o = 320)."""
     from wide_compiler import _hip
     n = 128 if m < 1024 else 32
     g = gen(114)
@@ -236,13 +240,15 @@ def test_grouped_gemm_large_tiles_plain(hip, m, o, k, c_ri, bias_dtype):
     c = torch.full((n, outer * (ri + 2) if c_ri else m, o), float("nan"), dtype=torch.bfloat16, device=DEV)
     _hip.grouped_gemm(n=n, m=m, o=o, k=k, a=a.to(DEV), a_sn=m * k, a_so=0, a_si=k, a_rows_inner=m,
                       w=w.to(DEV), w_sn=o * k, c=c, c_sn=c.shape[1] * o, c_so=pitch, c_si=o, c_rows_inner=ri,
-                      bias=bias.to(DEV) if bias is not None else None, bias_sn=o)
+                      bias=bias.to(DEV) if bias is not None else None, bias_sn=o, relu=relu)
     c = c.cpu()
     rows = [(r // ri) * (ri + 2) + r % ri for r in range(m)] if c_ri else list(range(m))
     got = c[:, rows]
     exact = torch.bmm(a.double(), w.double().transpose(1, 2).contiguous())
     if bias is not None:
         exact = exact + bias.double().unsqueeze(1)
+    if relu:
+        exact = F.relu(exact)
     assert rel_err(got, exact) <= TOL_BF16
     if c_ri:                                 # the gap rows between groups are never written
         gaps = [r for r in range(c.shape[1]) if r not in set(rows)]
