@@ -173,11 +173,11 @@ def cfg_seq(dev, steps, warmup) -> Dict:
                     byts=rows * (8 + 2 * d * 2)),
             _kernel("layernorm_kernel (256-wide rows, bf16, fp32 statistics)", "hbm", t_ln,
                     byts=2 * rows * d * 2 + 2 * n * d * 2),
-            _kernel("LSTM input projection (part_prep_kernel + gemm_xlp_kernel, 256 -> 2048, bf16 out)",
+            _kernel("LSTM input projection (part_prep_kernel + gemm_xl8_kernel, 256 -> 2048, bf16 out)",
                     "mfma", t_proj, flops=2.0 * rows * g * d, peak=PEAK["bf16_mfma"]),
             _kernel("lstm_part_kernel (LSTM recurrence, 128 steps, W_hh on-chip, 4 CUs per model)", "mfma",
                     t_rec, flops=2.0 * rows * g * hdim, peak=PEAK["bf16_mfma"]),
-            _kernel("gemm_xlp_kernel (vocab projection 512 -> 8192 + bias, bf16)", "mfma", t_fc,
+            _kernel("gemm_xl8_kernel (vocab projection 512 -> 8192 + bias, bf16)", "mfma", t_fc,
                     flops=2.0 * rows * v * hdim, peak=PEAK["bf16_mfma"]),
         ]
 
@@ -375,11 +375,11 @@ def cfg_attention(dev, steps, warmup) -> Dict:
         t_qkv = _event_time(project_qkv, steps, warmup)
         t_out = _event_time(lambda: wide._project(o, wide.out_weight, d * d, wide.out_bias, d, d), steps, warmup)
         rows = n * b * s
-        return [_kernel("gemm_xlp_kernel x2 (Q and K|V projections 256 -> 256 + 512 into one Q|K|V buffer, bf16)",
+        return [_kernel("gemm_xl8_kernel x2 (Q and K|V projections 256 -> 256 + 512 into one Q|K|V buffer, bf16)",
                         "mfma", t_qkv, flops=2.0 * rows * 3 * d * d, peak=PEAK["bf16_mfma"]),
                 _kernel("attn_res_kernel (fused softmax(QK^T)V, bf16, head_dim 32, K/V resident in LDS)", "mfma",
                         t_attn, flops=4.0 * n * b * hh * s * s * dh, peak=PEAK["bf16_mfma"]),
-                _kernel("gemm_xlp_kernel (output projection 256 -> 256, bf16)", "mfma", t_out,
+                _kernel("gemm_xl8_kernel (output projection 256 -> 256, bf16)", "mfma", t_out,
                         flops=2.0 * rows * d * d, peak=PEAK["bf16_mfma"])]
 
     n_cpu = 1

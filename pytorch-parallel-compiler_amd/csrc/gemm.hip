@@ -809,6 +809,275 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
     read_frags((ti + 1) * KS, fp0, w0, a0);
   }
 }
+// ---------------------------------------------------------------------------
+// Persistent XL bf16 kernel, two waves per SIMD (bf16 output, no residual).
+// The tile walk, the K-stage ring, the LDS layout of a stage and its LDS-DMA
+// staging are those of gemm_xlp_kernel; the 256 x 256 tile is split over 8
+// waves (2 x 4) of 128 x 64 each, as 8 x 4 MFMA 16x16x32 blocks (128 AGPR
+// accumulators per lane).  Two waves per SIMD keep v_mfma_f32_16x16x32_bf16
+// issuing every ~19 cycles where one wave manages ~28.  Wave w moves 4 of a
+// stage's W row blocks and 4 of its A row blocks (8 rows x 128 bytes each),
+// reads 8 W and 4 A fragments per 32-wide half stage, and stores its output
+// through a 16-row x 64-column LDS half strip.
+// ---------------------------------------------------------------------------
+constexpr int kX8Threads = 512;
+constexpr int kX8StripPitch = 64 * 2 + 16;                // bf16 half-strip row: 64 columns (bytes)
+constexpr int kX8StripBytes = 16 * kX8StripPitch;         // per wave
+
+template <typename TB, bool RELU>
+__global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, int tiles_total) {
+  __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 8 * kX8StripBytes + 2 * kXlBiasSlot];
+  lds_char* const smem = (lds_char*)smem_raw;        // keeps every LDS address 32-bit
+  // VMEM instructions a wave issues per tile epilogue: 16 stores and its bias load
+  constexpr int E = 17;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int ow = (wave & 1) * 128, mw = (wave >> 1) * 64;
+  const int tiles_per_model = p.tiles_m * p.tiles_o;
+  const int KS = p.k / kXlBK;
+
+  // ---- this workgroup's tiles: XCD x = blockIdx % 8 owns a contiguous range ----
+  const int G = gridDim.x;
+  int t_first, t_step, my_tiles;
+  if ((G & 7) == 0) {
+    const int x = blockIdx.x & 7, l = blockIdx.x >> 3, nwx = G >> 3;
+    const int lo = static_cast<int>((static_cast<int64_t>(tiles_total) * x) >> 3);
+    const int hi = static_cast<int>((static_cast<int64_t>(tiles_total) * (x + 1)) >> 3);
+    t_first = lo + l;
+    t_step = nwx;
+    my_tiles = t_first < hi ? (hi - t_first + nwx - 1) / nwx : 0;
+  } else {
+    t_first = blockIdx.x;
+    t_step = G;
+    my_tiles = t_first < tiles_total ? (tiles_total - t_first + G - 1) / G : 0;
+  }
+  const int S = my_tiles * KS;
+  if (S == 0) return;
+
+  // tile ti of this workgroup; its K stages run in a rotated order starting at stage
+  // (m-tile index mod KS), as in gemm_xlp_kernel
+  struct Tile { int mdl, m0, o0, rot; };
+  auto tile_of = [&](int ti) {
+    Tile t;
+    const int g = t_first + ti * t_step;
+    t.mdl = static_cast<int>(fdiv(static_cast<uint32_t>(g), p.fd_tpm));
+    const int rem = g - t.mdl * tiles_per_model;
+    const int to = static_cast<int>(fdiv(static_cast<uint32_t>(rem), p.fd_tm));
+    const int mt = rem - to * p.tiles_m;
+    t.m0 = mt * kXlB;
+    t.o0 = to * kXlB;
+    t.rot = mt - static_cast<int>(fdiv(static_cast<uint32_t>(mt), p.fd_ks)) * KS;
+    return t;
+  };
+
+  // ---- DMA of stage `stage` into slot stage & 1 (stages past the last reload it).
+  // Wave w moves the blocks gemm_xlp_kernel's wave w / 2 moves as its blocks
+  // 4 (w & 1) .. + 3 (W rows) and 8 + 4 (w & 1) .. + 3 (A rows): W and A rows
+  // 32 w + 8 q' for q' < 4.  Lane l writes row l >> 3 of a block, position l & 7,
+  // which receives global chunk (l & 7) ^ (l >> 3). ----
+  const uint32_t dchunk = ((lane & 7) ^ (lane >> 3)) * 8;
+  const uint32_t wlane = ((lane >> 3) * static_cast<uint32_t>(p.k) + dchunk) * 2u;
+  const uint32_t alane = ((lane >> 3) * static_cast<uint32_t>(p.a_si) + dchunk) * 2u;
+  struct Dma { const char* wmod; const char* amod; int slot, o0, m0; };
+  auto dma_of = [&](int stage) {
+    const int sidx = stage < S ? stage : S - 1;
+    const int ti = static_cast<int>(fdiv(static_cast<uint32_t>(sidx), p.fd_ks));
+    const Tile t = tile_of(ti);
+    int ks = sidx - ti * KS + t.rot;
+    if (ks >= KS) ks -= KS;
+    Dma d;
+    d.wmod = static_cast<const char*>(p.w) + static_cast<int64_t>(t.mdl) * p.w_sn * 2 + ks * 128;
+    d.amod = static_cast<const char*>(p.a) + static_cast<int64_t>(t.mdl) * p.a_sn * 2 + ks * 128;
+    d.slot = (stage & 1) * kXlStageBytes;
+    d.o0 = t.o0;
+    d.m0 = t.m0;
+    return d;
+  };
+  // block q (0..7) of this wave: q < 4 W rows, q >= 4 A rows
+  auto dma_block = [&](const Dma& d, int q) {
+    const int qq = q < 4 ? 4 * (wave & 1) + q : 8 + 4 * (wave & 1) + (q - 4);
+    xl_dma_block(p, d.wmod, d.amod, smem + d.slot, q < 4 ? d.o0 : d.m0, wave >> 1, qq, wlane, alane);
+  };
+  auto issue = [&](int stage) {
+    const Dma d = dma_of(stage);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) dma_block(d, q);
+  };
+
+  // fragment byte offsets: row = base + 16 * i + (lane & 15), chunk 4 * half + (lane >> 4)
+  const int fr = lane & 15;
+  const int fp0 = (((lane >> 4)) ^ (fr & 7)) << 4;
+  const int fp1 = ((4 + (lane >> 4)) ^ (fr & 7)) << 4;
+  const int wfo = (ow + fr) * 128, afo = kXlHalf + (mw + fr) * 128;
+  // fragment g of a K half: g < 8 is W rows ow + 16 g, g >= 8 A rows mw + 16 (g - 8)
+  auto read_frag = [&](int stage, int fpos, int g, bf16x8 (&wf)[8], bf16x8 (&af)[4]) {
+    const lds_char* st = smem + (stage & 1) * kXlStageBytes + fpos;
+    if (g < 8)
+      wf[g] = *(const lds_bf16x8*)(st + wfo + g * 2048);
+    else
+      af[g - 8] = *(const lds_bf16x8*)(st + afo + (g - 8) * 2048);
+  };
+  auto read_frags = [&](int stage, int fpos, bf16x8 (&wf)[8], bf16x8 (&af)[4]) {
+#pragma unroll
+    for (int g = 0; g < 12; ++g) read_frag(stage, fpos, g, wf, af);
+  };
+
+  // ---- bias of a tile: wave w moves the tile's columns [32 w, 32 w + 32) into LDS slot
+  // (tile index & 1) with one LDS-DMA load (columns past o read a valid column; the
+  // stores of those columns are dropped) ----
+  lds_char* const bias_lds = smem + 2 * kXlStageBytes + 8 * kX8StripBytes;
+  auto lane_now = []() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+  };
+  const char* const bias_base = p.bias ? static_cast<const char*>(p.bias) : static_cast<const char*>(p.c);
+  auto load_bias = [&](const Tile& t, int slot) {
+    constexpr int EPC = 16 / static_cast<int>(sizeof(TB));       // bias elements per 16-byte chunk
+    constexpr int LANES = 32 / EPC;                               // lanes that move the wave's 32 columns
+    const int ln = lane_now();
+    const int col = t.o0 + 32 * wave + EPC * (ln < LANES ? ln : 0);
+    const int cl = col < p.o ? col : p.o - EPC;
+    const int64_t eoff = p.bias ? static_cast<int64_t>(t.mdl) * p.b_sn + cl : 0;
+    if (ln < LANES)
+      __builtin_amdgcn_global_load_lds(bias_base + eoff * static_cast<int64_t>(sizeof(TB)),
+                                       (lds_ptr_t)(bias_lds + slot * kXlBiasSlot + 32 * wave * sizeof(TB)), 16, 0, 0);
+  };
+
+  // acc[i][j]: W rows ow + 16 i, A rows mw + 16 j; lane (g = lane >> 4, fr) holds C
+  // columns ow + 16 i + 4 g + e of row mw + 16 j + fr
+  f32x4 acc[8][4];
+
+  // ---- epilogue of tile t: acc (+ bias, ReLU) -> C, one 16-row x 64-column half strip at
+  // a time through LDS, then 16-byte row chunks: lane -> row 8 q + (lane >> 3), 8 columns
+  // from 8 (lane & 7) ----
+  lds_char* strip = smem + 2 * kXlStageBytes + wave * kX8StripBytes;
+  auto epilogue = [&](const Tile& t, int ti_parity) {
+    const __amdgpu_buffer_rsrc_t crs =
+        xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn, p.c_bytes);
+    const int ln = lane_now();
+    const int fr = ln & 15, g4 = ln >> 4;
+    if (KS == 1) {
+      vm_lgkm_wait<0>();
+      bare_barrier();
+    }
+    const int rr = ln >> 3, cc = ln & 7;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      // bias of the lane's columns ow + 64 hh + 16 i' + 4 g4 + e
+      float bv[4][4];
+      const lds_char* bl = bias_lds + (ti_parity & 1) * kXlBiasSlot + (ow + 64 * hh + 4 * g4) * sizeof(TB);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (sizeof(TB) == 4) {
+          const f32x4 b4 = *(const __attribute__((address_space(3))) f32x4*)(bl + 16 * i * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? b4[e] : 0.f;
+        } else {
+          const bf16x4 b4 = *(const lds_bf16x4*)(bl + 16 * i * 2);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? to_f32(b4[e]) : 0.f;
+        }
+      }
+      const int col = t.o0 + ow + 64 * hh + cc * 8;
+      const bool col_ok = col < p.o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bf16x4 o4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = acc[4 * hh + i][j][e] + bv[i][e];
+            if (RELU) v = relu_f(v);
+            o4[e] = from_f32<bf16>(v);
+          }
+          *(lds_bf16x4*)(strip + fr * kX8StripPitch + (16 * i + 4 * g4) * 2) = o4;
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);          // lgkmcnt(0): half strip written
+        __builtin_amdgcn_wave_barrier();
+        // the strip's 16 rows share one row decomposition (rows_inner % 16 == 0)
+        const int row0 = t.m0 + mw + 16 * j;
+        const uint32_t outer = fdiv(static_cast<uint32_t>(row0), p.c_ri);
+        const uint32_t inner = row0 - outer * p.c_ri.d;
+        const bool strip_ok = row0 < p.m && col_ok;
+        const uint32_t cbase =
+            (outer * static_cast<uint32_t>(p.c_so) + inner * static_cast<uint32_t>(p.c_si) + col) * 2u;
+        i32x4 raw[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) raw[q] = *(const lds_i32x4*)(strip + (8 * q + rr) * kX8StripPitch + cc * 16);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int lr = 8 * q + rr;
+          // non-temporal (nt): the output streams past the L2s, which keep the operand tiles
+          __builtin_amdgcn_raw_buffer_store_b128(
+              raw[q], crs, strip_ok ? cbase + static_cast<uint32_t>(lr * p.c_si) * 2u : kXlOob, 0, 2);
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);          // strip reads done before it is rewritten
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+  };
+
+  // ---- prologue: stage 0 landed and its first half read, stage 1 in flight ----
+  issue(0);
+  load_bias(tile_of(0), 0);
+  vm_lgkm_wait<0>();
+  bare_barrier();
+  issue(1);
+  // One fragment set (8 W + 4 A), read at the start of each half: the other wave on the
+  // SIMD issues its MFMAs while this one waits for the reads (two sets would not fit
+  // beside the 128 accumulators in the 256 registers a wave has at two waves per SIMD).
+  bf16x8 wf[8], af[4];
+  auto half = [&](int stage, int fpos, auto first_tag) {
+    constexpr bool kFirst = decltype(first_tag)::value;
+#pragma unroll
+    for (int g = 0; g < 12; ++g) read_frag(stage, fpos, g, wf, af);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
+                                                            0, 0, 0);
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+  // stage s: first half; wait for stage s + 1 (behind it only the epilogue of a tile that
+  // ended at s - 1) and for every wave's reads of stage s's first half... and second half:
+  // the second half's fragments are read before the barrier, so slot s & 1 is free after it
+  auto step = [&](bool after_epi, int s, auto first_tag) {
+    half(s, fp0, first_tag);
+#pragma unroll
+    for (int g = 0; g < 12; ++g) read_frag(s, fp1, g, wf, af);
+    if (after_epi) vm_lgkm_wait<E>();
+    else vm_lgkm_wait<0>();
+    bare_barrier();
+    {
+      const Dma d = dma_of(s + 2);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) dma_block(d, q);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);     // one DMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);     // four MFMAs
+    }
+  };
+  for (int ti = 0; ti < my_tiles; ++ti) {
+    step(ti > 0, ti * KS, yes{});
+    for (int ks = 1; ks < KS; ++ks) step(false, ti * KS + ks, no{});
+    epilogue(tile_of(ti), ti);
+    load_bias(tile_of(ti + 1 < my_tiles ? ti + 1 : ti), (ti + 1) & 1);
+  }
+  vm_lgkm_wait<0>();                               // no LDS-DMA load outlives the workgroup
+}
+
 // Elements from one model's base to the end of the last of its m rows (of `width`
 // columns) addressed as (m / ri) * so + (m % ri) * si.
 inline int64_t xl_span(const GemmParams& p, int64_t so, int64_t si, int64_t ri, int64_t width) {
@@ -840,8 +1109,12 @@ int32_t launch_xl(GemmParams p, hipStream_t st) {
   p.fd_tpm = make_fastdiv(static_cast<uint32_t>(p.tiles_m * p.tiles_o));
   p.fd_tm = make_fastdiv(static_cast<uint32_t>(p.tiles_m));
   const bool relu = p.act == WC_ACT_RELU;
-  auto kern = p.r ? (relu ? gemm_xlp_kernel<TB, true, true> : gemm_xlp_kernel<TB, true, false>)
-                  : (relu ? gemm_xlp_kernel<TB, false, true> : gemm_xlp_kernel<TB, false, false>);
+  if (!p.r) {
+    auto kern8 = relu ? gemm_xl8_kernel<TB, true> : gemm_xl8_kernel<TB, false>;
+    kern8<<<dim3(grid), dim3(kX8Threads), 0, st>>>(p, static_cast<int>(tiles));
+    return check_launch("wc_grouped_gemm");
+  }
+  auto kern = relu ? gemm_xlp_kernel<TB, true, true> : gemm_xlp_kernel<TB, true, false>;
   kern<<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
   return check_launch("wc_grouped_gemm");
 }
