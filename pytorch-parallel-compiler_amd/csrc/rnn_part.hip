@@ -98,12 +98,13 @@ struct KOrder {
   }
 };
 
-// acc[j] += the k-steps B..E-1 of (W_hh rows of tile j) x h^T: A fragments from LDS (wlw,
-// this lane's fragment base), AGPRs (wa) or VGPRs (wv); B fragments from this lane's h
-// row in LDS (hrow, k-step s at hrow + 32 s).
-template <int SL, int NA, int XL, int B, int E, int NT, int RA, int RV>
+// acc[j] += the k-steps B..E-1 of (W_hh rows of tile j) x h^T for the tiles J0 <= j < J1:
+// A fragments from LDS (wlw, this lane's fragment base), AGPRs (wa) or VGPRs (wv); B fragments
+// from this lane's h row in LDS (hrow, k-step s at hrow + 32 s).
+template <int SL, int NA, int XL, int B, int E, int J0, int J1, int NT, int RA, int RV>
 __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[NT], const bf16x8 (&wa)[RA][NT],
                                            const bf16x8 (&wv)[RV][NT], const bf16x8* wlw, const bf16* hrow) {
+  static_assert(0 <= J0 && J0 < J1 && J1 <= NT, "tile range");
   constexpr KOrder<SL, NA, XL, B, E> ord;
   constexpr int N = E - B;
   bf16x8 lf[NT];                                     // LDS-fed fragments of the current / next k-step
@@ -115,7 +116,7 @@ __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[NT], const bf16x8 (&wa)[
   bf16x8 hb = *reinterpret_cast<const bf16x8*>(hrow + ord.s[0] * 32);
   if (ord.lds[0]) {
 #pragma unroll
-    for (int j = 0; j < NT; ++j) load_tile(ord.s[0], j);
+    for (int j = J0; j < J1; ++j) load_tile(ord.s[0], j);
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) {
@@ -126,10 +127,10 @@ __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[NT], const bf16x8 (&wa)[
     // a register-fed k-step: read all of the next LDS-fed k-step's fragments under its MFMAs
     if (!ord.lds[i] && nxt_lds) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) load_tile(ord.s[i + 1], j);
+      for (int j = J0; j < J1; ++j) load_tile(ord.s[i + 1], j);
     }
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
+    for (int j = J0; j < J1; ++j) {
       bf16x8 a;
       if (in_lds(s, j)) a = lf[j];
       else if (s < SL + NA) a = wa[s < SL + NA ? s - SL : 0][j];
@@ -379,11 +380,14 @@ void lstm_part_kernel(PartParams p) {
   f32x4 acc[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  mfma_steps<SL, NA, XL, 0, KPP>(acc, wa, wv, wlw, hrow);
+  mfma_steps<SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);
   for (int t = 0; t < p.steps && !aborted; ++t) {
     // gates = h_{t-1} W_hh^T (MFMA; own columns already in acc) + gates_x (x W_ih^T + b_ih
     // + b_hh, added in the cell update)
-    mfma_steps<SL, NA, XL, KPP, KS>(acc, wa, wv, wlw, hrow);
+    // in two tile groups, so that the cell update of the first group can run between the
+    // second group's MFMAs (the h fragments are read once per group)
+    mfma_steps<SL, NA, XL, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
+    mfma_steps<SL, NA, XL, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
     // cell update of the lane's 8 units (i, f, g, o in acc[j][0..3])
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -416,7 +420,7 @@ void lstm_part_kernel(PartParams p) {
     lds_barrier();                                     // this part's h_t is in LDS
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    mfma_steps<SL, NA, XL, 0, KPP>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
+    mfma_steps<SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
     get(t, tag);
     put_out();
     load_gx(t + 1);                                    // lands during the next step's MFMAs
