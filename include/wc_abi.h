@@ -246,8 +246,8 @@ int32_t wc_rnn_forward_noalloc(const wc_rnn_args* args, void* stream);
  * Row m of A (and of C / R) lives at  i*stride_n + (m / rows_inner)*stride_outer
  * + (m % rows_inner)*stride_inner; the K (resp. O) dimension is contiguous.
  * W is [n, o, k] with row stride k and model stride w_stride_n.
- * dtype in {WC_F32, WC_BF16} (fp32 accumulation on MFMA); out_dtype is WC_F32
- * or dtype; bias_dtype is WC_F32 or dtype; bias and residual may be NULL.
+ * dtype in {WC_F32, WC_BF16, WC_F16} (fp32 accumulation on MFMA); out_dtype is
+ * WC_F32 or dtype; bias_dtype is WC_F32 or dtype; bias and residual may be NULL.
  */
 typedef struct wc_gemm_args {
   int32_t dtype, out_dtype, bias_dtype, act;

@@ -33,6 +33,18 @@ constexpr int kBK = 32;
 template <typename TA> struct Frag;
 template <> struct Frag<bf16> { typedef bf16x8 type; };
 template <> struct Frag<float> { typedef f32x4 type; };  // two per K-step
+template <> struct Frag<f16> { typedef bf16x8 type; };    // raw 16-bit lanes, as bf16
+
+// v_mfma_f32_16x16x32 on 16-bit operands carried as raw 16-byte fragments: the bf16 or
+// the fp16 instruction by the element type T
+template <typename T>
+__device__ __forceinline__ f32x4 mma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (std::is_same<T, f16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ float relu_f(float v) { return v > 0.f ? v : 0.f; }
 
@@ -168,7 +180,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmParams p) {
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = mma16<TA>(af[i], bfr[j], acc[i][j]);
     } else {
       f32x4 af[FM][2], bfr[FN][2];
 #pragma unroll
@@ -254,7 +266,7 @@ struct BigCfg {
   static_assert(CH % NT == 0, "chunks must divide evenly");
 };
 
-template <typename TC, typename TB, int WM, int WN, int FM, int FN>
+template <typename TA, typename TC, typename TB, int WM, int WN, int FM, int FN>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmParams p) {
   using C = BigCfg<WM, WN, FM, FN>;
   constexpr int NT = C::NT, BM = C::BM, BN = C::BN, CPT = C::CPT;
@@ -339,7 +351,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmParams p) {
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = mma16<TA>(af[i], bfr[j], acc[i][j]);
     }
     if (kt + 1 < ktiles) stash(stage ^ 1);
     __syncthreads();
@@ -391,10 +403,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmParams p) {
           if constexpr (sizeof(TC) == 4) {
             *reinterpret_cast<f32x4*>(cbase + off) = f32x4{v[0], v[1], v[2], v[3]};
           } else {
-            bf16x4 o4;
+            typedef TC tc4 __attribute__((ext_vector_type(4)));
+            tc4 o4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o4[e] = from_f32<bf16>(v[e]);
-            *reinterpret_cast<bf16x4*>(cbase + off) = o4;
+            for (int e = 0; e < 4; ++e) o4[e] = from_f32<TC>(v[e]);
+            *reinterpret_cast<tc4*>(cbase + off) = o4;
           }
         } else {
 #pragma unroll
@@ -508,7 +521,7 @@ __device__ __forceinline__ void xl_dma_block(const GemmParams& p, const char* wm
   }
 }
 
-template <typename TB, bool RES, bool RELU>
+template <typename TA, typename TB, bool RES, bool RELU>
 __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, int tiles_total) {
   __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 4 * kXlStripBytes + 2 * kXlBiasSlot];
   lds_char* const smem = (lds_char*)smem_raw;        // keeps every LDS address 32-bit
@@ -641,9 +654,9 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
   lds_char* strip = smem + 2 * kXlStageBytes + wave * kXlStripBytes;
   auto epilogue = [&](const Tile& t, int ti_parity) {
     const __amdgpu_buffer_rsrc_t crs =
-        xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn, p.c_bytes);
+        xl_rsrc(static_cast<TA*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn, p.c_bytes);
     const __amdgpu_buffer_rsrc_t rrs =
-        xl_rsrc(RES ? static_cast<const bf16*>(p.r) + static_cast<int64_t>(t.mdl) * p.r_sn : p.c, p.r_bytes);
+        xl_rsrc(RES ? static_cast<const TA*>(p.r) + static_cast<int64_t>(t.mdl) * p.r_sn : p.c, p.r_bytes);
     constexpr bool relu = RELU;
     const int lane = lane_now();
     const int fr = lane & 15;
@@ -663,7 +676,9 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
 #pragma unroll
           for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? b4[e] : 0.f;
         } else {
-          const bf16x4 b4 = *(const lds_bf16x4*)(bl + 16 * i * 2);
+          typedef TB tb4 __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) tb4 lds_tb4;
+          const auto b4 = *(const lds_tb4*)(bl + 16 * i * 2);
 #pragma unroll
           for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? to_f32(b4[e]) : 0.f;
         }
@@ -681,7 +696,7 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
         for (int e = 0; e < 4; ++e) {
           float v = acc[i][j][e] + bv[i][e];
           if (!RES && relu) v = relu_f(v);
-          o4[e] = from_f32<bf16>(v);
+          o4[e] = __builtin_bit_cast(bf16, from_f32<TA>(v));   // the strip holds raw 16-bit values
         }
         *(lds_bf16x4*)(strip + fr * kXlStripPitch + (16 * i + 4 * (lane >> 4)) * 2) = o4;
       }
@@ -708,14 +723,14 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
         const int lr = 4 * q + rsub;
         i32x4 outv = raw[q];
         if constexpr (RES) {
-          const bf16* a = reinterpret_cast<const bf16*>(&raw[q]);
-          const bf16* b = reinterpret_cast<const bf16*>(&rv[q]);
-          bf16* o = reinterpret_cast<bf16*>(&outv);
+          const TA* a = reinterpret_cast<const TA*>(&raw[q]);
+          const TA* b = reinterpret_cast<const TA*>(&rv[q]);
+          TA* o = reinterpret_cast<TA*>(&outv);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             float v = to_f32(a[e]) + to_f32(b[e]);
             if (relu) v = relu_f(v);
-            o[e] = from_f32<bf16>(v);
+            o[e] = from_f32<TA>(v);
           }
         }
         // non-temporal (nt): the output streams past the L2s, which keep the operand tiles
@@ -742,8 +757,7 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
-                                                            0, 0, 0);
+        acc[i][j] = mma16<TA>(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
   };
   auto interleave = [&]() {
 #pragma unroll
@@ -824,7 +838,7 @@ constexpr int kX8Threads = 512;
 constexpr int kX8StripPitch = 64 * 2 + 16;                // bf16 half-strip row: 64 columns (bytes)
 constexpr int kX8StripBytes = 16 * kX8StripPitch;         // per wave
 
-template <typename TB, bool RELU>
+template <typename TA, typename TB, bool RELU>
 __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, int tiles_total) {
   __shared__ __attribute__((aligned(1024))) char smem_raw[2 * kXlStageBytes + 8 * kX8StripBytes + 2 * kXlBiasSlot];
   lds_char* const smem = (lds_char*)smem_raw;        // keeps every LDS address 32-bit
@@ -955,7 +969,7 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
   lds_char* strip = smem + 2 * kXlStageBytes + wave * kX8StripBytes;
   auto epilogue = [&](const Tile& t, int ti_parity) {
     const __amdgpu_buffer_rsrc_t crs =
-        xl_rsrc(static_cast<bf16*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn, p.c_bytes);
+        xl_rsrc(static_cast<TA*>(p.c) + static_cast<int64_t>(t.mdl) * p.c_sn, p.c_bytes);
     const int ln = lane_now();
     const int fr = ln & 15, g4 = ln >> 4;
     if (KS == 1) {
@@ -975,7 +989,9 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
 #pragma unroll
           for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? b4[e] : 0.f;
         } else {
-          const bf16x4 b4 = *(const lds_bf16x4*)(bl + 16 * i * 2);
+          typedef TB tb4 __attribute__((ext_vector_type(4)));
+          typedef __attribute__((address_space(3))) tb4 lds_tb4;
+          const auto b4 = *(const lds_tb4*)(bl + 16 * i * 2);
 #pragma unroll
           for (int e = 0; e < 4; ++e) bv[i][e] = p.bias ? to_f32(b4[e]) : 0.f;
         }
@@ -991,7 +1007,7 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
           for (int e = 0; e < 4; ++e) {
             float v = acc[4 * hh + i][j][e] + bv[i][e];
             if (RELU) v = relu_f(v);
-            o4[e] = from_f32<bf16>(v);
+            o4[e] = __builtin_bit_cast(bf16, from_f32<TA>(v));   // the strip holds raw 16-bit values
           }
           *(lds_bf16x4*)(strip + fr * kX8StripPitch + (16 * i + 4 * g4) * 2) = o4;
         }
@@ -1038,8 +1054,7 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j],
-                                                            0, 0, 0);
+        acc[i][j] = mma16<TA>(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
   };
   using yes = std::true_type;
   using no = std::false_type;
@@ -1062,7 +1077,7 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = mma16<TA>(wf[i], af[j], acc[i][j]);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);     // one DMA
@@ -1087,7 +1102,7 @@ inline int64_t xl_span(const GemmParams& p, int64_t so, int64_t si, int64_t ri, 
 }
 
 
-template <typename TB>
+template <typename TA, typename TB>
 int32_t launch_xl(GemmParams p, hipStream_t st) {
   p.tiles_m = static_cast<int>(cdiv(p.m, kXlB));
   p.tiles_o = static_cast<int>(cdiv(p.o, kXlB));
@@ -1110,16 +1125,16 @@ int32_t launch_xl(GemmParams p, hipStream_t st) {
   p.fd_tm = make_fastdiv(static_cast<uint32_t>(p.tiles_m));
   const bool relu = p.act == WC_ACT_RELU;
   if (!p.r) {
-    auto kern8 = relu ? gemm_xl8_kernel<TB, true> : gemm_xl8_kernel<TB, false>;
+    auto kern8 = relu ? gemm_xl8_kernel<TA, TB, true> : gemm_xl8_kernel<TA, TB, false>;
     kern8<<<dim3(grid), dim3(kX8Threads), 0, st>>>(p, static_cast<int>(tiles));
     return check_launch("wc_grouped_gemm");
   }
-  auto kern = relu ? gemm_xlp_kernel<TB, true, true> : gemm_xlp_kernel<TB, true, false>;
+  auto kern = relu ? gemm_xlp_kernel<TA, TB, true, true> : gemm_xlp_kernel<TA, TB, true, false>;
   kern<<<dim3(grid), dim3(kXlThreads), 0, st>>>(p, static_cast<int>(tiles));
   return check_launch("wc_grouped_gemm");
 }
 
-template <typename TC, typename TB, int WM, int WN, int FM, int FN>
+template <typename TA, typename TC, typename TB, int WM, int WN, int FM, int FN>
 int32_t launch_big(GemmParams p, hipStream_t st) {
   using C = BigCfg<WM, WN, FM, FN>;
   p.tiles_m = static_cast<int>(cdiv(p.m, C::BM));
@@ -1127,7 +1142,7 @@ int32_t launch_big(GemmParams p, hipStream_t st) {
   const int64_t nblk = static_cast<int64_t>(p.n) * p.tiles_m * p.tiles_o;
   if (nblk >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_grouped_gemm: too many tiles");
   p.remap = (nblk % 8 == 0) ? 1 : 0;
-  auto kern = gemm_big_kernel<TC, TB, WM, WN, FM, FN>;
+  auto kern = gemm_big_kernel<TA, TC, TB, WM, WN, FM, FN>;
   if (C::LDS > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(C::LDS));
@@ -1183,8 +1198,8 @@ int32_t launch_gemm_t(const GemmParams& p, bool vec, hipStream_t st) {
   if constexpr (sizeof(TA) == 2) {
     const int64_t tiles256 = static_cast<int64_t>(p.n) * cdiv(p.m, 256) * cdiv(p.o, 256);
     if constexpr (sizeof(TC) == 2)
-      if (vec && tiles256 >= 256 && xl_shape_ok<TC>(p)) return launch_xl<TB>(p, st);
-    if (vec && tiles256 >= 256) return launch_big<TC, TB, 2, 4, 8, 4>(p, st);
+      if (vec && tiles256 >= 256 && xl_shape_ok<TC>(p)) return launch_xl<TA, TB>(p, st);
+    if (vec && tiles256 >= 256) return launch_big<TA, TC, TB, 2, 4, 8, 4>(p, st);
   }
   const int64_t tiles128 = static_cast<int64_t>(p.n) * cdiv(p.m, 128) * cdiv(p.o, 128);
   if (tiles128 >= 512) return launch_cfg<TA, TC, TB, 64, 64, 2, 2>(p, vec, st);
@@ -1222,6 +1237,16 @@ int32_t grouped_gemm(const GemmParams& p0, int32_t dtype, int32_t out_dtype, int
     if (out_dtype == WC_F32)
       return bias_f32 ? launch_gemm_t<bf16, float, float>(p, vec, st)
                       : launch_gemm_t<bf16, float, bf16>(p, vec, st);
+    return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: output dtype %s", dtype_name(out_dtype));
+  }
+  if (dtype == WC_F16) {
+    const bool bias_f32 = p.bias && bias_dtype == WC_F32;
+    if (p.bias && bias_dtype != WC_F32 && bias_dtype != WC_F16)
+      return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: bias dtype %s", dtype_name(bias_dtype));
+    if (out_dtype == WC_F16)
+      return bias_f32 ? launch_gemm_t<f16, f16, float>(p, vec, st) : launch_gemm_t<f16, f16, f16>(p, vec, st);
+    if (out_dtype == WC_F32)
+      return bias_f32 ? launch_gemm_t<f16, float, float>(p, vec, st) : launch_gemm_t<f16, float, f16>(p, vec, st);
     return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: output dtype %s", dtype_name(out_dtype));
   }
   return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: unsupported dtype %s", dtype_name(dtype));

@@ -255,6 +255,48 @@ def test_grouped_gemm_large_tiles_plain(hip, m, o, k, c_ri, bias_dtype, relu):
         assert torch.isnan(c[:, gaps]).all()
 
 
+TOL_F16 = 2e-3   # fp16 output rounding (2^-11 relative) over fp32 accumulation
+
+
+@pytest.mark.parametrize("m,o,k,n,res", [(64, 48, 40, 4, False), (96, 80, 64, 6, True), (257, 255, 72, 128, True),
+                                         (512, 256, 512, 128, False), (512, 256, 256, 128, True)])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("bias_dtype", [torch.float16, torch.float32])
+def test_grouped_gemm_fp16(hip, m, o, k, n, res, out_dtype, bias_dtype):
+    """fp16 operands on the fp16 MFMA (v_mfma_f32_16x16x32_f16) through every kernel family:
+    the small-tile kernel, the 128x64-wave large-tile kernel (k = 72), the two-waves-per-SIMD
+    persistent kernel (no residual) and the persistent kernel with a fused residual + ReLU."""
+    from wide_compiler import _hip
+    g = gen(117)
+    a = _rand((n, m, k), g, torch.float16)
+    w = (_rand((n, o, k), g) * k ** -0.5).to(torch.float16)
+    bias = _rand((n, o), g, bias_dtype)
+    r = _rand((n, m, o), g, out_dtype) if res else None
+    c = torch.empty((n, m, o), dtype=out_dtype, device=DEV)
+    _hip.grouped_gemm(n=n, m=m, o=o, k=k, a=a.to(DEV), a_sn=m * k, a_so=0, a_si=k, a_rows_inner=m, w=w.to(DEV),
+                      w_sn=o * k, c=c, c_sn=m * o, c_so=0, c_si=o, c_rows_inner=m, bias=bias.to(DEV), bias_sn=o,
+                      residual=None if r is None else r.to(DEV), r_sn=m * o, r_so=0, r_si=o, relu=res)
+    exact = torch.bmm(a.double(), w.double().transpose(1, 2).contiguous()) + bias.double().unsqueeze(1)
+    if res:
+        exact = F.relu(exact + r.double())
+    assert rel_err(c.cpu(), exact) <= (TOL_F16 if not res or out_dtype == torch.float32 else 2 * TOL_F16)
+
+
+def test_linear_fp16_module(hip):
+    """WideLinear built from fp16 nn.Linear modules runs on the fp16 MFMA path."""
+    import wide_compiler as wc
+    g = gen(118)
+    torch.manual_seed(118)
+    mods = [nn.Linear(96, 64) for _ in range(6)]
+    wide = wc.WideLinear.from_modules(mods).to(DEV, torch.float16)
+    x = _rand((6, 5, 7, 96), g, torch.float16)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    exact = wide_ref.linear(x.double(), wide.weight.detach().cpu().double(), wide.bias.detach().cpu().double())
+    assert y.dtype == torch.float16
+    assert rel_err(y, exact) <= TOL_F16
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_linear_strided_boundary_view_and_relu(hip, dtype):
     import wide_compiler as wc
