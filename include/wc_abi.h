@@ -389,7 +389,7 @@ int32_t wc_conv3d(const wc_conv3d_args* args, void* stream);
  * 215-231):  O = softmax(Q K^T * scale [+ causal mask]) V  per (n*b, head).
  * Q/K/V/O rows live at base + nb*stride_nb + s*stride_s + head*head_dim, i.e. the
  * [N*B, S, heads*head_dim] layout of the projection outputs, read in place.
- * head_dim in {16, 32, 64, 128}; dtype WC_F32 or WC_BF16; fp32 softmax / accumulation.
+ * head_dim in {16, 32, 64, 128}; dtype WC_F32, WC_BF16 or WC_F16; fp32 softmax / accumulation.
  */
 typedef struct wc_attn_args {
   int32_t dtype, causal;

@@ -160,8 +160,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
           const bf16x8 a = *reinterpret_cast<const bf16x8*>(krow + s * 32);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt)
-            sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                a, *reinterpret_cast<const bf16x8*>(&qf[nt][s][0]), sacc[mt][nt], 0, 0, 0);
+            sacc[mt][nt] = mma16<T>(a, *reinterpret_cast<const bf16x8*>(&qf[nt][s][0]), sacc[mt][nt]);
         } else {
           const f32x4 a0 = *reinterpret_cast<const f32x4*>(krow + s * 32);
           const f32x4 a1 = *reinterpret_cast<const f32x4*>(krow + s * 32 + 4);
@@ -229,8 +228,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            bp[nt][e] = static_cast<bf16>(sacc[2 * s][nt][e]);
-            bp[nt][4 + e] = static_cast<bf16>(sacc[2 * s + 1][nt][e]);
+            // P in the operand type, carried as raw 16-bit lanes
+            bp[nt][e] = __builtin_bit_cast(bf16, static_cast<T>(sacc[2 * s][nt][e]));
+            bp[nt][4 + e] = __builtin_bit_cast(bf16, static_cast<T>(sacc[2 * s + 1][nt][e]));
           }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
           }
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt)
-            acc_o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[nt], acc_o[dt][nt], 0, 0, 0);
+            acc_o[dt][nt] = mma16<T>(a, bp[nt], acc_o[dt][nt]);
         }
       }
     } else {
@@ -622,8 +622,8 @@ using namespace wc;
 extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
   clear_error();
   WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_attention: null args");
-  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "wc_attention: unsupported dtype %s",
-             dtype_name(a->dtype));
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16 || a->dtype == WC_F16, WC_ERR_DTYPE,
+             "wc_attention: unsupported dtype %s", dtype_name(a->dtype));
   WC_REQUIRE(a->nb >= 0 && a->heads > 0 && a->sq >= 0 && a->skv >= 0 && a->head_dim > 0, WC_ERR_SHAPE,
              "wc_attention: bad sizes");
   if (a->nb == 0 || a->sq == 0) return WC_OK;
@@ -678,5 +678,6 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
     }
   }
   if (a->dtype == WC_BF16) return launch_attn<bf16>(p, (int)a->head_dim, as_stream(stream));
+  if (a->dtype == WC_F16) return launch_attn<f16>(p, (int)a->head_dim, as_stream(stream));
   return launch_attn<float>(p, (int)a->head_dim, as_stream(stream));
 }

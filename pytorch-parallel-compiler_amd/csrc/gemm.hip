@@ -35,16 +35,6 @@ template <> struct Frag<bf16> { typedef bf16x8 type; };
 template <> struct Frag<float> { typedef f32x4 type; };  // two per K-step
 template <> struct Frag<f16> { typedef bf16x8 type; };    // raw 16-bit lanes, as bf16
 
-// v_mfma_f32_16x16x32 on 16-bit operands carried as raw 16-byte fragments: the bf16 or
-// the fp16 instruction by the element type T
-template <typename T>
-__device__ __forceinline__ f32x4 mma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  if constexpr (std::is_same<T, f16>::value)
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                  0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 
 __device__ __forceinline__ float relu_f(float v) { return v > 0.f ? v : 0.f; }
 

@@ -51,6 +51,25 @@ def test_self_attention(hip, dtype, n, b, t, d, h, causal):
         assert rel_err(y, _oracle(wide, x, x, x, causal, double=False)) <= TOL_BF16
 
 
+TOL_F16 = 5e-3   # fp16 Q / K / V / P and outputs (2^-11 relative rounding each)
+
+
+@pytest.mark.parametrize("n,b,t,d,h", [(3, 2, 64, 64, 2), (2, 2, 130, 256, 8), (2, 1, 200, 256, 2),
+                                       (2, 2, 100, 512, 4)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_self_attention_fp16(hip, n, b, t, d, h, causal):
+    """fp16 models: projections on the fp16 MFMA GEMM, attention on the general kernel with
+    P rounded to fp16 for the fp16 MFMA (head dims 32, 64, 128)."""
+    import wide_compiler as wc
+    g = gen(405)
+    wide = wc.WideAttention.from_modules(_mha(n, d, h, 405, torch.float32)).to(DEV, torch.float16).eval()
+    x = torch.randn(n, b, t, d, generator=g).to(torch.float16)
+    with torch.no_grad():
+        y = wide(x.to(DEV), is_causal=causal).cpu()
+    assert y.dtype == torch.float16
+    assert rel_err(y, _oracle(wide, x, x, x, causal)) <= TOL_F16
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_cross_attention_mha_mode(hip, dtype):
     import wide_compiler as wc
