@@ -323,7 +323,8 @@ int64_t wc_conv_packed_weight_elems(int64_t n, int64_t c_out, int64_t c_in, int6
  * (strides x_stride_n, x_stride_b); y and residual likewise with [c_out, h_out, w_out]
  * blocks.  BN is eval-mode (y = (v - mean) / sqrt(var + eps) * weight + bias),
  * applied when bn_mean != NULL.  Parameters are [n*c_out] of param_dtype.
- * dtype in {WC_F32, WC_BF16}; fp32 accumulation on MFMA.
+ * dtype in {WC_F32, WC_BF16, WC_F16}; fp32 accumulation on MFMA (fp16: the general
+ * packed-weight kernel).
  */
 typedef struct wc_conv_args {
   int32_t dtype, param_dtype, act;
@@ -366,7 +367,7 @@ int32_t wc_conv2d_direct_weights(const wc_conv_args* args);
  * (strides x_stride_n, x_stride_b); y likewise with [c_out, d_out, h_out, w_out]
  * blocks.  packed_weight from wc_conv_pack_weights(w, n, c_out, c_in, kd * kh, kw, ...)
  * on the grouped filter bank [n*c_out, c_in, kd, kh, kw]; bias [n*c_out] of
- * param_dtype or NULL.  dtype in {WC_F32, WC_BF16}; fp32 accumulation on MFMA.
+ * param_dtype or NULL.  dtype in {WC_F32, WC_BF16, WC_F16}; fp32 accumulation on MFMA.
  */
 typedef struct wc_conv3d_args {
   int32_t dtype, param_dtype, act;

@@ -57,7 +57,9 @@ constexpr int kConvThreads = 256;
 constexpr int kFN = 4;            // 16-wide MFMA tiles along output channels (64)
 
 __device__ __forceinline__ float ldp(const void* p, int dt, int64_t i) {
-  return dt == WC_F32 ? static_cast<const float*>(p)[i] : static_cast<float>(static_cast<const bf16*>(p)[i]);
+  if (dt == WC_F32) return static_cast<const float*>(p)[i];
+  if (dt == WC_F16) return static_cast<float>(static_cast<const f16*>(p)[i]);
+  return static_cast<float>(static_cast<const bf16*>(p)[i]);
 }
 
 template <typename T> struct ConvTraits;
@@ -66,6 +68,10 @@ template <typename T> struct ConvTraits;
 template <> struct ConvTraits<bf16> {
   static constexpr int kFM = 4;    // 64 pixels per wave, 256 per tile
   static constexpr int kPad = 8;   // channel pitch padding (elements)
+};
+template <> struct ConvTraits<f16> {
+  static constexpr int kFM = 4;
+  static constexpr int kPad = 8;
 };
 template <> struct ConvTraits<float> {
   static constexpr int kFM = 2;    // 32 pixels per wave, 128 per tile
@@ -327,8 +333,7 @@ __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
           const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xs[aoff[i] + toff]);
 #pragma unroll
           for (int j = 0; j < kFN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, *reinterpret_cast<const bf16x8*>(&bcur[2 * j]),
-                                                                 acc[i][j], 0, 0, 0);
+            acc[i][j] = mma16<T>(a, *reinterpret_cast<const bf16x8*>(&bcur[2 * j]), acc[i][j]);
         }
       } else {
 #pragma unroll
@@ -1311,6 +1316,9 @@ extern "C" int32_t wc_conv_pack_weights(const void* w, int64_t n, int64_t c_out,
   else if (dtype == WC_BF16)
     conv_pack_kernel<bf16><<<grid, 256, 0, st>>>(static_cast<const bf16*>(w), static_cast<bf16*>(out), total,
                                                  (int)c_in, ci32, (int)(kh * kw));
+  else if (dtype == WC_F16)
+    conv_pack_kernel<f16><<<grid, 256, 0, st>>>(static_cast<const f16*>(w), static_cast<f16*>(out), total,
+                                                (int)c_in, ci32, (int)(kh * kw));
   else
     return set_error(WC_ERR_DTYPE, "wc_conv_pack_weights: unsupported dtype %s", dtype_name(dtype));
   return check_launch("wc_conv_pack_weights");
@@ -1356,8 +1364,8 @@ extern "C" int32_t wc_conv2d_direct_weights(const wc_conv_args* a) {
 extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   clear_error();
   WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_conv2d: null args");
-  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "wc_conv2d: unsupported dtype %s",
-             dtype_name(a->dtype));
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16 || a->dtype == WC_F16, WC_ERR_DTYPE,
+             "wc_conv2d: unsupported dtype %s", dtype_name(a->dtype));
   WC_REQUIRE(a->param_dtype == WC_F32 || a->param_dtype == a->dtype, WC_ERR_DTYPE,
              "wc_conv2d: parameter dtype %s", dtype_name(a->param_dtype));
   WC_REQUIRE(a->n >= 0 && a->batch >= 0 && a->c_in > 0 && a->c_out >= 0 && a->h > 0 && a->w > 0 &&
@@ -1416,6 +1424,7 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   p.x_cs = static_cast<int64_t>(p.h) * p.w;
   p.y_cs = static_cast<int64_t>(p.ho) * p.wo;
   const bool f32 = a->dtype == WC_F32;
+  const bool f16m = a->dtype == WC_F16;              // fp16: the general kernel only
   if (!(f32 ? conv_plan<float>(p) : conv_plan<bf16>(p)))
     return set_error(WC_ERR_LIMIT, "wc_conv2d: tile does not fit in LDS");
   p.fd_plane = make_fastdiv(static_cast<uint32_t>(p.ir * p.ic));
@@ -1430,7 +1439,7 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   p.vec_out = (yal && ral && p.tc % ve == 0 && p.wo % ve == 0) ? 1 : 0;
   if (p.wn) {
     // the filter bank itself: only the resident-weight kernel reads that layout
-    WC_REQUIRE(!f32 && conv_res_ok(p), WC_ERR_ARG,
+    WC_REQUIRE(!f32 && !f16m && conv_res_ok(p), WC_ERR_ARG,
                "wc_conv2d: these sizes need packed weights (wc_conv_pack_weights); "
                "wc_conv2d_direct_weights tells when the filter bank itself will do");
     return conv_res_dispatch(p, as_stream(stream));
@@ -1444,12 +1453,12 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   const size_t lds = in > epi ? in : epi;
   hipStream_t st = as_stream(stream);
   // resident-weight path: bf16 "same" convolution, stride 1, C_in 32 / 64, C_out % 64 == 0
-  if (!f32) {
+  if (!f32 && !f16m) {
     const int32_t rc = conv_res_dispatch(p, st);
     if (rc != 1) return rc;
   }
   // fast path: weights and input chunk both staged in LDS (bf16, stride 1, W % 8 == 0)
-  if (!f32 && p.sh == 1 && p.sw == 1 && p.kh * p.kw <= kFastTaps && p.w % 8 == 0 && aligned(p.x, 16) &&
+  if (!f32 && !f16m && p.sh == 1 && p.sw == 1 && p.kh * p.kw <= kFastTaps && p.w % 8 == 0 && aligned(p.x, 16) &&
       (p.x_sn * es) % 16 == 0 && (p.x_sb * es) % 16 == 0 && (static_cast<int64_t>(p.h) * p.w * es) % 16 == 0) {
     ConvParams q = p;
     if (conv_fast_plan(q)) {
@@ -1479,14 +1488,15 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   }
   const dim3 grid(static_cast<uint32_t>(nblk));
   if (f32) return launch_big_lds(conv_kernel<float>, p, grid, lds, st);
+  if (f16m) return launch_big_lds(conv_kernel<f16>, p, grid, lds, st);
   return launch_big_lds(conv_kernel<bf16>, p, grid, lds, st);
 }
 
 extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
   clear_error();
   WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_conv3d: null args");
-  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "wc_conv3d: unsupported dtype %s",
-             dtype_name(a->dtype));
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16 || a->dtype == WC_F16, WC_ERR_DTYPE,
+             "wc_conv3d: unsupported dtype %s", dtype_name(a->dtype));
   WC_REQUIRE(a->param_dtype == WC_F32 || a->param_dtype == a->dtype, WC_ERR_DTYPE,
              "wc_conv3d: parameter dtype %s", dtype_name(a->param_dtype));
   WC_REQUIRE(a->act == WC_ACT_NONE || a->act == WC_ACT_RELU, WC_ERR_ARG, "wc_conv3d: bad act %d", a->act);
@@ -1546,6 +1556,7 @@ extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
   p.y_sn = a->y_stride_n;
   p.y_sb = a->y_stride_b;
   const bool f32 = a->dtype == WC_F32;
+  const bool f16m = a->dtype == WC_F16;              // fp16: the general kernel only
   if (!(f32 ? conv_plan<float>(p) : conv_plan<bf16>(p)))
     return set_error(WC_ERR_LIMIT, "wc_conv3d: tile does not fit in LDS");
   p.fd_plane = make_fastdiv(static_cast<uint32_t>(p.ir * p.ic));
@@ -1568,5 +1579,6 @@ extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
   const dim3 grid(static_cast<uint32_t>(nblk));
   hipStream_t st = as_stream(stream);
   if (f32) return launch_big_lds(conv_kernel<float>, p, grid, lds, st);
+  if (f16m) return launch_big_lds(conv_kernel<f16>, p, grid, lds, st);
   return launch_big_lds(conv_kernel<bf16>, p, grid, lds, st);
 }

@@ -433,7 +433,7 @@ __global__ __launch_bounds__(kStepThreads, CELL == WC_CELL_GRU ? 2 : 4) void rnn
               const bf16x8 a = *reinterpret_cast<const bf16x8*>(arow + k * 32);
 #pragma unroll
               for (int j = 0; j < NTW; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, rb[s][j][0], acc[j], 0, 0, 0);
+                acc[j] = mma16<T>(a, rb[s][j][0], acc[j]);
             } else {
               const f32x4 a0 = *reinterpret_cast<const f32x4*>(arow + k * 32);
               const f32x4 a1 = *reinterpret_cast<const f32x4*>(arow + k * 32 + 4);
@@ -618,8 +618,8 @@ static int32_t rnn_check(const wc_rnn_args* a, const char* what, RnnParams& p, i
   WC_REQUIRE(a != nullptr, WC_ERR_NULL, "%s: null args", what);
   WC_REQUIRE(a->cell == WC_CELL_GRU || a->cell == WC_CELL_LSTM, WC_ERR_ARG, "%s: unknown cell %d", what,
              a->cell);
-  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16, WC_ERR_DTYPE, "%s: unsupported dtype %s", what,
-             dtype_name(a->dtype));
+  WC_REQUIRE(a->dtype == WC_F32 || a->dtype == WC_BF16 || a->dtype == WC_F16, WC_ERR_DTYPE,
+             "%s: unsupported dtype %s", what, dtype_name(a->dtype));
   WC_REQUIRE(a->n >= 0 && a->batch >= 0 && a->steps >= 0 && a->input_size > 0 && a->hidden > 0,
              WC_ERR_SHAPE, "%s: bad sizes", what);
   gates = a->cell == WC_CELL_GRU ? 3 : 4;
@@ -713,6 +713,10 @@ static int32_t persistent_recurrence(const wc_rnn_args* a, RnnParams p, int gate
     if (a->cell == WC_CELL_GRU) return launch_rec<float, WC_CELL_GRU>(p, grid, block, lds, st);
     return launch_rec<float, WC_CELL_LSTM>(p, grid, block, lds, st);
   }
+  if (a->dtype == WC_F16) {
+    if (a->cell == WC_CELL_GRU) return launch_rec<f16, WC_CELL_GRU>(p, grid, block, lds, st);
+    return launch_rec<f16, WC_CELL_LSTM>(p, grid, block, lds, st);
+  }
   if (a->cell == WC_CELL_GRU) return launch_rec<bf16, WC_CELL_GRU>(p, grid, block, lds, st);
   return launch_rec<bf16, WC_CELL_LSTM>(p, grid, block, lds, st);
 }
@@ -737,6 +741,9 @@ extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
     if (a->dtype == WC_F32)
       return a->cell == WC_CELL_GRU ? streamed_recurrence<float, WC_CELL_GRU>(a, p, st)
                                     : streamed_recurrence<float, WC_CELL_LSTM>(a, p, st);
+    if (a->dtype == WC_F16)
+      return a->cell == WC_CELL_GRU ? streamed_recurrence<f16, WC_CELL_GRU>(a, p, st)
+                                    : streamed_recurrence<f16, WC_CELL_LSTM>(a, p, st);
     return a->cell == WC_CELL_GRU ? streamed_recurrence<bf16, WC_CELL_GRU>(a, p, st)
                                   : streamed_recurrence<bf16, WC_CELL_LSTM>(a, p, st);
   }

@@ -46,6 +46,33 @@ def test_conv2d(hip, dtype, n, b, ci, co, hw, k, stride, pad, dil):
                                           dilation=wide.dilation)) <= TOL_BF16
 
 
+TOL_F16 = 2e-3   # fp16 output rounding (2^-11 relative) over fp32 accumulation
+
+
+@pytest.mark.parametrize("n,b,ci,co,hw,k,stride,pad,dil", [
+    (4, 2, 64, 64, (32, 32), 3, 1, 1, 1),
+    (2, 1, 40, 72, (9, 11), 3, 2, 1, 1),
+    (2, 3, 8, 8, (12, 12), 5, 1, 2, 2),
+    (5, 1, 16, 130, (6, 7), 1, 1, 0, 1),
+])
+def test_conv2d_fp16(hip, n, b, ci, co, hw, k, stride, pad, dil):
+    """fp16 models: packed-weight implicit GEMM on the fp16 MFMA (v_mfma_f32_16x16x32_f16)."""
+    import wide_compiler as wc
+    g = gen(205)
+    torch.manual_seed(205)
+    mods = [nn.Conv2d(ci, co, k, stride=stride, padding=pad, dilation=dil) for _ in range(n)]
+    wide = wc.WideConv2d.from_modules(mods).to(DEV, torch.float16)
+    x = _rand((n, b, ci, *hw), g, torch.float16)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    cw = wide.grouped_conv.weight.detach().cpu()
+    cb = wide.grouped_conv.bias.detach().cpu()
+    exact = wide_ref.conv2d(x.double(), cw.double(), cb.double(), n, stride=wide.stride, padding=wide.padding,
+                            dilation=wide.dilation)
+    assert y.dtype == torch.float16
+    assert rel_err(y, exact) <= TOL_F16
+
+
 def test_conv2d_weight_update_invalidates_packing(hip):
     import wide_compiler as wc
     g = gen(201)
@@ -324,6 +351,22 @@ def test_conv3d(hip, dtype, n, b, ci, co, dhw, k, stride, pad, dil):
     assert rel_err(y, exact) <= tol(dtype)
     if dtype == torch.bfloat16:    # the reference's own bf16 path (CPU)
         assert rel_err(y, wide_ref.conv3d(x, w, bias, n, c.stride, c.padding, c.dilation)) <= TOL_BF16
+
+
+def test_conv3d_fp16(hip):
+    import wide_compiler as wc
+    g = gen(206)
+    torch.manual_seed(206)
+    n, b, ci, co = 3, 2, 8, 16
+    mods = [nn.Conv3d(ci, co, 3, padding=1) for _ in range(n)]
+    wide = wc.WideConv3d.from_modules(mods).to(DEV, torch.float16)
+    x = _rand((n, b, ci, 6, 7, 8), g, torch.float16)
+    with torch.no_grad():
+        y = wide(x.to(DEV)).cpu()
+    ref = torch.stack([F.conv3d(x[i].double(), mods[i].weight.detach().to(torch.float16).double(),
+                                mods[i].bias.detach().to(torch.float16).double(), padding=1) for i in range(n)])
+    assert y.dtype == torch.float16
+    assert rel_err(y, ref) <= TOL_F16
 
 
 def test_conv3d_sequential_matches_grouped_and_relu(hip):

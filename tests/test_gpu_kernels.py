@@ -395,6 +395,27 @@ def test_lstm(hip, dtype, n, b, t, i, h, with_state):
         assert rel_err(cn, rc) <= TOL_BF16
 
 
+@pytest.mark.parametrize("cell,n,b,t,i,h", [("gru", 32, 4, 32, 64, 128), ("gru", 3, 2, 5, 8, 16),
+                                             ("lstm", 3, 16, 9, 32, 512), ("lstm", 4, 3, 7, 20, 64),
+                                             ("gru", 2, 18, 5, 16, 512)])
+def test_rnn_fp16(hip, cell, n, b, t, i, h):
+    """fp16 recurrences: fp16 input projection GEMM, the persistent kernel (W_hh in registers,
+    fp32 math) for small hidden sizes, the streamed kernel (fp16 MFMA per step) for 512; the
+    per-timestep bar of fp16 at every step."""
+    import wide_compiler as wc
+    g = gen(119)
+    cls, wcls, ref = (nn.GRU, wc.WideGRU, wide_ref.gru) if cell == "gru" else (nn.LSTM, wc.WideLSTM, wide_ref.lstm)
+    mods = _rnn_modules(cls, n, i, h, 119, torch.float32)
+    wide = wcls.from_modules(mods).to(DEV, torch.float16)
+    x = _rand((n, b, t, i), g, torch.float16)
+    with torch.no_grad():
+        out = wide(x.to(DEV))[0].cpu()
+    p = [getattr(wide, k).detach().cpu().double() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    eo = ref(x.double(), *p)[0]
+    assert out.dtype == torch.float16
+    assert max(_per_step_err(out, eo)) <= 5e-3, _per_step_err(out, eo)
+
+
 def test_gru_matches_nn_gru_per_model(hip):
     """The kernel against torch.nn.GRU itself (the reference's validation target)."""
     import wide_compiler as wc
