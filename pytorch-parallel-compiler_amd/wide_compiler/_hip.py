@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence
 
 import torch
 from torch import Tensor
@@ -339,8 +339,30 @@ def mlp2_args(*, n: int, m: int, in_features: int, hidden: int, out_features: in
     return a
 
 
+try:
+    # CPython launcher of the entry points (built beside libwide_hip.so): a call through it
+    # costs a fraction of a ctypes call, which dominates a small forward's host time
+    from . import _wc_launch
+except ImportError:     # not built: the ctypes binding of the same entry points
+    _wc_launch = None
+_entries: Dict[str, int] = {}
+
+
+def entry_address(name: str) -> int:
+    """Address of libwide_hip.so's entry point `name` (looked up once)."""
+    a = _entries.get(name)
+    if a is None:
+        a = _entries[name] = ctypes.cast(getattr(lib(), name), ctypes.c_void_p).value
+    return a
+
+
 def mlp2_launch(a: "_Mlp2Args", stream: int) -> None:
-    _check(lib().wc_mlp2(ctypes.byref(a), stream), "wc_mlp2")
+    if _wc_launch is not None:
+        rc = _wc_launch.call2(_entries.get("wc_mlp2") or entry_address("wc_mlp2"), ctypes.addressof(a), stream)
+    else:
+        rc = lib().wc_mlp2(ctypes.byref(a), stream)
+    if rc:
+        _check(rc, "wc_mlp2")
 
 
 def mlp2(**kw) -> None:
