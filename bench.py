@@ -359,26 +359,16 @@ def cfg_attention(dev, steps, warmup) -> Dict:
         return max(errs)
 
     def kernels():
-        qkv = torch.empty((n, b, s, 3 * d), device=dev, dtype=x.dtype)
         o = torch.empty((n, b, s, d), device=dev, dtype=x.dtype)
-        st = (s * 3 * d, 3 * d)
-        attn = lambda: _hip.attention(q=qkv, k=qkv[..., d:], v=qkv[..., 2 * d:], o=o, nb=n * b, heads=hh,  # noqa
-                                      sq=s, skv=s, head_dim=dh, q_strides=st, k_strides=st, v_strides=st,
-                                      o_strides=(s * d, d), scale=dh ** -0.5, causal=False)
-
-        def project_qkv():                   # the two GEMMs of WideAttention's self-attention path
-            wide._project(x, wide.q_weight, d * d, wide.q_bias, d, d, out=qkv, col0=0)
-            wide._project(x, wide.kv_weight, 2 * d * d, wide.kv_bias, 2 * d, 2 * d, out=qkv, col0=d)
-        with torch.inference_mode():
-            project_qkv()
-        t_attn = _event_time(attn, steps, warmup)
-        t_qkv = _event_time(project_qkv, steps, warmup)
+        fused = lambda: _hip.self_attention(x=x, q_weight=wide.q_weight, kv_weight=wide.kv_weight,  # noqa: E731
+                                            q_bias=wide.q_bias, kv_bias=wide.kv_bias, o=o, heads=hh,
+                                            scale=dh ** -0.5, causal=False)
+        t_attn = _event_time(fused, steps, warmup)
         t_out = _event_time(lambda: wide._project(o, wide.out_weight, d * d, wide.out_bias, d, d), steps, warmup)
         rows = n * b * s
-        return [_kernel("gemm_xl8_kernel x2 (Q and K|V projections 256 -> 256 + 512 into one Q|K|V buffer, bf16)",
-                        "mfma", t_qkv, flops=2.0 * rows * 3 * d * d, peak=PEAK["bf16_mfma"]),
-                _kernel("attn_res_kernel (fused softmax(QK^T)V, bf16, head_dim 32, K/V resident in LDS)", "mfma",
-                        t_attn, flops=4.0 * n * b * hh * s * s * dh, peak=PEAK["bf16_mfma"]),
+        return [_kernel("attn_qkv_kernel (Q/K/V projections 256 -> 3 x 256 + softmax(QK^T)V, bf16, head_dim 32, "
+                        "K/V resident in LDS)", "mfma", t_attn,
+                        flops=2.0 * rows * 3 * d * d + 4.0 * n * b * hh * s * s * dh, peak=PEAK["bf16_mfma"]),
                 _kernel("gemm_xl8_kernel (output projection 256 -> 256, bf16)", "mfma", t_out,
                         flops=2.0 * rows * d * d, peak=PEAK["bf16_mfma"])]
 

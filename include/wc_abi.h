@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define WC_ABI_VERSION 2
+#define WC_ABI_VERSION 3
 
 /* element types */
 enum {
@@ -413,6 +413,40 @@ typedef struct wc_attn_args {
 } wc_attn_args;
 
 int32_t wc_attention(const wc_attn_args* args, void* stream);
+
+/*
+ * Self-attention core with the Q and K|V projections fused in -- replaces the Q, K and V
+ * einsums and bias adds, the head reshapes and F.scaled_dot_product_attention of
+ * WideAttention._forward_fused (wide_compiler/core/primitives/wide_attention.py:197-231)
+ * when query, key and value are one tensor x:
+ *   O = softmax((x Wq^T + bq) (x Wk^T + bk)^T * scale [+ causal mask]) (x Wv^T + bv)
+ * per (model, batch row, head), with Wk, Wv = kv_weight rows [0, D), [D, 2D) and bk, bv the
+ * matching halves of kv_bias.  The output projection stays a grouped GEMM (wc_grouped_gemm).
+ * x row t of (model n, batch row b) at x + n*x_stride_n + b*x_stride_b + t*x_stride_s (D
+ * contiguous elements); O row at o + (n*B + b)*o_stride_nb + t*o_stride_s.  Weights and
+ * biases have contiguous rows.  Supported (else WC_ERR_LIMIT, nothing launched): dtype
+ * WC_BF16, head_dim = d_model / heads = 32, 1 <= s <= 512, d_model <= 768; no mask.  Q, K, V
+ * are rounded to bf16 after the fp32 bias add, as the unfused path's GEMMs round them.
+ */
+typedef struct wc_self_attn_args {
+  int32_t dtype, causal;
+  int64_t n, b, s, d_model, heads;
+  float scale;
+  const void* x;
+  int64_t x_stride_n, x_stride_b, x_stride_s;
+  const void* q_weight;        /* [N][D][D] */
+  int64_t q_weight_stride_n;
+  const void* kv_weight;       /* [N][2D][D] */
+  int64_t kv_weight_stride_n;
+  const void* q_bias;          /* [N][D] or NULL */
+  int64_t q_bias_stride_n;
+  const void* kv_bias;         /* [N][2D] or NULL */
+  int64_t kv_bias_stride_n;
+  void* o;
+  int64_t o_stride_nb, o_stride_s;
+} wc_self_attn_args;
+
+int32_t wc_self_attention(const wc_self_attn_args* args, void* stream);
 
 #ifdef __cplusplus
 }

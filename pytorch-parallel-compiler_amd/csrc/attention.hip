@@ -339,6 +339,149 @@ inline size_t res_lds_bytes(int dh, int skvp) {
   return (static_cast<size_t>(skvp) * (dh + 8) + static_cast<size_t>(dh) * (skvp + 4)) * sizeof(bf16);
 }
 
+// The key loop of attn_res_kernel as functions, for attn_qkv_kernel.  attn_res_kernel keeps its
+// own inline copy: its causal variant compiled through these functions takes 136 VGPRs
+// instead of 121, which costs a wave per SIMD.
+//
+// One wave's two 32-query blocks in the resident-KV key loop: the Q^T fragments (B operand of
+// S^T = K Q^T, pre-scaled by scale * log2(e)), the row of -base that the extra k-step adds
+// (qneg: B operand, k = 0 of the lanes < 32), the O^T accumulators, and per query row the
+// running base (a bf16 value, 0 until the first block sets it) and the running sum.
+template <int NKS, int DT>
+struct ResRows {
+  bf16x8 qf[2][NKS];
+  bf16x8 qneg[2];
+  f32x16 oacc[2][DT];
+  float base[2], lrun[2];
+};
+
+template <int NKS, int DT>
+__device__ __forceinline__ void res_rows_init(ResRows<NKS, DT>& r) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.qneg[b][e] = static_cast<bf16>(0.0f);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) r.oacc[b][d][e] = 0.f;
+    r.base[b] = 0.f;
+    r.lrun[b] = 0.f;
+  }
+}
+
+// K extended by a column of ones: A operand of the extra k-step, k = 0 of the lanes < 32
+__device__ __forceinline__ bf16x8 res_kone(int hf) {
+  bf16x8 kone;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) kone[e] = static_cast<bf16>(e == 0 && hf == 0 ? 1.0f : 0.0f);
+  return kone;
+}
+
+// One 32-key block starting at key0, for both query blocks (first queries qrow[0], qrow[1]).  kf: A fragments of S^T = K Q^T
+// (lane: key key0 + l%32, k-step k).  vf: A fragments of O^T += V^T P^T (lane: head dim
+// 32 d + l%32; k-step j takes the keys of S^T registers 8 j .. 8 j + 7, i.e. keys
+// 16 j + 8 (e / 4) + 4 (l / 32) + e % 4 of the block).  Both query blocks' scores come
+// first (their MFMA latency hides behind the first block's softmax), then per query block
+// the softmax and P V.
+template <int NKS, int DT, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void res_key_block(ResRows<NKS, DT>& r, const int (&qrow)[2], const bf16x8 (&kf)[NKS],
+                                              const bf16x8 (&vf)[DT][2], const bf16x8& kone, int key0,
+                                              bool first, int skv, int hf, int l32) {
+  f32x16 s[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    if (CAUSAL && key0 > qrow[b] + 31) continue;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[b][e] = 0.f;
+#pragma unroll
+    for (int k = 0; k < NKS; ++k) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[k], r.qf[b][k], s[b], 0, 0, 0);
+    s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kone, r.qneg[b], s[b], 0, 0, 0);
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    if (CAUSAL && key0 > qrow[b] + 31) continue;
+    if constexpr (MASK) {
+      const int q = qrow[b] + l32;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = key0 + (i >> 2) * 8 + 4 * hf + (i & 3);
+        if (key >= skv || (CAUSAL && key > q)) s[b][i] = -INFINITY;
+      }
+    }
+    // tree reductions keep the dependency chains short
+    const float m0 = __builtin_fmaxf(__builtin_fmaxf(s[b][0], s[b][1]), s[b][2]);
+    const float m1 = __builtin_fmaxf(__builtin_fmaxf(s[b][3], s[b][4]), s[b][5]);
+    const float m2 = __builtin_fmaxf(__builtin_fmaxf(s[b][6], s[b][7]), s[b][8]);
+    const float m3 = __builtin_fmaxf(__builtin_fmaxf(s[b][9], s[b][10]), s[b][11]);
+    const float m4 = __builtin_fmaxf(__builtin_fmaxf(s[b][12], s[b][13]), s[b][14]);
+    float bm = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(m0, m1), m2),
+                               __builtin_fmaxf(__builtin_fmaxf(m3, m4), s[b][15]));
+    bm = other_half_max(bm);                          // block max relative to base[b]
+    const bool up = first || bm > kLazyRescale;
+    if (__builtin_amdgcn_ballot_w64(up)) {
+      // new base (a bf16 value, so -base is exact in qneg); this block's exponents
+      // are moved by the same shift d and earlier blocks rescaled by 2^-d
+      const float nbase = up && bm > -INFINITY ? static_cast<float>(static_cast<bf16>(r.base[b] + bm)) : r.base[b];
+      const float d = nbase - r.base[b];
+      const float alpha = d == 0.f ? 1.0f : __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+      for (int dd = 0; dd < DT; ++dd) r.oacc[b][dd] *= alpha;
+      r.lrun[b] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[b][i] -= d;
+      r.base[b] = nbase;
+      r.qneg[b][0] = static_cast<bf16>(hf == 0 ? -nbase : 0.0f);
+    }
+    float pv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pv[i] = __builtin_amdgcn_exp2f(s[b][i]);
+    bf16x8 pf[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pf[i >> 3][i & 7] = static_cast<bf16>(pv[i]);
+    // row sum of the bf16-rounded P that P V uses: v_dot2_f32_bf16 against (1, 1), two
+    // bf16 values per instruction on two independent chains
+    float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bf16x2 pair = {pf[i >> 2][2 * (i & 3)], pf[i >> 2][2 * (i & 3) + 1]};
+      if (i & 1)
+        l1 = __builtin_amdgcn_fdot2_f32_bf16(pair, kOnes2, l1, false);
+      else
+        l0 = __builtin_amdgcn_fdot2_f32_bf16(pair, kOnes2, l0, false);
+    }
+    r.lrun[b] += l0 + l1;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        r.oacc[b][d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[d][j], pf[j], r.oacc[b][d], 0, 0, 0);
+  }
+}
+
+// O = (O^T / l)^T: lane holds query qrow[b] + l%32, head dims 8 (i/4) + 4 (l/32) + i%4 (+32 d)
+// of register i; ob points at head dim 0 of query 0
+template <int NKS, int DT>
+__device__ __forceinline__ void res_store_o(const ResRows<NKS, DT>& r, const int (&qrow)[2], bf16* ob, int64_t o_ss,
+                                            int sq, int hf, int l32) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const float lt = other_half_sum(r.lrun[b]);
+    const int q = qrow[b] + l32;
+    if (q >= sq) continue;
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bf16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = from_f32<bf16>(r.oacc[b][d][4 * g4 + e] * inv);
+        *reinterpret_cast<bf16x4*>(ob + static_cast<int64_t>(q) * o_ss + d * 32 + g4 * 8 + 4 * hf) = o4;
+      }
+  }
+}
+
 template <int DH, int W, bool CAUSAL>
 __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp) {
   constexpr int KP = res_kpitch<DH>();
@@ -583,6 +726,247 @@ int32_t launch_res(AttnParams p, int skvp, hipStream_t st) {
   return check_launch("wc_attention");
 }
 
+// ---------------------------------------------------------------------------
+// Self-attention with the Q, K and V projections inside (bf16, head dim 32).
+// One workgroup per (model*batch, head), holding every token of the row (S <= W*64):
+//   phase 1  the head's 96 projection rows (its Q, K and V rows of the weights, D wide)
+//            and their biases (fp32, zero when absent) are staged in LDS;
+//   phase 2  wave w projects its two 32-token blocks w and 2W-1-w (its query blocks) with
+//            v_mfma_f32_32x32x16_bf16, reading x straight from memory (no other wave needs
+//            those rows): Q^T = Wq x^T and K^T = Wk x^T (lane: token l%32, head dims
+//            8 (i/4) + 4 (l/32) + i%4 in register i) and V = x Wv^T (lane: head dim l%32,
+//            tokens 8 (i/4) + 4 (l/32) + i%4).  Registers 8k..8k+7 of Q^T are then the B
+//            fragments of k-step k of S^T = K Q^T for the head-dim order
+//            16 k + 8 (e/4) + 4 (l/32) + e%4, which the K^T registers share, and registers
+//            8j..8j+7 of V are the A fragments of k-step j of O^T += V^T P^T for their key
+//            block, so neither needs a lane exchange.  The accumulators start at the bias;
+//   phase 3  K and V (rounded to bf16) go to LDS over the weights in fragment
+//            order, [32-key block][k-step][lane half][lane%32][8], read back with one
+//            conflict-free 16-byte load per fragment;
+// then the resident key loop (res_key_block) over the key blocks.
+// ---------------------------------------------------------------------------
+struct QkvParams {
+  int nb, heads, b, s, d;                            // nb = models * b rows; d = model dim
+  float scale_log2;
+  const bf16* x;
+  int64_t x_sn, x_sb, x_ss;
+  const bf16* wq;                                    // [models][d][d]
+  int64_t wq_sn;
+  const bf16* wkv;                                   // [models][2d][d]: K rows, then V rows
+  int64_t wkv_sn;
+  const bf16* bq;                                    // [models][d] or null
+  int64_t bq_sn;
+  const bf16* bkv;                                   // [models][2d] or null
+  int64_t bkv_sn;
+  bf16* o;
+  int64_t o_sb, o_ss;
+};
+
+constexpr int kQkvRows = 96;                         // Q, K and V rows of one head (head dim 32)
+constexpr int kQkvBlockElems = 1024;                 // K (or V) fragments of one 32-key block
+
+inline size_t qkv_lds_bytes(int d, int w) {
+  // phases 1-2: the weight rows, then their 96 biases in fp32
+  const size_t wts = static_cast<size_t>(kQkvRows) * (d + 8) * sizeof(bf16) + kQkvRows * sizeof(float);
+  const size_t kv = static_cast<size_t>(2 * w) * 2 * kQkvBlockElems * sizeof(bf16);
+  return wts > kv ? wts : kv;
+}
+
+template <int W, bool CAUSAL>
+__global__ __launch_bounds__(W * 64, 4) void attn_qkv_kernel(QkvParams p) {   // 4 waves per SIMD
+  constexpr int NKS = 2, DT = 1;                     // head dim 32: two 16-dim k-steps, one O^T tile
+  extern __shared__ float4 smem4[];
+  bf16* const wsm = reinterpret_cast<bf16*>(smem4);  // phases 1-2: [96][d + 8], then float [96] biases
+  bf16* const ksm = wsm;                             // phase 3 on: [2W][NKS][2][32][8]
+  bf16* const vsm = wsm + 2 * W * kQkvBlockElems;    //             [2W][2][2][32][8]
+  const int wp = p.d + 8;
+  float* const bsm = reinterpret_cast<float*>(wsm + kQkvRows * wp);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hf = lane >> 5;
+  // XCD x takes the contiguous range [x G / 8, (x + 1) G / 8) of (row, head) ids: the heads of
+  // one row read its x through one L2, and the rows of one model its weights
+  const int G = gridDim.x;
+  const int bid = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int nb = bid / p.heads, h = bid - nb * p.heads;
+  const int mdl = nb / p.b, bb = nb - mdl * p.b;
+
+  // ---- phase 1: rows 0-31 = Wq, 32-63 = Wk, 64-95 = Wv rows of head h ----
+  {
+    const bf16* wq = p.wq + mdl * p.wq_sn + static_cast<int64_t>(h) * 32 * p.d;
+    const bf16* wk = p.wkv + mdl * p.wkv_sn + static_cast<int64_t>(h) * 32 * p.d;
+    const bf16* wv = wk + static_cast<int64_t>(p.d) * p.d;
+    if (tid < kQkvRows) {                            // biases; absent ones are zero
+      const bf16* bsrc = tid < 32 ? (p.bq ? p.bq + mdl * p.bq_sn + h * 32 + tid : nullptr)
+                                  : (p.bkv ? p.bkv + mdl * p.bkv_sn + (tid < 64 ? 0 : p.d) + h * 32 + (tid & 31)
+                                           : nullptr);
+      bsm[tid] = bsrc ? static_cast<float>(*bsrc) : 0.f;
+    }
+    const int cpr = p.d / 8;                         // 16-byte chunks per row
+    const int total = kQkvRows * cpr;
+    constexpr int U = 4;                             // chunks per thread in flight
+    for (int e0 = tid; e0 < total; e0 += U * W * 64) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * W * 64;
+        const int row = e / cpr, c = (e - row * cpr) * 8;
+        const bf16* src = row < 32 ? wq + row * p.d : row < 64 ? wk + (row - 32) * p.d : wv + (row - 64) * p.d;
+        v[u] = e < total ? *reinterpret_cast<const uint4*>(src + c) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * W * 64;
+        if (e >= total) continue;
+        const int row = e / cpr, c = (e - row * cpr) * 8;
+        *reinterpret_cast<uint4*>(wsm + row * wp + c) = v[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: Q, K, V of the wave's token blocks ----
+  const int qrow[2] = {wave * 32, (2 * W - 1 - wave) * 32};
+  ResRows<NKS, DT> r;
+  bf16x8 kreg[2][NKS], vreg[2][2];
+  const float c = p.scale_log2;
+  const bf16* xb = p.x + mdl * p.x_sn + bb * p.x_sb;
+  const int ksteps = p.d / 16;                       // even: d is a multiple of 32
+  // one pass over the k-steps of block b: Q^T if QP, K^T and V if KVP (both, for both blocks)
+  auto project = [&](int b, auto qp_tag, auto kvp_tag) {
+    constexpr bool QP = decltype(qp_tag)::value, KVP = decltype(kvp_tag)::value;
+    // the accumulators start at the bias of their head dims (an fp32 add before the bf16
+    // rounding, as in the projection GEMM's epilogue)
+    f32x16 aq, ak, av;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 tq = QP ? *reinterpret_cast<const f32x4*>(bsm + 8 * i + 4 * hf) : f32x4{};
+      const f32x4 tk = KVP ? *reinterpret_cast<const f32x4*>(bsm + 32 + 8 * i + 4 * hf) : f32x4{};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        aq[4 * i + e] = tq[e];
+        ak[4 * i + e] = tk[e];
+      }
+    }
+    const float bv = KVP ? bsm[64 + l32] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) av[e] = bv;
+    if (qrow[b] < p.s) {                             // blocks past the last token stay unused
+      int tok = qrow[b] + l32;
+      tok = tok < p.s ? tok : p.s - 1;
+      const bf16* xr = xb + static_cast<int64_t>(tok) * p.x_ss + 8 * hf;
+      const bf16* wr = wsm + l32 * wp + 8 * hf;
+      bf16x8 xa[2], xn[2];
+      xa[0] = *reinterpret_cast<const bf16x8*>(xr);
+      xa[1] = *reinterpret_cast<const bf16x8*>(xr + 16);
+      for (int s = 0; s < ksteps; s += 2) {
+        xn[0] = xa[0];
+        xn[1] = xa[1];
+        if (s + 2 < ksteps) {                        // next pair of k-steps in flight
+          xn[0] = *reinterpret_cast<const bf16x8*>(xr + 16 * (s + 2));
+          xn[1] = *reinterpret_cast<const bf16x8*>(xr + 16 * (s + 3));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16* w = wr + 16 * (s + u);
+          if constexpr (QP) {
+            const bf16x8 fq = *reinterpret_cast<const bf16x8*>(w);
+            aq = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fq, xa[u], aq, 0, 0, 0);
+          }
+          if constexpr (KVP) {
+            const bf16x8 fk = *reinterpret_cast<const bf16x8*>(w + 32 * wp);
+            const bf16x8 fv = *reinterpret_cast<const bf16x8*>(w + 64 * wp);
+            ak = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fk, xa[u], ak, 0, 0, 0);
+            av = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa[u], fv, av, 0, 0, 0);
+          }
+        }
+        xa[0] = xn[0];
+        xa[1] = xn[1];
+      }
+    }
+    // Q is pre-scaled by scale * log2(e) after its bf16 rounding and rounded again, as
+    // attn_res_kernel does with the Q it reads
+#pragma unroll
+    for (int k = 0; k < NKS; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * k + e;
+        if constexpr (QP) r.qf[b][k][e] = static_cast<bf16>(static_cast<float>(static_cast<bf16>(aq[i])) * c);
+        if constexpr (KVP) {
+          kreg[b][k][e] = static_cast<bf16>(ak[i]);
+          vreg[b][k][e] = static_cast<bf16>(av[i]);
+        }
+      }
+  };
+  using yes = std::integral_constant<bool, true>;
+  using no = std::integral_constant<bool, false>;
+  project(0, yes{}, yes{});
+  project(1, yes{}, yes{});
+  __syncthreads();                                   // every wave is done with the weights
+
+  // ---- phase 3: K and V of the wave's blocks into LDS, fragment order ----
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int kb = qrow[b] / 32;
+#pragma unroll
+    for (int k = 0; k < NKS; ++k)
+      *reinterpret_cast<bf16x8*>(ksm + (((kb * NKS + k) * 2 + hf) * 32 + l32) * 8) = kreg[b][k];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<bf16x8*>(vsm + (((kb * 2 + j) * 2 + hf) * 32 + l32) * 8) = vreg[b][j];
+  }
+  const bf16x8 kone = res_kone(hf);
+  res_rows_init(r);
+  __syncthreads();
+
+  const int nkv = (p.s + 31) / 32;                   // key blocks
+  int nkb = nkv;
+  if (CAUSAL) {
+    const int qmax = qrow[1] + 31;                   // qrow[1] >= qrow[0]
+    const int last = (qmax < p.s ? qmax : p.s - 1) / 32 + 1;
+    nkb = last < nkb ? last : nkb;
+  }
+  auto key_block = [&](int kbk, auto mask_tag, bool first) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    bf16x8 kf[NKS];
+#pragma unroll
+    for (int k = 0; k < NKS; ++k)
+      kf[k] = *reinterpret_cast<const bf16x8*>(ksm + (((kbk * NKS + k) * 2 + hf) * 32 + l32) * 8);
+    bf16x8 vf[DT][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      vf[0][j] = *reinterpret_cast<const bf16x8*>(vsm + (((kbk * 2 + j) * 2 + hf) * 32 + l32) * 8);
+    res_key_block<NKS, DT, CAUSAL, MASK>(r, qrow, kf, vf, kone, kbk * 32, first, p.s, hf, l32);
+  };
+  using masked = std::integral_constant<bool, true>;
+  using unmasked = std::integral_constant<bool, false>;
+  if (CAUSAL) {
+    for (int kbk = 0; kbk < nkb; ++kbk) key_block(kbk, masked{}, kbk == 0);
+  } else {
+    const int nfull = p.s / 32;                      // blocks with 32 valid keys
+    for (int kbk = 0; kbk < nfull; ++kbk) key_block(kbk, unmasked{}, kbk == 0);
+    if (nfull < nkb) key_block(nfull, masked{}, nfull == 0);
+  }
+  res_store_o(r, qrow, p.o + nb * p.o_sb + h * 32, p.o_ss, p.s, hf, l32);
+}
+
+template <int W>
+int32_t launch_qkv(const QkvParams& p, bool causal, hipStream_t st) {
+  const int64_t blocks = static_cast<int64_t>(p.nb) * p.heads;
+  if (blocks >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_self_attention: too many (row, head) pairs");
+  const size_t lds = qkv_lds_bytes(p.d, W);
+  auto kernel = causal ? attn_qkv_kernel<W, true> : attn_qkv_kernel<W, false>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess)
+      return set_error(static_cast<int32_t>(e), "wc_self_attention: LDS of %zu bytes refused: %s", lds,
+                       hipGetErrorString(e));
+  }
+  kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(W * 64), lds, st>>>(p);
+  return check_launch("wc_self_attention");
+}
+
 template <typename T, int DH>
 int32_t launch_attn_dh(const AttnParams& p, dim3 grid, hipStream_t st) {
   constexpr bool BF = sizeof(T) == 2;
@@ -680,4 +1064,57 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
   if (a->dtype == WC_BF16) return launch_attn<bf16>(p, (int)a->head_dim, as_stream(stream));
   if (a->dtype == WC_F16) return launch_attn<f16>(p, (int)a->head_dim, as_stream(stream));
   return launch_attn<float>(p, (int)a->head_dim, as_stream(stream));
+}
+
+extern "C" int32_t wc_self_attention(const wc_self_attn_args* a, void* stream) {
+  clear_error();
+  WC_REQUIRE(a != nullptr, WC_ERR_NULL, "wc_self_attention: null args");
+  WC_REQUIRE(a->dtype == WC_BF16, WC_ERR_LIMIT, "wc_self_attention: dtype %s (the fused kernel is bf16 only)",
+             dtype_name(a->dtype));
+  WC_REQUIRE(a->n >= 0 && a->b >= 0 && a->s >= 0 && a->d_model > 0 && a->heads > 0, WC_ERR_SHAPE,
+             "wc_self_attention: bad sizes");
+  WC_REQUIRE(a->d_model % a->heads == 0 && a->d_model / a->heads == 32, WC_ERR_LIMIT,
+             "wc_self_attention: head dim %lld (the fused kernel takes 32)",
+             static_cast<long long>(a->d_model % a->heads == 0 ? a->d_model / a->heads : 0));
+  WC_REQUIRE(a->s <= 512 && a->d_model <= 768, WC_ERR_LIMIT,
+             "wc_self_attention: s = %lld, d_model = %lld (the fused kernel takes s <= 512, d_model <= 768)",
+             static_cast<long long>(a->s), static_cast<long long>(a->d_model));
+  if (a->n == 0 || a->b == 0 || a->s == 0) return WC_OK;
+  WC_REQUIRE(a->x && a->q_weight && a->kv_weight && a->o, WC_ERR_NULL, "wc_self_attention: null pointer");
+  WC_REQUIRE(a->n * a->b < 0x7fffffffll && a->x_stride_n >= 0 && a->x_stride_b >= 0 && a->x_stride_s >= 0 &&
+                 a->o_stride_nb >= 0 && a->o_stride_s >= 0 && a->q_weight_stride_n >= 0 &&
+                 a->kv_weight_stride_n >= 0 && a->q_bias_stride_n >= 0 && a->kv_bias_stride_n >= 0,
+             WC_ERR_ARG, "wc_self_attention: negative stride or too many rows");
+  const bool al = aligned(a->x, 16) && aligned(a->q_weight, 16) && aligned(a->kv_weight, 16) &&
+                  (a->x_stride_n * 2) % 16 == 0 && (a->x_stride_b * 2) % 16 == 0 && (a->x_stride_s * 2) % 16 == 0 &&
+                  (a->q_weight_stride_n * 2) % 16 == 0 && (a->kv_weight_stride_n * 2) % 16 == 0 &&
+                  (!a->q_bias || (aligned(a->q_bias, 8) && (a->q_bias_stride_n * 2) % 8 == 0)) &&
+                  (!a->kv_bias || (aligned(a->kv_bias, 8) && (a->kv_bias_stride_n * 2) % 8 == 0)) &&
+                  aligned(a->o, 8) && (a->o_stride_nb * 2) % 8 == 0 && (a->o_stride_s * 2) % 8 == 0;
+  WC_REQUIRE(al, WC_ERR_ALIGN, "wc_self_attention: x and weight rows need 16-byte, bias and output rows 8-byte "
+             "alignment");
+  QkvParams p;
+  p.nb = static_cast<int>(a->n * a->b);
+  p.heads = static_cast<int>(a->heads);
+  p.b = static_cast<int>(a->b);
+  p.s = static_cast<int>(a->s);
+  p.d = static_cast<int>(a->d_model);
+  p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.x = static_cast<const bf16*>(a->x);
+  p.x_sn = a->x_stride_n;
+  p.x_sb = a->x_stride_b;
+  p.x_ss = a->x_stride_s;
+  p.wq = static_cast<const bf16*>(a->q_weight);
+  p.wq_sn = a->q_weight_stride_n;
+  p.wkv = static_cast<const bf16*>(a->kv_weight);
+  p.wkv_sn = a->kv_weight_stride_n;
+  p.bq = static_cast<const bf16*>(a->q_bias);
+  p.bq_sn = a->q_bias_stride_n;
+  p.bkv = static_cast<const bf16*>(a->kv_bias);
+  p.bkv_sn = a->kv_bias_stride_n;
+  p.o = static_cast<bf16*>(a->o);
+  p.o_sb = a->o_stride_nb;
+  p.o_ss = a->o_stride_s;
+  return a->s > 256 ? launch_qkv<8>(p, a->causal != 0, as_stream(stream))
+                    : launch_qkv<4>(p, a->causal != 0, as_stream(stream));
 }

@@ -23,7 +23,7 @@ from typing import Dict, List, Optional, Sequence
 import torch
 from torch import Tensor
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, F16 = 0, 1, 2
 ACT_NONE, ACT_RELU = 0, 1
@@ -134,6 +134,21 @@ class _AttnArgs(ctypes.Structure):
     ]
 
 
+class _SelfAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
+        ("n", ctypes.c_int64), ("b", ctypes.c_int64), ("s", ctypes.c_int64), ("d_model", ctypes.c_int64),
+        ("heads", ctypes.c_int64), ("scale", ctypes.c_float),
+        ("x", ctypes.c_void_p), ("x_stride_n", ctypes.c_int64), ("x_stride_b", ctypes.c_int64),
+        ("x_stride_s", ctypes.c_int64),
+        ("q_weight", ctypes.c_void_p), ("q_weight_stride_n", ctypes.c_int64),
+        ("kv_weight", ctypes.c_void_p), ("kv_weight_stride_n", ctypes.c_int64),
+        ("q_bias", ctypes.c_void_p), ("q_bias_stride_n", ctypes.c_int64),
+        ("kv_bias", ctypes.c_void_p), ("kv_bias_stride_n", ctypes.c_int64),
+        ("o", ctypes.c_void_p), ("o_stride_nb", ctypes.c_int64), ("o_stride_s", ctypes.c_int64),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -166,6 +181,7 @@ SIGNATURES = {
     "wc_conv2d_direct_weights": (_I32, [ctypes.POINTER(_ConvArgs)]),
     "wc_conv3d": (_I32, [ctypes.POINTER(_Conv3dArgs), _P]),
     "wc_attention": (_I32, [ctypes.POINTER(_AttnArgs), _P]),
+    "wc_self_attention": (_I32, [ctypes.POINTER(_SelfAttnArgs), _P]),
 }
 
 
@@ -545,6 +561,29 @@ def attention(*, q: Tensor, k: Tensor, v: Tensor, o: Tensor, nb: int, heads: int
     _check(lib().wc_attention(ctypes.byref(a), stream_of(q)), "wc_attention")
 
 
+def self_attention(*, x: Tensor, q_weight: Tensor, kv_weight: Tensor, q_bias: Optional[Tensor],
+                   kv_bias: Optional[Tensor], o: Tensor, heads: int, scale: float, causal: bool) -> None:
+    """Fused self-attention core with the Q and K|V projections inside (wc_self_attention):
+    x [N, B, S, D] (unit last stride), q_weight [N, D, D] and kv_weight [N, 2D, D] with
+    contiguous rows, biases [N, D] / [N, 2D] or None, o [N, B, S, D] contiguous (the attention
+    output before the output projection)."""
+    n, b, s, d = x.shape
+    a = _SelfAttnArgs()
+    a.dtype = dtype_code(x.dtype, "self_attention")
+    a.causal = 1 if causal else 0
+    a.n, a.b, a.s, a.d_model, a.heads = n, b, s, d, heads
+    a.scale = float(scale)
+    a.x, a.x_stride_n, a.x_stride_b, a.x_stride_s = x.data_ptr(), x.stride(0), x.stride(1), x.stride(2)
+    a.q_weight, a.q_weight_stride_n = q_weight.data_ptr(), q_weight.stride(0)
+    a.kv_weight, a.kv_weight_stride_n = kv_weight.data_ptr(), kv_weight.stride(0)
+    if q_bias is not None:
+        a.q_bias, a.q_bias_stride_n = q_bias.data_ptr(), q_bias.stride(0)
+    if kv_bias is not None:
+        a.kv_bias, a.kv_bias_stride_n = kv_bias.data_ptr(), kv_bias.stride(0)
+    a.o, a.o_stride_nb, a.o_stride_s = o.data_ptr(), o.stride(1), o.stride(2)
+    _check(lib().wc_self_attention(ctypes.byref(a), stream_of(x)), "wc_self_attention")
+
+
 def exported_symbols() -> List[str]:
     return list(SIGNATURES)
 
@@ -555,6 +594,6 @@ def exported_symbols() -> List[str]:
 # code for the hot path.
 for _name in ("pack_rows", "swap01", "embedding_gather", "layernorm", "bn_eval", "group_norm", "grouped_gemm",
               "mlp2", "mlp2_args", "mlp2_launch", "rnn_forward", "rnn_forward_noalloc", "rnn_phase", "conv_pack_weights", "conv2d", "conv3d",
-              "attention", "rnn_sync_check"):
+              "attention", "self_attention", "rnn_sync_check"):
     globals()[_name] = torch.compiler.disable(globals()[_name])
 del _name

@@ -8,10 +8,13 @@ WideAttention: N independent nn.MultiheadAttention modules
 Parameters keep the reference layout: q_weight [N, D, D], kv_weight [N, 2D, D],
 out_weight [N, D, D], q_bias [N, D], kv_bias [N, 2D], out_bias [N, D].
 
-Execution (every strategy): the Q and K/V projections are grouped MFMA GEMMs with the bias
-in the epilogue (one K|V GEMM over kv_weight when key is value), the attention core is the
-fused flash-style kernel wc_attention reading Q/K/V in place in the projections' [N*B, S,
-heads*Dh] layout, and the output projection is a third grouped GEMM.  Inference only:
+Execution (every strategy): bf16 self-attention with head dim 32, at most 512 tokens and no
+explicit mask runs the Q, K and V projections inside the attention kernel (wc_self_attention:
+each (model, batch row, head) workgroup projects its head from x and keeps K and V in LDS).
+Otherwise the Q and K/V projections are grouped MFMA GEMMs with the bias in the epilogue (one
+K|V GEMM over kv_weight when key is value) and the attention core is the fused flash-style
+kernel wc_attention reading Q/K/V in place in the projections' [N*B, S, heads*Dh] layout.  The
+output projection is a grouped GEMM in both cases.  Inference only:
 dropout in training mode raises.  ``attn_mask`` follows scaled_dot_product_attention over the
 [N*B, heads, Tq, Tkv] scores (wide_attention.py:222-228): boolean (True = attend) or additive,
 broadcastable to that shape, not together with ``is_causal``; a query whose keys are all masked
@@ -51,6 +54,8 @@ class WideAttention(nn.Module):
         if strategy == AttentionStrategy.AUTO:
             strategy = AttentionStrategy.FUSED
         self._strategy = strategy
+        # projections inside the attention kernel where it applies (False: always separate GEMMs)
+        self.fuse_projections = True
         self.q_weight = nn.Parameter(torch.empty(n, d_model, d_model))
         self.kv_weight = nn.Parameter(torch.empty(n, 2 * d_model, d_model))
         if bias:
@@ -156,6 +161,11 @@ class WideAttention(nn.Module):
         qw = self.q_weight if self.q_weight.is_contiguous() else self.q_weight.contiguous()
         ow = self.out_weight if self.out_weight.is_contiguous() else self.out_weight.contiguous()
         kvb = self.kv_bias
+        if query is key and key is value and self._fusable(query, mask, params):
+            attn = torch.empty((n, b, tq, d), dtype=query.dtype, device=query.device)
+            _hip.self_attention(x=query, q_weight=qw, kv_weight=kvw, q_bias=self.q_bias, kv_bias=kvb, o=attn,
+                                heads=hh, scale=dh ** -0.5, causal=is_causal)
+            return self._project(attn, ow, d * d, self.out_bias, d, d)
         if query is key and key is value:
             # self-attention: the Q and K|V GEMMs write columns [0, D) and [D, 3D) of one
             # [N, B, T, 3D] = Q | K | V buffer, which the attention kernel reads in place; the
@@ -188,6 +198,17 @@ class WideAttention(nn.Module):
                            q_strides=(tq * d, d), k_strides=k_strides, v_strides=v_strides, o_strides=(tq * d, d),
                            scale=dh ** -0.5, causal=is_causal, mask=mask)
         return self._project(attn, ow, d * d, self.out_bias, d, d)
+
+    def _fusable(self, x: Tensor, mask: Optional[Tensor], params) -> bool:
+        """The conditions of wc_self_attention: bf16, head dim 32, 1 <= S <= 512, D <= 768, no
+        explicit mask, x rows and strides 16-byte aligned, biases with contiguous rows."""
+        if not self.fuse_projections or mask is not None or x.dtype != torch.bfloat16 or self.d_head != 32:
+            return False
+        if not (1 <= x.shape[2] <= 512 and self.d_model <= 768 and x.shape[1] > 0):
+            return False
+        if x.stride(3) != 1 or x.data_ptr() % 16 or any(st % 8 for st in x.stride()[:3]):
+            return False
+        return all(t is None or (t.is_contiguous() and t.data_ptr() % 16 == 0) for t in params)
 
     @classmethod
     def from_modules(cls, modules: List[nn.MultiheadAttention],

@@ -125,3 +125,24 @@ def test_mlp2_arg_checks(hip):
     a.x_rows_inner, a.y_rows_inner = 0, 4
     assert hip.lib().wc_mlp2(ctypes.byref(a), None) < 0
     assert "rows_inner" in hip.last_error()
+
+
+def test_self_attention_arg_checks(hip):
+    """wc_self_attention validates on the host before any launch (pointers never dereferenced)."""
+    lib = hip.lib()
+    assert lib.wc_self_attention(None, None) == -1
+    a = hip._SelfAttnArgs()
+    a.dtype, a.n, a.b, a.s, a.d_model, a.heads = hip.BF16, 2, 3, 64, 256, 8
+    a.x = a.q_weight = a.kv_weight = a.o = 16
+    a.x_stride_n, a.x_stride_b, a.x_stride_s = 3 * 64 * 256, 64 * 256, 256
+    a.o_stride_nb, a.o_stride_s = 64 * 256, 256
+    a.q_weight_stride_n, a.kv_weight_stride_n = 256 * 256, 512 * 256
+    for field, value, code in (("dtype", hip.F32, -5), ("heads", 4, -5), ("s", 513, -5), ("d_model", 800, -5),
+                               ("x", 18, -4), ("x_stride_s", 252, -4), ("x_stride_b", -1, -6)):
+        old = getattr(a, field)
+        setattr(a, field, value)
+        assert lib.wc_self_attention(ctypes.byref(a), None) == code, field
+        assert "wc_self_attention" in hip.last_error()
+        setattr(a, field, old)
+    a.n = 0
+    assert lib.wc_self_attention(ctypes.byref(a), None) == 0

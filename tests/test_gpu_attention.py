@@ -155,6 +155,61 @@ def test_attention_mask(hip, dtype, kind, n, b, tq, tkv, d, h):
     assert rel_err(y, exact) <= tol(dtype)
 
 
+@pytest.mark.parametrize("n,b,t,d,h,bias,strided", [(2, 3, 512, 256, 8, True, False), (3, 2, 257, 96, 3, False, True),
+                                                    (2, 2, 1, 64, 2, True, False), (1, 3, 256, 128, 4, True, True),
+                                                    (2, 1, 100, 768, 24, True, False), (2, 2, 33, 32, 1, False, False)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_self_attention_fused_projections(hip, monkeypatch, n, b, t, d, h, bias, strided, causal):
+    """bf16 self-attention with head dim 32 runs the Q/K/V projections inside the attention
+    kernel (wc_self_attention).  Checked against the fp64 and bf16-input fp32 oracles and against
+    the unfused path (projection GEMMs + resident attention kernel) on the same inputs: without
+    bias, on a strided input view, one token, 32 tokens + 1, 256 (4-wave tiles) and 512 tokens,
+    and a 768-wide model (the largest weight staging)."""
+    import wide_compiler as wc
+    from wide_compiler import _hip
+    g = gen(406)
+    torch.manual_seed(406)
+    wide = wc.WideAttention(n, d, h, bias=bias)
+    if bias:
+        with torch.no_grad():
+            for p_ in (wide.q_bias, wide.kv_bias, wide.out_bias):
+                p_.normal_(0, 0.1)
+    wide = wide.to(DEV, torch.bfloat16).eval()
+    if strided:
+        base = torch.randn(n, b, t, d + 32, generator=g).to(torch.bfloat16)
+        xd = base.to(DEV)[..., 16:16 + d]
+        x = base[..., 16:16 + d]
+    else:
+        x = torch.randn(n, b, t, d, generator=g).to(torch.bfloat16)
+        xd = x.to(DEV)
+    calls = []
+    fused = _hip.self_attention
+    monkeypatch.setattr(_hip, "self_attention", lambda **kw: (calls.append(1), fused(**kw))[1])
+    with torch.no_grad():
+        y = wide(xd, is_causal=causal).cpu()
+        assert calls, "the fused projection kernel did not run"
+        wide.fuse_projections = False
+        y_sep = wide(xd, is_causal=causal).cpu()
+    assert len(calls) == 1
+    assert rel_err(y, _oracle(wide, x, x, x, causal)) <= TOL_BF16
+    assert rel_err(y, _oracle(wide, x, x, x, causal, double=False)) <= TOL_BF16
+    assert rel_err(y, y_sep) <= TOL_BF16
+
+
+def test_self_attention_fused_rejects(hip):
+    """wc_self_attention refuses what its kernel does not take (nothing is launched)."""
+    from wide_compiler import _hip
+    n, b, d = 1, 1, 128
+    w = torch.zeros(n, d, d, device=DEV, dtype=torch.bfloat16)
+    kv = torch.zeros(n, 2 * d, d, device=DEV, dtype=torch.bfloat16)
+    for t, heads, dtype in ((513, 4, torch.bfloat16), (64, 2, torch.bfloat16), (64, 4, torch.float32)):
+        x = torch.zeros(n, b, t, d, device=DEV, dtype=dtype)
+        o = torch.empty_like(x)
+        with pytest.raises(RuntimeError, match="wc_self_attention"):
+            _hip.self_attention(x=x, q_weight=w.to(dtype), kv_weight=kv.to(dtype), q_bias=None, kv_bias=None, o=o,
+                                heads=heads, scale=0.1, causal=False)
+
+
 def test_attention_config_n16(hip):
     """The attention configuration at full size: N=16 MHA(256, 8 heads), B=8, S=512, bf16.
     Every model against the fp32 oracle, three spread models against fp64."""
