@@ -682,7 +682,14 @@ __global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp
   using masked = std::integral_constant<bool, true>;
   using unmasked = std::integral_constant<bool, false>;
   if (CAUSAL) {
-    for (int kbk = 0; kbk < nkb; ++kbk) key_block(kbk, masked{}, kbk == 0);
+    // only the blocks on a query block's diagonal, or past the last key, need the mask
+    for (int kbk = 0; kbk < nkb; ++kbk) {
+      const int key0 = kbk * 32;
+      if ((key0 + 31 > qrow[0] && key0 <= qrow[0] + 31) || key0 + 31 > qrow[1] || key0 + 32 > p.skv)
+        key_block(kbk, masked{}, kbk == 0);
+      else
+        key_block(kbk, unmasked{}, kbk == 0);
+    }
   } else {
     const int nfull = p.skv / 32;                    // blocks with 32 valid keys
     for (int kbk = 0; kbk < nfull; ++kbk) key_block(kbk, unmasked{}, kbk == 0);
@@ -941,7 +948,14 @@ __global__ __launch_bounds__(W * 64, 4) void attn_qkv_kernel(QkvParams p) {   //
   using masked = std::integral_constant<bool, true>;
   using unmasked = std::integral_constant<bool, false>;
   if (CAUSAL) {
-    for (int kbk = 0; kbk < nkb; ++kbk) key_block(kbk, masked{}, kbk == 0);
+    // only the blocks on a query block's diagonal, or past the last key, need the mask
+    for (int kbk = 0; kbk < nkb; ++kbk) {
+      const int key0 = kbk * 32;
+      if ((key0 + 31 > qrow[0] && key0 <= qrow[0] + 31) || key0 + 31 > qrow[1] || key0 + 32 > p.s)
+        key_block(kbk, masked{}, kbk == 0);
+      else
+        key_block(kbk, unmasked{}, kbk == 0);
+    }
   } else {
     const int nfull = p.s / 32;                      // blocks with 32 valid keys
     for (int kbk = 0; kbk < nfull; ++kbk) key_block(kbk, unmasked{}, kbk == 0);
