@@ -61,8 +61,18 @@ def compile(  # noqa: A001 - public name of the reference API
     if cfg.compile:
         if cfg.debug:
             print(f"[WideCompiler] Compiling with mode={cfg.compile_mode}")
-        wide = torch.compile(wide, mode=cfg.compile_mode, backend=cfg.compile_backend, **cfg.compile_options)
+        wide = _compiled(wide, cfg)
     return wide
+
+
+def _compiled(wide: nn.Module, cfg: WideConfig) -> nn.Module:
+    """compile_model=True (api.py:137-147): mode "reduce-overhead" asks for CUDA graphs, which
+    torch.compile cannot take over these kernels' launches, so the model captures and replays
+    its own launches (TracedWideModel.use_graphs); other modes wrap it in torch.compile, which
+    leaves each kernel call as an opaque call between compiled regions."""
+    if cfg.compile_mode == "reduce-overhead":
+        return wide.use_graphs(True)
+    return torch.compile(wide, mode=cfg.compile_mode, backend=cfg.compile_backend, **cfg.compile_options)
 
 
 class WideBuilder:
@@ -114,8 +124,7 @@ class WideBuilder:
         if self._config.validate:
             _validate_model(wide, self._models, self._sample_input, self._config)
         if self._config.compile:
-            wide = torch.compile(wide, mode=self._config.compile_mode,
-                                 backend=self._config.compile_backend, **self._config.compile_options)
+            wide = _compiled(wide, self._config)
         return wide
 
 

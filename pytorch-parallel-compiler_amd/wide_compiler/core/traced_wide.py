@@ -438,7 +438,51 @@ class TracedWideModel(nn.Module):
         self.__dict__["_fwd_plan"] = plan
         return plan
 
+    def use_graphs(self, enabled: bool = True) -> "TracedWideModel":
+        """Opt-in launch batching: the forward's launches for one input layout (shape, strides,
+        dtype, device, grad mode) are captured once into a HIP graph (torch.cuda.CUDAGraph) and
+        replayed on the current stream for every later input of that layout; the input is first
+        copied into the graph's input buffer unless it is that buffer.  The reference reaches CUDA
+        graphs through torch.compile(mode="reduce-overhead") (api.py:137-147), which cannot capture
+        these kernels' launches from outside.  As with reduce-overhead, the returned tensor is the
+        graph's output buffer: the next call with the same layout overwrites it (clone it to keep
+        it).  Parameters are read by address, so in-place writes are seen by later replays;
+        replacing a parameter tensor, or changing the model, needs ``use_graphs(True)`` again,
+        which drops the captured graphs."""
+        self.__dict__["_graphs"] = {} if enabled else None
+        return self
+
     def forward(self, x: Tensor) -> Tensor:
+        graphs = self.__dict__.get("_graphs")
+        if graphs is not None and x.is_cuda and not torch.cuda.is_current_stream_capturing():
+            key = (x.shape, x.stride(), x.dtype, x.device, torch.is_grad_enabled(), torch.is_inference_mode_enabled())
+            entry = graphs.get(key)
+            if entry is None:
+                entry = graphs[key] = self._capture(x)
+            graph, static_x, static_y = entry
+            if x.data_ptr() != static_x.data_ptr():
+                static_x.copy_(x)
+            graph.replay()
+            return static_y
+        return self._forward_launches(x)
+
+    def _capture(self, x: Tensor) -> Tuple["torch.cuda.CUDAGraph", Tensor, Tensor]:
+        """Warm up once on a side stream (fills the plan and kept launch arguments outside the
+        capture), then capture one forward over a private input buffer."""
+        static_x = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+        static_x.copy_(x)
+        cur = torch.cuda.current_stream(x.device)
+        side = torch.cuda.Stream(device=x.device)        # default priority
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            self._forward_launches(static_x)
+        cur.wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_y = self._forward_launches(static_x)
+        return graph, static_x, static_y
+
+    def _forward_launches(self, x: Tensor) -> Tensor:
         # a model that is one fused MLP launch writing the packed output: replay its kept
         # launch arguments for an input of the form seen before (the whole forward is then
         # one allocation and one launch on the host)

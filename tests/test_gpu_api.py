@@ -1,5 +1,6 @@
 """GPU checks of the drop-in API behaviour: compile_model=True (torch.compile around the wide
-model, reference api.py:138-147) in both modes, parameter writes through ``.data`` seen by
+model, reference api.py:138-147; mode "reduce-overhead" replays the model's own captured
+launches) in both modes, graph replay of a traced model, parameter writes through ``.data`` seen by
 the next forward (the reference reads its parameters on every call), a residual whose ReLU
 alias follows the conv it feeds, and WideBatchNorm1d (wide_batchnorm_1d.py:53-73) alone and
 folded into a traced Conv1d epilogue."""
@@ -172,3 +173,67 @@ def test_traced_conv1d_bn1d_relu_folds_and_matches(hip):
         outs = wc.unpack(wide(wc.pack(ins)), 4)
         for k in range(4):
             assert rel_err(outs[k], models[k](ins[k])) <= TOL_F32
+
+
+class _Block(nn.Module):
+    """conv3x3-BN-ReLU-conv3x3-BN + identity, ReLU (the ResBlock shape of the conv tests)."""
+
+    def __init__(self, c):
+        super().__init__()
+        self.conv1 = nn.Conv2d(c, c, 3, padding=1)
+        self.bn1 = nn.BatchNorm2d(c)
+        self.conv2 = nn.Conv2d(c, c, 3, padding=1)
+        self.bn2 = nn.BatchNorm2d(c)
+
+    def forward(self, x):
+        out = F.relu(self.bn1(self.conv1(x)))
+        return F.relu(self.bn2(self.conv2(out)) + x)
+
+
+def _graph_models(kind):
+    torch.manual_seed(310)
+    if kind == "mlp":
+        return [_MLP().to(DEV) for _ in range(6)], (4, 16), torch.float32
+    mods = []
+    for _ in range(3):
+        m = _Block(32)
+        with torch.no_grad():
+            for bn in (m.bn1, m.bn2):
+                bn.weight.normal_(1.0, 0.1)
+                bn.bias.normal_(0.0, 0.1)
+        mods.append(m.to(DEV, torch.bfloat16).eval())
+    return mods, (2, 32, 16, 16), torch.bfloat16
+
+
+@pytest.mark.parametrize("kind", ["mlp", "resblock"])
+def test_traced_graph_replay_matches_eager(hip, kind):
+    """use_graphs(): captured once per input layout, replayed for new input tensors with the
+    program's own eager work between replays; every replay equals the eager forward bit for bit,
+    a second layout gets its own graph, and the output buffer is reused (documented)."""
+    import wide_compiler as wc
+    models, shape, dtype = _graph_models(kind)
+    n = len(models)
+    sample = torch.randn(*shape, device=DEV).to(dtype)
+    eager = wc.compile(models, sample).eval()
+    graphed = wc.compile(models, sample).eval().use_graphs()
+    g = gen(311)
+    packed_shape = (shape[0], n * shape[1], *shape[2:])
+    outs = []
+    with torch.no_grad():
+        for i in range(4):
+            x = torch.randn(*packed_shape, generator=g).to(DEV, dtype)
+            ref = eager(x).clone()
+            got = graphed(x)
+            outs.append(got)
+            assert torch.equal(got, ref), (kind, i)
+            torch.cuda.synchronize()
+            (x * 2).sum().item()                        # eager work between replays
+        assert all(o.data_ptr() == outs[0].data_ptr() for o in outs)
+        x2 = torch.randn(2 * shape[0], *packed_shape[1:], generator=g).to(DEV, dtype)
+        assert torch.equal(graphed(x2), eager(x2))
+        assert len(graphed.__dict__["_graphs"]) == 2
+        x = torch.randn(*packed_shape, generator=g).to(DEV, dtype)
+        assert torch.equal(graphed(x), eager(x))       # the first layout's graph again
+    graphed.use_graphs(False)
+    with torch.no_grad():
+        assert torch.equal(graphed(x), eager(x))
