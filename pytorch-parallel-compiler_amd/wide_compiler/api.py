@@ -66,12 +66,10 @@ def compile(  # noqa: A001 - public name of the reference API
 
 
 def _compiled(wide: nn.Module, cfg: WideConfig) -> nn.Module:
-    """compile_model=True (api.py:137-147): mode "reduce-overhead" asks for CUDA graphs, which
-    torch.compile cannot take over these kernels' launches, so the model captures and replays
-    its own launches (TracedWideModel.use_graphs); other modes wrap it in torch.compile, which
-    leaves each kernel call as an opaque call between compiled regions."""
-    if cfg.compile_mode == "reduce-overhead":
-        return wide.use_graphs(True)
+    """compile_model=True (api.py:137-147): torch.compile around the model, which leaves each
+    kernel call as an opaque call between compiled regions.  (TracedWideModel.use_graphs() is the
+    explicit way to capture the kernels' own launches; measured on the c1 and c3 models it is
+    slower than direct dispatch, so no mode turns it on by itself.)"""
     return torch.compile(wide, mode=cfg.compile_mode, backend=cfg.compile_backend, **cfg.compile_options)
 
 

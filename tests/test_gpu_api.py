@@ -1,6 +1,6 @@
 """GPU checks of the drop-in API behaviour: compile_model=True (torch.compile around the wide
-model, reference api.py:138-147; mode "reduce-overhead" replays the model's own captured
-launches) in both modes, graph replay of a traced model, parameter writes through ``.data`` seen by
+model, reference api.py:138-147) in both modes, graph replay of a traced model
+(TracedWideModel.use_graphs), parameter writes through ``.data`` seen by
 the next forward (the reference reads its parameters on every call), a residual whose ReLU
 alias follows the conv it feeds, and WideBatchNorm1d (wide_batchnorm_1d.py:53-73) alone and
 folded into a traced Conv1d epilogue."""
@@ -207,33 +207,43 @@ def _graph_models(kind):
 
 @pytest.mark.parametrize("kind", ["mlp", "resblock"])
 def test_traced_graph_replay_matches_eager(hip, kind):
-    """use_graphs(): captured once per input layout, replayed for new input tensors with the
-    program's own eager work between replays; every replay equals the eager forward bit for bit,
-    a second layout gets its own graph, and the output buffer is reused (documented)."""
+    """use_graphs(): the second forward of one input buffer captures, later ones replay, with the
+    program's own eager work between replays; every call equals the eager forward bit for bit.
+    A second buffer layout gets its own graph, replays reuse one output buffer (documented), and
+    inputs at fresh addresses run directly (no capture, no copy)."""
     import wide_compiler as wc
     models, shape, dtype = _graph_models(kind)
     n = len(models)
     sample = torch.randn(*shape, device=DEV).to(dtype)
     eager = wc.compile(models, sample).eval()
     graphed = wc.compile(models, sample).eval().use_graphs()
+    graphs = graphed.__dict__["_graphs"]
     g = gen(311)
     packed_shape = (shape[0], n * shape[1], *shape[2:])
+    xbuf = torch.empty(packed_shape, device=DEV, dtype=dtype)
     outs = []
     with torch.no_grad():
-        for i in range(4):
-            x = torch.randn(*packed_shape, generator=g).to(DEV, dtype)
-            ref = eager(x).clone()
-            got = graphed(x)
+        for i in range(5):
+            xbuf.copy_(torch.randn(*packed_shape, generator=g).to(DEV, dtype))
+            ref = eager(xbuf).clone()
+            got = graphed(xbuf)
             outs.append(got)
             assert torch.equal(got, ref), (kind, i)
+            assert len(graphs) == (0 if i == 0 else 1)
             torch.cuda.synchronize()
-            (x * 2).sum().item()                        # eager work between replays
-        assert all(o.data_ptr() == outs[0].data_ptr() for o in outs)
-        x2 = torch.randn(2 * shape[0], *packed_shape[1:], generator=g).to(DEV, dtype)
-        assert torch.equal(graphed(x2), eager(x2))
-        assert len(graphed.__dict__["_graphs"]) == 2
-        x = torch.randn(*packed_shape, generator=g).to(DEV, dtype)
-        assert torch.equal(graphed(x), eager(x))       # the first layout's graph again
+            (xbuf * 2).sum().item()                     # eager work between replays
+        assert all(o.data_ptr() == outs[1].data_ptr() for o in outs[1:])
+        x2 = torch.empty((2 * shape[0], *packed_shape[1:]), device=DEV, dtype=dtype)
+        for _ in range(3):
+            x2.copy_(torch.randn(*x2.shape, generator=g).to(DEV, dtype))
+            assert torch.equal(graphed(x2), eager(x2))
+        assert len(graphs) == 2
+        for _ in range(3):                              # fresh tensors: direct launches only
+            x = torch.randn(*packed_shape, generator=g).to(DEV, dtype)
+            assert torch.equal(graphed(x), eager(x))
+        assert len(graphs) == 2
+        xbuf.copy_(torch.randn(*packed_shape, generator=g).to(DEV, dtype))
+        assert torch.equal(graphed(xbuf), eager(xbuf))  # the first buffer's graph again
     graphed.use_graphs(False)
     with torch.no_grad():
-        assert torch.equal(graphed(x), eager(x))
+        assert torch.equal(graphed(xbuf), eager(xbuf))
