@@ -68,8 +68,8 @@ def compile(  # noqa: A001 - public name of the reference API
 def _compiled(wide: nn.Module, cfg: WideConfig) -> nn.Module:
     """compile_model=True (api.py:137-147): torch.compile around the model, which leaves each
     kernel call as an opaque call between compiled regions.  (TracedWideModel.use_graphs() is the
-    explicit way to capture the kernels' own launches; measured on the c1 and c3 models it is
-    slower than direct dispatch, so no mode turns it on by itself.)"""
+    explicit way to capture the kernels' own launches; measured on a traced 100-model MLP and a
+    100-model ResBlock it is slower than direct dispatch, so no mode turns it on by itself.)"""
     return torch.compile(wide, mode=cfg.compile_mode, backend=cfg.compile_backend, **cfg.compile_options)
 
 

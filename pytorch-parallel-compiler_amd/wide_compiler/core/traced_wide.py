@@ -449,8 +449,8 @@ class TracedWideModel(nn.Module):
         kernels' launches from outside.  As in reduce-overhead mode, a replay returns the graph's
         output buffer, which the next replay overwrites (clone it to keep it).  A replay costs
         ~15-20 us of host time (torch.cuda.CUDAGraph.replay), so it pays off only for models that
-        run many launches; the fused c1 MLP (one launch) and c3 ResBlock (two) dispatch faster
-        directly (9.6 against 21.4 us, 153.7 against 158.5 us).  Parameters are
+        run many launches; a traced 100-model MLP (one fused launch) and 100-model ResBlock (two)
+        dispatch faster directly (9.6 against 21.4 us, 153.7 against 158.5 us).  Parameters are
         read by address, so in-place writes are seen by later replays; after replacing a
         parameter tensor or changing the model call ``use_graphs(True)`` again, which drops the
         captured graphs.  At most ``kMaxGraphs`` graphs are kept (the oldest is dropped)."""
