@@ -160,3 +160,25 @@ def test_residual_is_read_from_the_stage_that_computes_it():
         assert order[res] < order[conv]
     assert wide._residual_of == {"c2": "c1"}
     assert wide.stages["c1"].fused_activation == "relu"
+
+
+def test_self_attention_fusion_rules():
+    """WideAttention routes self-attention to the fused projection kernel only where it applies:
+    bf16, head dim 32, 1 <= S <= 512, D <= 768, no mask, 16-byte aligned rows (host logic only)."""
+    import torch
+    import wide_compiler as wc
+    w = wc.WideAttention(2, 64, 2).to(torch.bfloat16)
+    params = (w.q_weight, w.kv_weight, w.out_weight, w.q_bias, w.kv_bias, w.out_bias)
+    x = torch.zeros(2, 3, 40, 64, dtype=torch.bfloat16)
+    assert w._fusable(x, None, params)
+    assert not w._fusable(x, torch.zeros(40, 40, dtype=torch.bool), params)
+    assert not w._fusable(x.float(), None, params)
+    assert not w._fusable(torch.zeros(2, 3, 513, 64, dtype=torch.bfloat16), None, params)
+    assert not w._fusable(torch.zeros(2, 3, 0, 64, dtype=torch.bfloat16), None, params)
+    assert not w._fusable(torch.zeros(2, 3, 40, 66, dtype=torch.bfloat16)[..., :64], None, params)
+    assert w._fusable(torch.zeros(2, 3, 40, 72, dtype=torch.bfloat16)[..., 8:], None, params)
+    w.fuse_projections = False
+    assert not w._fusable(x, None, params)
+    w64 = wc.WideAttention(2, 128, 2).to(torch.bfloat16)          # head dim 64
+    assert not w64._fusable(torch.zeros(2, 3, 40, 128, dtype=torch.bfloat16), None,
+                            (w64.q_weight, w64.kv_weight, w64.out_weight, w64.q_bias, w64.kv_bias, w64.out_bias))
