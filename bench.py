@@ -155,24 +155,21 @@ def cfg_seq(dev, steps, warmup) -> Dict:
 
     def kernels():
         with torch.inference_mode():
-            x = wide.ln(wide.emb(ids, per_model=True))
+            x = wide.emb.forward_layernorm(ids, wide.ln, per_model=True)
             hs, _ = wide.lstm(x)
             lstm = wide.lstm
             a, ws = _hip.rnn_args(cell=_hip.CELL_LSTM, x=x, w_ih=lstm.weight_ih, w_hh=lstm.weight_hh,
                                   b_ih=lstm.bias_ih, b_hh=lstm.bias_hh, h0=None, c0=None, out=hs,
                                   h_n=None, c_n=None)
-            t_emb = _event_time(lambda: wide.emb(ids, per_model=True), 20, 2)
-            t_ln = _event_time(lambda: wide.ln(x), 20, 2)
+            t_emb = _event_time(lambda: wide.emb.forward_layernorm(ids, wide.ln, per_model=True), 20, 2)
             t_proj = _event_time(lambda: _hip.rnn_phase(a, "input_projection", x), 10, 2)
             t_rec = _event_time(lambda: _hip.rnn_phase(a, "recurrence", x), 10, 2)
             t_fc = _event_time(lambda: wide.fc.forward_into(hs, logits), 10, 2)
         rows = n * b * t
         g = 4 * hdim
         return [
-            _kernel("seg_copy_kernel<GatherMap> (per-model embedding gather, bf16)", "hbm", t_emb,
-                    byts=rows * (8 + 2 * d * 2)),
-            _kernel("layernorm_kernel (256-wide rows, bf16, fp32 statistics)", "hbm", t_ln,
-                    byts=2 * rows * d * 2 + 2 * n * d * 2),
+            _kernel("layernorm_vec_kernel<gather> (per-model embedding gather + LayerNorm, 256-wide rows, bf16, "
+                    "fp32 statistics)", "hbm", t_emb, byts=rows * (8 + 2 * d * 2) + 2 * n * d * 2),
             _kernel("LSTM input projection (part_prep_kernel + gemm_xl8_kernel, 256 -> 2048, bf16 out)",
                     "mfma", t_proj, flops=2.0 * rows * g * d, peak=PEAK["bf16_mfma"]),
             _kernel("lstm_part_kernel (LSTM recurrence, 128 steps, W_hh on-chip, 4 CUs per model)", "mfma",

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define WC_ABI_VERSION 3
+#define WC_ABI_VERSION 4
 
 /* element types */
 enum {
@@ -127,6 +127,25 @@ int32_t wc_layernorm(const void* x, int64_t x_model_stride, int64_t x_row_stride
                      void* y, int64_t y_model_stride, int64_t y_row_stride,
                      int64_t n, int64_t rows_per_model, int64_t dim, float eps,
                      int32_t dtype, int32_t param_dtype, void* stream);
+
+/*
+ * Embedding gather followed by LayerNorm, in one pass -- replaces WideEmbedding.forward
+ * (wide_compiler/core/primitives/wide_embedding.py:93-131) feeding WideLayerNorm.forward
+ * (wide_compiler/core/primitives/wide_layernorm.py:48-67) when the embedding's output goes
+ * only to the LayerNorm:
+ *   out[i, r, :] = LayerNorm_i(weight[i, id, :]),  id = ids[r] (ids_shared != 0, ids [rows])
+ *                                                  or ids[i*rows + r] (ids_shared == 0, ids [n, rows])
+ * weight contiguous [n, vocab, dim] of `dtype`; gamma, beta [n, dim] of `param_dtype` (beta may
+ * be NULL); out contiguous [n, rows, dim].  An id outside [0, vocab) normalises a zero row (the
+ * row wc_embedding_gather writes for it) and stores 1 into *err_flag when err_flag != NULL.
+ * The output equals wc_embedding_gather followed by wc_layernorm bit for bit.  Rows must be
+ * 16-byte vectors (dim a multiple of 16 / element size, at most 256 vectors) with 16-byte aligned
+ * weight, gamma, beta and out; otherwise WC_ERR_LIMIT and nothing is launched.
+ */
+int32_t wc_embedding_layernorm(const void* weight, int64_t n, int64_t vocab, int64_t dim,
+                               const int64_t* ids, int64_t rows, int32_t ids_shared,
+                               const void* gamma, const void* beta, float eps, int32_t dtype,
+                               int32_t param_dtype, void* out, int32_t* err_flag, void* stream);
 
 /*
  * Eval-mode BatchNorm per (model, channel) on N-first [n, b, c, hw] --

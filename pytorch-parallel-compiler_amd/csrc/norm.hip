@@ -165,11 +165,21 @@ __device__ __forceinline__ float group_reduce(float v) {
 // a wave keeps RPG x ITEMS x 1 KB in flight; gamma / beta are read once per
 // group as 16-byte vectors; two-pass statistics in fp32 registers; one
 // reciprocal square root per row.
-template <typename T, typename P, int L, int ITEMS, int RPG>
+// The embedding gather in front of the LayerNorm (GATHER): row r of model m reads table row
+// ids[r] (shared ids) or ids[m * rows + r] of model m (x = the table, xms its model stride); an
+// id outside [0, vocab) reads a zero row, as the gather kernel writes one, and sets *err.
+struct LnGather {
+  const int64_t* ids;
+  int64_t vocab;
+  int ids_shared;
+  int32_t* err;
+};
+
+template <typename T, typename P, int L, int ITEMS, int RPG, bool GATHER = false>
 __global__ __launch_bounds__(kNormBlock) void layernorm_vec_kernel(
     const T* __restrict__ x, int64_t xms, int64_t xrs, const P* __restrict__ gamma,
     const P* __restrict__ beta, T* __restrict__ y, int64_t yms, int64_t yrs, uint32_t rows_total,
-    FastDiv rows_per_model, int dim, float eps) {
+    FastDiv rows_per_model, int dim, float eps, LnGather gth) {
   constexpr int V = 16 / sizeof(T);
   const int tid = threadIdx.x;
   const int j = tid & (L - 1);
@@ -182,12 +192,29 @@ __global__ __launch_bounds__(kNormBlock) void layernorm_vec_kernel(
 
   float v[RPG][ITEMS][V];
 #pragma unroll
-  for (int r = 0; r < RPG; ++r)
+  for (int r = 0; r < RPG; ++r) {
+    const T* src = xr + static_cast<int64_t>(r) * xrs;
+    bool ok = true;
+    if constexpr (GATHER) {
+      const int64_t id = gth.ids[gth.ids_shared ? static_cast<int64_t>(r0 + r)
+                                                : static_cast<int64_t>(m) * rows_per_model.d + r0 + r];
+      ok = id >= 0 && id < gth.vocab;
+      src = x + static_cast<int64_t>(m) * xms + (ok ? id : 0) * dim;
+      if (!ok && j == 0 && gth.err) *gth.err = 1;
+    }
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int e = (it * L + j) * V;
-      if (e < dim) LoadV<T, V>::ld(xr + static_cast<int64_t>(r) * xrs + e, v[r][it]);
+      if (e < dim) {
+        if (ok) {
+          LoadV<T, V>::ld(src + e, v[r][it]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < V; ++q) v[r][it][q] = 0.f;
+        }
+      }
     }
+  }
   float gv[ITEMS][V], bv[ITEMS][V];
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it) {
@@ -293,7 +320,8 @@ int32_t launch_layernorm(const void* x, int64_t xms, int64_t xrs, const void* g,
     const int64_t groups = cdiv(rows_total, R);                                                       \
     const dim3 grid(static_cast<uint32_t>(cdiv(groups, kNormBlock / (L))));                          \
     layernorm_vec_kernel<T, P, L, IT, R><<<grid, kNormBlock, 0, st>>>(xt, xms, xrs, gt, bt, yt, yms, yrs, \
-                                                                      rows_total, fr, (int)dim, eps);  \
+                                                                      rows_total, fr, (int)dim, eps,   \
+                                                                      LnGather{});                    \
     return check_launch("wc_layernorm");                                                              \
   }
 #define WC_LNV_R(L, IT) WC_LNV(L, IT, 4) WC_LNV(L, IT, 2) WC_LNV(L, IT, 1)
@@ -309,6 +337,48 @@ int32_t launch_layernorm(const void* x, int64_t xms, int64_t xrs, const void* g,
   return launch_layernorm_v<T, P, 1>(static_cast<const T*>(x), xms, xrs, static_cast<const P*>(g),
                                      static_cast<const P*>(b), static_cast<T*>(y), yms, yrs, n, rpm,
                                      (int)dim, eps, st);
+}
+
+// Embedding gather + LayerNorm in one pass: the vector-path LayerNorm kernel reading its rows
+// through the ids, with the shape selection of launch_layernorm's vector path, so the output
+// equals wc_embedding_gather followed by wc_layernorm bit for bit.  WC_ERR_LIMIT (nothing
+// launched) where that path does not apply.
+template <typename T, typename P>
+int32_t launch_emb_layernorm(const void* w, int64_t n, int64_t vocab, int64_t dim, const int64_t* ids,
+                             int64_t rows, int ids_shared, const void* g, const void* b, float eps, void* y,
+                             int32_t* err, hipStream_t st) {
+  constexpr int VMAX = 16 / sizeof(T);
+  const int es = sizeof(T);
+  const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(w), reinterpret_cast<uintptr_t>(y),
+                                   reinterpret_cast<uintptr_t>(g), reinterpret_cast<uintptr_t>(b),
+                                   static_cast<uint64_t>(dim * es), static_cast<uint64_t>(dim * sizeof(P))});
+  if (!(vb >= 16 && dim % VMAX == 0 && dim <= 4 * 64 * VMAX))
+    return set_error(WC_ERR_LIMIT, "wc_embedding_layernorm: dim %lld or alignment outside the fused kernel "
+                     "(16-byte rows, dim a multiple of %d up to %d)", static_cast<long long>(dim), VMAX,
+                     4 * 64 * VMAX);
+  const int64_t nvec = dim / VMAX;
+  const uint32_t rows_total = static_cast<uint32_t>(n * rows);
+  const FastDiv fr = make_fastdiv(static_cast<uint32_t>(rows));
+  const int rpg = (rows % 4 == 0) ? 4 : ((rows % 2 == 0) ? 2 : 1);
+  const T* wt = static_cast<const T*>(w);
+  const P* gt = static_cast<const P*>(g);
+  const P* bt = static_cast<const P*>(b);
+  T* yt = static_cast<T*>(y);
+  const LnGather gth{ids, vocab, ids_shared, err};
+#define WC_ELN(L, IT, R)                                                                                \
+  if (nvec <= (L) * (IT) && rpg == (R)) {                                                             \
+    const int64_t groups = cdiv(rows_total, R);                                                      \
+    const dim3 grid(static_cast<uint32_t>(cdiv(groups, kNormBlock / (L))));                         \
+    layernorm_vec_kernel<T, P, L, IT, R, true><<<grid, kNormBlock, 0, st>>>(                         \
+        wt, vocab * dim, 0, gt, bt, yt, rows * dim, dim, rows_total, fr, (int)dim, eps, gth);       \
+    return check_launch("wc_embedding_layernorm");                                                  \
+  }
+#define WC_ELN_R(L, IT) WC_ELN(L, IT, 4) WC_ELN(L, IT, 2) WC_ELN(L, IT, 1)
+  WC_ELN_R(4, 1) WC_ELN_R(8, 1) WC_ELN_R(16, 1) WC_ELN_R(32, 1) WC_ELN_R(64, 1)
+  WC_ELN_R(64, 2) WC_ELN_R(64, 4)
+#undef WC_ELN_R
+#undef WC_ELN
+  return set_error(WC_ERR_LIMIT, "wc_embedding_layernorm: dim %lld too large", static_cast<long long>(dim));
 }
 
 template <typename T, typename P>
@@ -552,6 +622,35 @@ extern "C" int32_t wc_layernorm(const void* x, int64_t x_model_stride, int64_t x
     return launch_layernorm<f16, f16>(x, x_model_stride, x_row_stride, gamma, beta, y,
                                       y_model_stride, y_row_stride, n, rows_per_model, dim, eps, st);
   return set_error(WC_ERR_DTYPE, "wc_layernorm: unsupported dtype pair (%s, %s)", dtype_name(dtype),
+                   dtype_name(param_dtype));
+}
+
+extern "C" int32_t wc_embedding_layernorm(const void* weight, int64_t n, int64_t vocab, int64_t dim,
+                                          const int64_t* ids, int64_t rows, int32_t ids_shared,
+                                          const void* gamma, const void* beta, float eps, int32_t dtype,
+                                          int32_t param_dtype, void* out, int32_t* err_flag, void* stream) {
+  clear_error();
+  WC_REQUIRE(n >= 0 && vocab >= 0 && dim >= 0 && rows >= 0, WC_ERR_SHAPE,
+             "wc_embedding_layernorm: negative size");
+  if (n == 0 || rows == 0 || dim == 0) return WC_OK;
+  WC_REQUIRE(weight && ids && gamma && out, WC_ERR_NULL, "wc_embedding_layernorm: null pointer");
+  WC_REQUIRE(rows < 0x7fffffffll && n * rows < 0x7fffffffll, WC_ERR_LIMIT,
+             "wc_embedding_layernorm: too many rows");
+  hipStream_t st = as_stream(stream);
+  const int shared = ids_shared ? 1 : 0;
+  if (dtype == WC_F32 && param_dtype == WC_F32)
+    return launch_emb_layernorm<float, float>(weight, n, vocab, dim, ids, rows, shared, gamma, beta, eps, out,
+                                              err_flag, st);
+  if (dtype == WC_BF16 && param_dtype == WC_BF16)
+    return launch_emb_layernorm<bf16, bf16>(weight, n, vocab, dim, ids, rows, shared, gamma, beta, eps, out,
+                                            err_flag, st);
+  if (dtype == WC_BF16 && param_dtype == WC_F32)
+    return launch_emb_layernorm<bf16, float>(weight, n, vocab, dim, ids, rows, shared, gamma, beta, eps, out,
+                                             err_flag, st);
+  if (dtype == WC_F16 && param_dtype == WC_F16)
+    return launch_emb_layernorm<f16, f16>(weight, n, vocab, dim, ids, rows, shared, gamma, beta, eps, out,
+                                          err_flag, st);
+  return set_error(WC_ERR_DTYPE, "wc_embedding_layernorm: unsupported dtype pair (%s, %s)", dtype_name(dtype),
                    dtype_name(param_dtype));
 }
 

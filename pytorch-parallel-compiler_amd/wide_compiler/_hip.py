@@ -23,11 +23,12 @@ from typing import Dict, List, Optional, Sequence
 import torch
 from torch import Tensor
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, BF16, F16 = 0, 1, 2
 ACT_NONE, ACT_RELU = 0, 1
 CELL_GRU, CELL_LSTM = 0, 1
+ERR_LIMIT = -5                  # WC_ERR_LIMIT: a size or layout the kernel does not take
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -163,6 +164,7 @@ SIGNATURES = {
     "wc_swap01": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "wc_embedding_gather": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _I64, _I32, _P, _P, _P]),
     "wc_layernorm": (_I32, [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I32, _I32, _P]),
+    "wc_embedding_layernorm": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I32, _P, _P, _F, _I32, _I32, _P, _P, _P]),
     "wc_bn_eval": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _P]),
     "wc_group_norm": (_I32, [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _F, _I32, _I32, _I32, _P]),
     "wc_rnn_workspace_bytes": (_I64, [ctypes.POINTER(_RnnArgs)]),
@@ -283,6 +285,22 @@ def embedding_gather(weight: Tensor, ids: Tensor, out: Tensor, shared: bool,
     _check(lib().wc_embedding_gather(weight.data_ptr(), n, vocab, dim, dtype_code(weight.dtype, "embedding"),
                                      ids.data_ptr(), rows, 1 if shared else 0, out.data_ptr(),
                                      ptr(err_flag), stream_of(weight)), "wc_embedding_gather")
+
+
+def embedding_layernorm(weight: Tensor, ids: Tensor, gamma: Tensor, beta: Optional[Tensor], eps: float,
+                        out: Tensor, shared: bool, err_flag: Optional[Tensor] = None) -> bool:
+    """Gather + LayerNorm in one launch (wc_embedding_layernorm); False (nothing launched) where
+    the fused kernel does not take the row size or alignment."""
+    n, vocab, dim = weight.shape
+    rows = ids.numel() if shared else ids.numel() // max(n, 1)
+    rc = lib().wc_embedding_layernorm(weight.data_ptr(), n, vocab, dim, ids.data_ptr(), rows, 1 if shared else 0,
+                                      gamma.data_ptr(), ptr(beta), float(eps), dtype_code(weight.dtype, "embedding"),
+                                      dtype_code(gamma.dtype, "layernorm"), out.data_ptr(), ptr(err_flag),
+                                      stream_of(weight))
+    if rc == ERR_LIMIT:
+        return False
+    _check(rc, "wc_embedding_layernorm")
+    return True
 
 
 def layernorm(x: Tensor, x_ms: int, x_rs: int, gamma: Tensor, beta: Optional[Tensor], y: Tensor,
@@ -593,7 +611,7 @@ def exported_symbols() -> List[str]:
 # but ends the compiled region there and runs the call as is, so inductor never generates
 # code for the hot path.
 for _name in ("pack_rows", "swap01", "embedding_gather", "layernorm", "bn_eval", "group_norm", "grouped_gemm",
-              "mlp2", "mlp2_args", "mlp2_launch", "rnn_forward", "rnn_forward_noalloc", "rnn_phase", "conv_pack_weights", "conv2d", "conv3d",
+              "mlp2", "mlp2_args", "mlp2_launch", "embedding_layernorm", "rnn_forward", "rnn_forward_noalloc", "rnn_phase", "conv_pack_weights", "conv2d", "conv3d",
               "attention", "self_attention", "rnn_sync_check"):
     globals()[_name] = torch.compiler.disable(globals()[_name])
 del _name

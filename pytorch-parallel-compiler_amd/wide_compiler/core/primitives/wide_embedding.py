@@ -80,6 +80,35 @@ class WideEmbedding(nn.Module):
                 self.index_error()
         return out
 
+    def forward_layernorm(self, x: Tensor, ln: "WideLayerNorm", per_model: bool = False) -> Tensor:
+        """``ln(self(x, per_model))`` with the LayerNorm applied while the rows are gathered (one
+        launch, the gathered rows never written): the same values bit for bit, and the same
+        out-of-range id behaviour (a zero row is normalised and the flag is set).  Shapes or
+        alignments the fused kernel does not take run the two launches."""
+        what = "WideEmbedding"
+        w = self.weight
+        d = self.embedding_dim
+        if ln.n != self.n or ln.normalized_shape != d:
+            raise RuntimeError(f"{what}: LayerNorm {ln} does not match {self}")
+        _hip.require_device(what, x, w, ln.weight, ln.bias)
+        _hip.require_forward_only(what, w, ln.weight, ln.bias)
+        if x.dtype not in (torch.int64, torch.int32, torch.int16, torch.int8, torch.uint8):
+            raise IndexError(f"{what}: indices must be an integer tensor, got {x.dtype}")
+        if per_model and (x.dim() < 1 or x.shape[0] != self.n):
+            raise RuntimeError(f"{what}: per-model ids must be [N={self.n}, ...], got {list(x.shape)}")
+        ids = x.to(torch.int64).contiguous()
+        w = w if w.is_contiguous() else w.contiguous()
+        shape = (*x.shape, d) if per_model else (self.n, *x.shape, d)
+        out = torch.empty(shape, dtype=w.dtype, device=w.device)
+        if out.numel() == 0:
+            return out
+        if not _hip.embedding_layernorm(w, ids, ln.weight, ln.bias, ln.eps, out, shared=not per_model,
+                                        err_flag=self._flag(w.device)):
+            return ln(self.forward(x, per_model=per_model))
+        if self.strict_ids and not torch.cuda.is_current_stream_capturing():
+            self.index_error()
+        return out
+
     def index_error(self) -> None:
         """Raise IndexError if any lookup since the last call used an out-of-range id."""
         if self._err is not None and int(self._err.item()) != 0:

@@ -144,7 +144,8 @@ class SeqModel(nn.Module):
 
 class WideSeqModel(nn.Module):
     """N SeqModels fused primitive by primitive: per-model embedding gather (each model reads
-    its own ids), N-first LayerNorm, WideLSTM, WideLinear over the vocabulary.  The wide
+    its own ids) with the N-first LayerNorm applied as the rows are gathered, WideLSTM,
+    WideLinear over the vocabulary.  The wide
     primitives are the reference's (wide_embedding.py, wide_layernorm.py, wide_lstm.py,
     wide_linear.py); the composition is not traced because the LSTM returns a tuple."""
 
@@ -159,7 +160,7 @@ class WideSeqModel(nn.Module):
 
     def forward(self, ids: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """ids [N, B, T] (model i uses row i) -> logits [N, B, T, V]."""
-        x = self.ln(self.emb(ids, per_model=True))
+        x = self.emb.forward_layernorm(ids, self.ln, per_model=True)   # = self.ln(self.emb(ids, ...))
         h, _ = self.lstm(x)
         return self.fc.forward_into(h, out)
 

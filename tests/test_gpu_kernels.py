@@ -91,6 +91,47 @@ def test_embedding_per_model_bit_exact_and_oob_flag(hip):
         wide.index_error()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,vocab,d,ids_shape,per_model", [(4, 50, 256, (4, 3, 9), True), (3, 40, 64, (5, 7), False),
+                                                           (2, 30, 32, (2, 6), True), (5, 33, 48, (5, 3, 5), True),
+                                                           (2, 17, 1024, (2, 4), True), (3, 20, 36, (3, 2), True)])
+def test_embedding_layernorm_fused_bit_exact(hip, dtype, n, vocab, d, ids_shape, per_model):
+    """forward_layernorm (gather + LayerNorm in one launch) equals the gather followed by the
+    LayerNorm bit for bit, against the oracle within the dtype's bar, shared and per-model ids,
+    with an out-of-range id (a normalised zero row, the flag set).  Row sizes the fused kernel does
+    not take (36 16-bit elements: 72-byte rows) run the two launches."""
+    import wide_compiler as wc
+    g = gen(107)
+    emb = wc.WideEmbedding(n, vocab, d).to(DEV, dtype)
+    ln = wc.WideLayerNorm(n, d).to(DEV, dtype)
+    with torch.no_grad():
+        ln.weight.copy_(torch.randn(n * d, generator=g))
+        ln.bias.copy_(torch.randn(n * d, generator=g))
+    ids = torch.randint(0, vocab, ids_shape, generator=g)
+    with torch.no_grad():
+        fused = emb.forward_layernorm(ids.to(DEV), ln, per_model=per_model).cpu()
+        two = ln(emb(ids.to(DEV), per_model=per_model)).cpu()
+    assert torch.equal(fused, two)
+    w = emb.weight.detach().cpu()
+    gathered = (torch.stack([w[k][ids[k]] for k in range(n)]) if per_model
+                else wide_ref.embedding(w, ids))
+    exact = wide_ref.layernorm(gathered.double(), ln.weight.detach().cpu().double(),
+                               ln.bias.detach().cpu().double(), n, ln.eps)
+    assert rel_err(fused, exact) <= (TOL_F32 if dtype == torch.float32 else TOL_BF16)
+    emb.index_error()
+    bad = ids.clone()
+    bad.view(-1)[3] = vocab
+    with torch.no_grad():
+        fused = emb.forward_layernorm(bad.to(DEV), ln, per_model=per_model).cpu()
+    with pytest.raises(IndexError):
+        emb.index_error()
+    with torch.no_grad():
+        two = ln(emb(bad.to(DEV), per_model=per_model)).cpu()
+    assert torch.equal(fused, two)
+    with pytest.raises(IndexError):
+        emb.index_error()
+
+
 # ----------------------------------------------------------------------------- norms
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("shape", [(4, 3, 5, 256), (2, 7, 96), (3, 2, 1000), (64, 16, 8, 256)])
