@@ -1,7 +1,9 @@
 // Two chained per-model Linear layers in one launch:
 //   h[i][m] = act1( x[i][m] W1[i]^T + b1[i] )        (kept in LDS, never in HBM)
 //   y[i][m] = act2( h[i][m] W2[i]^T + b2[i] )
-// A workgroup (4 waves) owns 32 rows of one model.  x rows, W1, W2 and h live in LDS
+// A workgroup (4 waves) owns 32 rows of one model, or 16 when 32-row workgroups would
+// leave compute units idle (few models and rows): then all four waves share one 16-row
+// block and split its column tiles four ways instead of two.  x rows, W1, W2 and h live in LDS
 // as rows of 16-byte chunks, chunk q of row r stored at position q ^ (r & sw) (sw + 1
 // a power of two dividing the row's chunk count), so the 16-byte fragment reads of
 // consecutive rows hit distinct banks.  x, W1 and W2 are staged with LDS-DMA loads
@@ -19,7 +21,7 @@
 namespace wc {
 namespace {
 
-constexpr int kMlpRows = 32;                     // rows per workgroup
+constexpr int kMlpRows = 32;                     // rows per workgroup (at most)
 constexpr int kMlpThreads = 256;
 constexpr int kMlpMaxColBlocks = 16;             // hidden, out <= 256 (16-column blocks)
 
@@ -42,8 +44,8 @@ struct MlpParams {
   int row_blocks;
 };
 
-inline size_t mlp_lds_bytes(int es, int in, int hid, int out) {
-  return static_cast<size_t>(es) * (static_cast<size_t>(kMlpRows + hid) * in + static_cast<size_t>(kMlpRows + out) * hid);
+inline size_t mlp_lds_bytes(int es, int in, int hid, int out, int rows = kMlpRows) {
+  return static_cast<size_t>(es) * (static_cast<size_t>(rows + hid) * in + static_cast<size_t>(rows + out) * hid);
 }
 
 // Largest power of two <= 16 dividing n, minus one (n a multiple of 8).
@@ -140,30 +142,59 @@ __device__ __forceinline__ void mlp_pair(const char* a, const char* b, int n, in
   }
 }
 
+// One 16x16 tile A[ra..ra+15] x B[rb..rb+15]^T over K = k: the column block left over
+// when a wave's share of a layer's column blocks is odd.
 template <typename T>
+__device__ __forceinline__ void mlp_one(const char* a, const char* b, int n, int sw, int k, int ra, int rb,
+                                        f32x4& acc) {
+  acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  MlpFrag<T> fa = mlp_frag<T>(a, n, sw, ra, 0);
+  MlpFrag<T> fb = mlp_frag<T>(b, n, sw, rb, 0);
+  for (int k0 = 0; k0 < k; k0 += 32) {
+    const int kn = min(k0 + 32, k - 32);
+    const MlpFrag<T> na = mlp_frag<T>(a, n, sw, ra, kn);
+    const MlpFrag<T> nb = mlp_frag<T>(b, n, sw, rb, kn);
+    acc = mlp_mma<T>(fa, fb, acc);
+    fa = na;
+    fb = nb;
+  }
+}
+
+// ROWS = 32: waves 0/1 and 2/3 take the two 16-row blocks, each pair splitting the column
+// blocks two ways; ROWS = 16: the four waves split the one row block's column blocks.
+template <typename T, int ROWS>
 __global__ __launch_bounds__(kMlpThreads) void mlp2_kernel(MlpParams p) {
+  static_assert(ROWS == 16 || ROWS == 32, "16 or 32 rows per workgroup");
+  constexpr int RB = ROWS / 16;                  // row blocks per workgroup
+  constexpr int CW = 4 / RB;                     // waves splitting a row block's column blocks
   constexpr int VE = 16 / sizeof(T);             // elements per 16-byte chunk
   extern __shared__ __attribute__((aligned(16))) char mlp_smem[];
-  char* xs = mlp_smem;                                          // [32][nin] chunks
-  char* w1s = xs + kMlpRows * p.nin * 16;                       // [hid][nin]
-  char* hs = w1s + p.hid * p.nin * 16;                          // [32][nhid]
-  char* w2s = hs + kMlpRows * p.nhid * 16;                      // [out][nhid]
+  char* xs = mlp_smem;                                          // [ROWS][nin] chunks
+  char* w1s = xs + ROWS * p.nin * 16;                           // [hid][nin]
+  char* hs = w1s + p.hid * p.nin * 16;                          // [ROWS][nhid]
+  char* w2s = hs + ROWS * p.nhid * 16;                          // [out][nhid]
 
-  const int mdl = blockIdx.x / p.row_blocks;
-  const int m0 = (blockIdx.x - mdl * p.row_blocks) * kMlpRows;
+  // Dispatch deals workgroups to the 8 XCDs in turn. With a grid of a multiple of 8, slot
+  // b runs logical block (b % 8) * (grid / 8) + b / 8, so a model's consecutive row blocks
+  // share one XCD's L2 and its weights are read from HBM once.
+  int blk = static_cast<int>(blockIdx.x);
+  if ((gridDim.x & 7) == 0) blk = (blk & 7) * static_cast<int>(gridDim.x >> 3) + (blk >> 3);
+  const int mdl = blk / p.row_blocks;
+  const int m0 = (blk - mdl * p.row_blocks) * ROWS;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int fr = lane & 15, rq = (lane >> 4) * 4;
-  const int rbk = (wave & 1) * 16;               // the wave's 16-row block
+  const int rbk = (wave % RB) * 16;              // the wave's 16-row block
+  const int cg = wave / RB;                      // its column blocks: cg + CW i
   const int cb1 = p.hid / 16, cb2 = p.out / 16;  // column blocks per layer
 
-  // biases of the lane's columns (block j = (wave >> 1) + 2 i), read ahead of the staging
+  // biases of the lane's columns (block j = cg + CW i), read ahead of the staging
   float b1v[kMlpMaxColBlocks / 2], b2v[kMlpMaxColBlocks / 2];
   {
     const T* b1 = static_cast<const T*>(p.b1);
     const T* b2 = static_cast<const T*>(p.b2);
 #pragma unroll
     for (int i = 0; i < kMlpMaxColBlocks / 2; ++i) {
-      const int j = (wave >> 1) + 2 * i;
+      const int j = cg + CW * i;
       b1v[i] = b1 ? to_f32(b1[static_cast<int64_t>(mdl) * p.hid + min(j, cb1 - 1) * 16 + fr]) : 0.f;
       b2v[i] = b2 ? to_f32(b2[static_cast<int64_t>(mdl) * p.out + min(j, cb2 - 1) * 16 + fr]) : 0.f;
     }
@@ -175,7 +206,7 @@ __global__ __launch_bounds__(kMlpThreads) void mlp2_kernel(MlpParams p) {
     const char* w1b = static_cast<const char*>(p.w1) + static_cast<int64_t>(mdl) * p.hid * p.in * sizeof(T);
     const char* w2b = static_cast<const char*>(p.w2) + static_cast<int64_t>(mdl) * p.out * p.hid * sizeof(T);
     const int last = p.m - 1;
-    mlp_dma(xs, kMlpRows, p.nin, p.nin_d, p.sw_in, [&](int r) {
+    mlp_dma(xs, ROWS, p.nin, p.nin_d, p.sw_in, [&](int r) {
       const uint32_t gm = static_cast<uint32_t>(min(m0 + r, last));
       const uint32_t outer = fdiv(gm, p.x_ri);
       const uint32_t inner = gm - outer * p.x_ri.d;
@@ -191,13 +222,17 @@ __global__ __launch_bounds__(kMlpThreads) void mlp2_kernel(MlpParams p) {
   // ---- h = act1(x W1^T + b1) -> LDS (element type) ----
 #pragma unroll
   for (int i = 0; i < kMlpMaxColBlocks / 2; i += 2) {
-    if (2 * i >= cb1 - (wave >> 1)) break;
-    const int j0 = (wave >> 1) + 2 * i, j1 = min(j0 + 2, cb1 - 1);
+    const int j0 = cg + CW * i, j1 = j0 + CW;
+    if (j0 >= cb1) break;
+    const bool two = j1 < cb1;
     f32x4 acc[2];
-    mlp_pair<T>(xs, w1s, p.nin, p.sw_in, p.in, rbk + fr, j0 * 16 + fr, j1 * 16 + fr, acc[0], acc[1]);
+    if (two)
+      mlp_pair<T>(xs, w1s, p.nin, p.sw_in, p.in, rbk + fr, j0 * 16 + fr, j1 * 16 + fr, acc[0], acc[1]);
+    else
+      mlp_one<T>(xs, w1s, p.nin, p.sw_in, p.in, rbk + fr, j0 * 16 + fr, acc[0]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      if (u == 1 && j0 + 2 >= cb1) break;
+      if (u == 1 && !two) break;
       const int col = (u ? j1 : j0) * 16 + fr;
       const float bv = b1v[i + u];
 #pragma unroll
@@ -229,13 +264,17 @@ __global__ __launch_bounds__(kMlpThreads) void mlp2_kernel(MlpParams p) {
   }
 #pragma unroll
   for (int i = 0; i < kMlpMaxColBlocks / 2; i += 2) {
-    if (2 * i >= cb2 - (wave >> 1)) break;
-    const int j0 = (wave >> 1) + 2 * i, j1 = min(j0 + 2, cb2 - 1);
+    const int j0 = cg + CW * i, j1 = j0 + CW;
+    if (j0 >= cb2) break;
+    const bool two = j1 < cb2;
     f32x4 acc[2];
-    mlp_pair<T>(hs, w2s, p.nhid, p.sw_hid, p.hid, rbk + fr, j0 * 16 + fr, j1 * 16 + fr, acc[0], acc[1]);
+    if (two)
+      mlp_pair<T>(hs, w2s, p.nhid, p.sw_hid, p.hid, rbk + fr, j0 * 16 + fr, j1 * 16 + fr, acc[0], acc[1]);
+    else
+      mlp_one<T>(hs, w2s, p.nhid, p.sw_hid, p.hid, rbk + fr, j0 * 16 + fr, acc[0]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      if (u == 1 && j0 + 2 >= cb2) break;
+      if (u == 1 && !two) break;
       const int col = (u ? j1 : j0) * 16 + fr;
       const float bv = b2v[i + u];
 #pragma unroll
@@ -312,22 +351,35 @@ extern "C" int32_t wc_mlp2(const wc_mlp2_args* a, void* stream) {
   p.y_so = a->y_stride_outer;
   p.y_si = a->y_stride_inner;
   p.y_ri = make_fastdiv(static_cast<uint32_t>(a->y_rows_inner));
-  p.row_blocks = static_cast<int>(cdiv(p.m, kMlpRows));
+  // 16-row workgroups when 32-row ones would not cover the compute units
+  const int cus = device_cu_count();
+  const int rows = static_cast<int64_t>(p.n) * cdiv(p.m, kMlpRows) < cus ? 16 : kMlpRows;
+  p.row_blocks = static_cast<int>(cdiv(p.m, rows));
   const int64_t blocks = static_cast<int64_t>(p.n) * p.row_blocks;
   WC_REQUIRE(blocks < 0x7fffffffll, WC_ERR_LIMIT, "wc_mlp2: too many blocks");
   hipStream_t st = as_stream(stream);
   const bool f32 = a->dtype == WC_F32;
-  const size_t lds = mlp_lds_bytes(es, p.in, p.hid, p.out);
-  auto kern = f32 ? reinterpret_cast<const void*>(mlp2_kernel<float>) : reinterpret_cast<const void*>(mlp2_kernel<bf16>);
+  const size_t lds = mlp_lds_bytes(es, p.in, p.hid, p.out, rows);
+  const void* kern = rows == 16 ? (f32 ? reinterpret_cast<const void*>(mlp2_kernel<float, 16>)
+                                       : reinterpret_cast<const void*>(mlp2_kernel<bf16, 16>))
+                                : (f32 ? reinterpret_cast<const void*>(mlp2_kernel<float, kMlpRows>)
+                                       : reinterpret_cast<const void*>(mlp2_kernel<bf16, kMlpRows>));
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess)
       return set_error(static_cast<int32_t>(e), "wc_mlp2: LDS of %zu bytes refused: %s", lds, hipGetErrorString(e));
   }
   const dim3 grid(static_cast<uint32_t>(blocks));
-  if (f32)
-    mlp2_kernel<float><<<grid, kMlpThreads, lds, st>>>(p);
-  else
-    mlp2_kernel<bf16><<<grid, kMlpThreads, lds, st>>>(p);
+  if (rows == 16) {
+    if (f32)
+      mlp2_kernel<float, 16><<<grid, kMlpThreads, lds, st>>>(p);
+    else
+      mlp2_kernel<bf16, 16><<<grid, kMlpThreads, lds, st>>>(p);
+  } else {
+    if (f32)
+      mlp2_kernel<float, kMlpRows><<<grid, kMlpThreads, lds, st>>>(p);
+    else
+      mlp2_kernel<bf16, kMlpRows><<<grid, kMlpThreads, lds, st>>>(p);
+  }
   return check_launch("wc_mlp2");
 }

@@ -538,6 +538,8 @@ class _MLPTap(_MLP):
     (4, 9, 20, 40, 12, True),         # sizes the fused kernel does not take: two launches
     (5, 100, 64, 96, 128, True),      # fp32: 24-chunk h rows (swizzle over 8), 4 row blocks
     (3, 40, 128, 192, 128, True),     # bf16: 12 hidden column blocks; fp32 exceeds LDS: two launches
+    (8, 1040, 64, 128, 48, True),     # 264 workgroups of 32 rows (the others run 16-row ones);
+                                      # 3 output column blocks: one wave's tile is unpaired
 ])
 def test_traced_linear_chain(hip, dtype, n, b, d_in, d_hidden, d_out, relu):
     """Linear -> [ReLU] -> Linear runs as one wc_mlp2 launch when the sizes allow it."""
