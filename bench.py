@@ -160,11 +160,12 @@ def cfg_seq(dev, steps, warmup) -> Dict:
             lstm = wide.lstm
             a, ws = _hip.rnn_args(cell=_hip.CELL_LSTM, x=x, w_ih=lstm.weight_ih, w_hh=lstm.weight_hh,
                                   b_ih=lstm.bias_ih, b_hh=lstm.bias_hh, h0=None, c0=None, out=hs,
-                                  h_n=None, c_n=None)
+                                  h_n=None, c_n=None, status=_hip.rnn_status_word(x.device))
             t_emb = _event_time(lambda: wide.emb.forward_layernorm(ids, wide.ln, per_model=True), 20, 2)
             t_proj = _event_time(lambda: _hip.rnn_phase(a, "input_projection", x), 10, 2)
             t_rec = _event_time(lambda: _hip.rnn_phase(a, "recurrence", x), 10, 2)
             t_fc = _event_time(lambda: wide.fc.forward_into(hs, logits), 10, 2)
+        _hip.rnn_sync_check(block=True)      # every timed recurrence ran to its end
         rows = n * b * t
         g = 4 * hdim
         return [
@@ -477,16 +478,22 @@ def _graph_of(step):
 def _run_config(cfg: Dict, steps: int, warmup: int, mode: str) -> Dict:
     """value / mode / parity / kernels of one configuration."""
     import torch
+    from wide_compiler import _hip
     n, b = cfg["n"], cfg["batch"]
     step = cfg["step"]
+    # rnn_sync_check(block=True) raises if a bounded wait of the partitioned LSTM gave up in
+    # any launch or graph replay since the last check (the status word collects them all)
     parity = cfg["parity"]()
+    _hip.rnn_sync_check(block=True)
     eager_s = _timed(step, steps, warmup)
+    _hip.rnn_sync_check(block=True)
     graph_s, graph = None, None
     if mode in ("graph", "best"):
         graph, same = _graph_of(step)
         if not same:
             raise RuntimeError("graph replay differs from the eager forward")
         graph_s = _timed(graph.replay, steps, warmup)
+        _hip.rnn_sync_check(block=True)
     if mode == "eager" or graph_s is None:
         wall, used = eager_s, "eager"
     elif mode == "graph":
@@ -570,6 +577,7 @@ def main() -> int:
         return 2
 
     import torch
+    from wide_compiler import _hip
 
     dev = torch.device("cuda", 0)
     if args.copy_calibration:
@@ -595,6 +603,7 @@ def main() -> int:
         flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
         cold = _step_times(run_step, args.steps, flush)
         del flush
+    _hip.rnn_sync_check(block=True)
     hot_med, cold_med = _median(hot), _median(cold)
 
     dom = dict(r["dominant"])

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define WC_ABI_VERSION 4
+#define WC_ABI_VERSION 5
 
 /* element types */
 enum {
@@ -204,6 +204,12 @@ typedef struct wc_rnn_args {
   void* workspace;           /* device scratch of >= wc_rnn_workspace_bytes(args) bytes,
                                 16-byte aligned; holds the fp32 input projection */
   int64_t workspace_bytes;
+  void* status;              /* optional caller-owned int32 device word: the partitioned
+                                LSTM sets it to 1 when a bounded cross-workgroup wait gives
+                                up, and the library never clears it (so it also collects
+                                the verdicts of graph replays until the caller reads and
+                                clears it).  NULL: the workspace's own status word
+                                (wc_rnn_status_offset), zeroed by every input projection. */
 } wc_rnn_args;
 
 /* Bytes of workspace wc_rnn_forward needs for these sizes on the current device.
@@ -218,6 +224,15 @@ int64_t wc_rnn_workspace_bytes(const wc_rnn_args* args);
  * it; the recurrence sets it to 1 if a cross-workgroup wait timed out, in which
  * case out / h_n / c_n are invalid. */
 int64_t wc_rnn_status_offset(const wc_rnn_args* args);
+
+/* Poll rounds after which a wait of the partitioned LSTM gives up, for launches made
+ * from now on (process-wide; a launch captured into a graph keeps the value it was
+ * captured with).  0 gives up at the first wait without polling, so every workgroup
+ * leaves at once and the status word is set; a negative value restores the default
+ * (2^21 rounds of >= ~0.5 us).  Returns the previous value.  No counterpart in the
+ * reference (its recurrence has no cross-workgroup waits): a test hook for the
+ * give-up path. */
+int32_t wc_rnn_set_spin_limit(int32_t polls);
 
 /* Runs wc_rnn_input_projection, then wc_rnn_recurrence. */
 int32_t wc_rnn_forward(const wc_rnn_args* args, void* stream);

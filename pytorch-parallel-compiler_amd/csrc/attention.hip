@@ -294,7 +294,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 //   S^T = K Q^T      lane l holds query l%32 and 16 of the block's 32 keys
 //                    (keys 8 (r/4) + 4 (l/32) + r%4 in register r)
 //   softmax          block max in-lane over 16 keys, then across the lane
-//                    halves with v_permlane32_swap (no LDS); the running max
+//                    halves through the lane crossbar; the running max
 //                    only moves when a block exceeds it by 2^8 (P <= 2^8 keeps
 //                    fp32 sums exact enough), so most blocks skip the rescale
 //   O^T += V^T P^T   P^T is the S^T register block itself: k-step j takes
@@ -305,21 +305,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 constexpr float kLazyRescale = 8.0f;
 constexpr bf16x2 kOnes2 = {bf16(1.0f), bf16(1.0f)};
 
-// (v of this lane, v of lane l ^ 32) via v_permlane32_swap on an opaque copy:
-// the compiler folds the intrinsic when both operands are the same value, so
-// the exchange is written out, with the wait states around the swap.
+// (v of this lane, v of lane l ^ 32) through the lane crossbar (ds_bpermute_b32).
+// The half-wave swap instruction (v_permlane32_swap) is not used: its 16-lane sibling
+// delivered a stale first word now and then in the conv epilogue, with the compiler's
+// wait states around it, and a stale softmax max or row sum would corrupt whole rows.
 __device__ __forceinline__ void half_swap(float v, float& mine, float& other) {
-  float a = v, b;
-  asm volatile(
-      "s_nop 1\n\t"
-      "v_mov_b32 %1, %0\n\t"
-      "s_nop 1\n\t"
-      "v_permlane32_swap_b32 %0, %1\n\t"
-      "s_nop 1"
-      : "+v"(a), "=&v"(b));
-  // a = {v[0:31], v[0:31]}, b = {v[32:63], v[32:63]}
   mine = v;
-  other = (threadIdx.x & 32) ? a : b;
+  other = __shfl_xor(v, 32, 64);
 }
 __device__ __forceinline__ float other_half_max(float v) {
   float m, o;

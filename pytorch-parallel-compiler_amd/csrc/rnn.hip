@@ -614,6 +614,8 @@ extern "C" int64_t wc_rnn_status_offset(const wc_rnn_args* a) {
   return part_plan(a) ? part_status_offset(a) : -1;
 }
 
+extern "C" int32_t wc_rnn_set_spin_limit(int32_t polls) { return part_set_spin_limit(polls); }
+
 static int32_t rnn_check(const wc_rnn_args* a, const char* what, RnnParams& p, int& gates) {
   WC_REQUIRE(a != nullptr, WC_ERR_NULL, "%s: null args", what);
   WC_REQUIRE(a->cell == WC_CELL_GRU || a->cell == WC_CELL_LSTM, WC_ERR_ARG, "%s: unknown cell %d", what,
@@ -636,6 +638,7 @@ static int32_t rnn_check(const wc_rnn_args* a, const char* what, RnnParams& p, i
   WC_REQUIRE(a->workspace_bytes >= rnn_ws_bytes(a), WC_ERR_ARG, "%s: workspace of %lld bytes < %lld needed",
              what, (long long)a->workspace_bytes, (long long)rnn_ws_bytes(a));
   WC_REQUIRE(aligned(a->workspace, 16), WC_ERR_ALIGN, "%s: workspace not 16-byte aligned", what);
+  WC_REQUIRE(aligned(a->status, 4), WC_ERR_ALIGN, "%s: status word not 4-byte aligned", what);
   return WC_OK;
 }
 

@@ -33,10 +33,14 @@
 // `base` lives in the caller's workspace: the input projection zeroes it and fills
 // the slots with tag 0xFFFF, and the last workgroup of a model to finish advances it
 // by T, so a slot's stale tag is always 1 or 2 steps behind the one a reader expects.
-// Every wait is bounded: past the limit the workgroup records 1 in the status word
-// and leaves (the outputs are then invalid).  The host launches the grid
-// cooperatively, so all workgroups are co-resident or the launch fails.
+// Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
+// at the first wait without polling) the workgroup records 1 in the status word
+// and leaves (the outputs are then invalid).  The status word is the caller's own
+// when one is passed (never cleared here), else a word of the workspace that the
+// input projection zeroes.  The host launches the grid cooperatively, so all
+// workgroups are co-resident or the launch fails.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -51,12 +55,13 @@ constexpr int kSyncInts = 32;          // one 128-byte block per model:
 constexpr int kSyncDone = 16;          //   finished-parts counter
 constexpr int kSyncBase = 17;          //   tag of this launch's step 0
 constexpr int kSyncXcc = 20;           //   per part: (tag of step 0 << 16) | (XCD + 1)
-constexpr int kSpinLimit = 1 << 21;    // poll rounds (each >= ~0.5 us) before giving up
+constexpr int kSpinLimit = 1 << 21;    // default poll rounds (each >= ~0.5 us) before giving up
 constexpr int kSc1 = 16;               // buffer-op cache policy: device scope (sc1)
 constexpr uint32_t kTagFill = 0xFFFFu;
 
 struct PartParams {
   int n, batch, steps, remap;
+  int spin_limit;     // poll rounds of a wait before it gives up (0: at once)
   const bf16* gx;     // [n, batch, steps, 4H]: x W_ih^T + b_ih + b_hh, rounded to bf16
   const bf16* w_hh;   // [n, 4H, H]
   const bf16* h0;     // [n, batch, H] or null
@@ -66,8 +71,10 @@ struct PartParams {
   bf16* cn;           // [n, batch, H] or null
   uint32_t* xch;      // [n][2][16][H] exchange words
   int* sync;          // [n][kSyncInts]
-  int* status;        // set to 1 when a wait timed out
+  int* status;        // set to 1 when a wait gave up
 };
+
+std::atomic<int> g_spin_limit{kSpinLimit};
 
 // Where the (k-step s, row tile j) fragments of W_hh live: s < SL in LDS, s < SL + NA in
 // AGPRs, tiles j < XL of k-step SL + NA in LDS as well, the rest in VGPRs.
@@ -278,12 +285,12 @@ void lstm_part_kernel(PartParams p) {
       if (lane < P) {
         int spins = 0;
         while (true) {
-          got = static_cast<uint32_t>(sync_load(my_sync + kSyncXcc + lane));
-          if ((got >> 16) == tag0 && (got & 0xFFFFu) != 0) break;
-          if (++spins > kSpinLimit) {
+          if (spins++ >= p.spin_limit) {
             ok = false;
             break;
           }
+          got = static_cast<uint32_t>(sync_load(my_sync + kSyncXcc + lane));
+          if ((got >> 16) == tag0 && (got & 0xFFFFu) != 0) break;
           __builtin_amdgcn_s_sleep(1);
         }
       }
@@ -338,6 +345,10 @@ void lstm_part_kernel(PartParams p) {
       }
       int spins = 0;
       while (pending) {
+        if (spins++ >= p.spin_limit) {
+          *abort_flag = 1;
+          break;
+        }
         asm volatile("" ::: "memory");   // every round issues its loads anew
         u32x4 v[PG];
 #pragma unroll
@@ -360,13 +371,7 @@ void lstm_part_kernel(PartParams p) {
             pending &= ~(1u << k);
           }
         }
-        if (pending) {
-          if (++spins > kSpinLimit) {
-            *abort_flag = 1;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-        }
+        if (pending) __builtin_amdgcn_s_sleep(1);
       }
     }
   };
@@ -509,7 +514,8 @@ int32_t launch_part(const wc_rnn_args* a, hipStream_t st) {
   p.cn = static_cast<bf16*>(a->c_n);
   p.xch = reinterpret_cast<uint32_t*>(ws + l.xch);
   p.sync = reinterpret_cast<int*>(ws + l.sync);
-  p.status = reinterpret_cast<int*>(ws + l.status);
+  p.status = a->status ? static_cast<int*>(a->status) : reinterpret_cast<int*>(ws + l.status);
+  p.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   const size_t lds = part_lds_bytes<H>();
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cap) != hipSuccess)
@@ -560,6 +566,10 @@ bool part_plan(const wc_rnn_args* a) {
 int64_t part_workspace_bytes(const wc_rnn_args* a) { return part_layout(a).total; }
 
 int64_t part_status_offset(const wc_rnn_args* a) { return part_layout(a).status; }
+
+int32_t part_set_spin_limit(int32_t polls) {
+  return g_spin_limit.exchange(polls < 0 ? kSpinLimit : polls);
+}
 
 int32_t part_prepare(const wc_rnn_args* a, hipStream_t st, void** bias_f32) {
   const PartLayout l = part_layout(a);

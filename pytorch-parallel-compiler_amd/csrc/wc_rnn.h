@@ -24,6 +24,9 @@ bool part_plan(const wc_rnn_args* a);
 // workspace bytes and the byte offset of its status word under that plan
 int64_t part_workspace_bytes(const wc_rnn_args* a);
 int64_t part_status_offset(const wc_rnn_args* a);
+// poll rounds after which a wait of launches made from now on gives up (0: at the first
+// wait, < 0: the default); returns the previous value
+int32_t part_set_spin_limit(int32_t polls);
 // before the input projection: zero the plan's counters and status word, reset the
 // exchange buffer, and write bias = b_ih + b_hh (fp32) into the workspace; *bias_f32
 // receives its address (null when the layer has no bias)

@@ -23,7 +23,7 @@ from typing import Dict, List, Optional, Sequence
 import torch
 from torch import Tensor
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, BF16, F16 = 0, 1, 2
 ACT_NONE, ACT_RELU = 0, 1
@@ -53,6 +53,7 @@ class _RnnArgs(ctypes.Structure):
         ("h0", ctypes.c_void_p), ("c0", ctypes.c_void_p),
         ("out", ctypes.c_void_p), ("h_n", ctypes.c_void_p), ("c_n", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_int64),
+        ("status", ctypes.c_void_p),
     ]
 
 
@@ -172,6 +173,7 @@ SIGNATURES = {
     "wc_rnn_noalloc_scratch_bytes": (_I64, []),
     "wc_rnn_forward_noalloc": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_forward": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
+    "wc_rnn_set_spin_limit": (_I32, [_I32]),
     "wc_rnn_input_projection": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_rnn_recurrence": (_I32, [ctypes.POINTER(_RnnArgs), _P]),
     "wc_grouped_gemm": (_I32, [ctypes.POINTER(_GemmArgs), _P]),
@@ -407,9 +409,11 @@ def mlp2(**kw) -> None:
 def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional[Tensor],
              b_hh: Optional[Tensor], h0: Optional[Tensor], c0: Optional[Tensor], out: Tensor,
              h_n: Optional[Tensor], c_n: Optional[Tensor], workspace: Optional[Tensor] = None,
-             allocate: bool = True):
+             allocate: bool = True, status: Optional[Tensor] = None):
     """Fill the wc_rnn_args struct; allocates the workspace unless one is given or
-    allocate is False (then the struct carries no workspace).  Returns (args, workspace)."""
+    allocate is False (then the struct carries no workspace).  ``status`` is an optional
+    int32 device word that a give-up of the partitioned LSTM's bounded waits sets (never
+    cleared by the library).  Returns (args, workspace)."""
     n, batch, steps, in_size = x.shape
     hidden = w_hh.shape[-1]
     a = _RnnArgs()
@@ -421,6 +425,10 @@ def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional
     a.w_ih, a.w_hh, a.b_ih, a.b_hh = w_ih.data_ptr(), w_hh.data_ptr(), ptr(b_ih), ptr(b_hh)
     a.h0, a.c0 = ptr(h0), ptr(c0)
     a.out, a.h_n, a.c_n = out.data_ptr(), ptr(h_n), ptr(c_n)
+    if status is not None:
+        if status.dtype != torch.int32 or status.device != x.device:
+            raise ValueError("rnn status word must be an int32 tensor on the input's device")
+        a.status = status.data_ptr()
     if not allocate and workspace is None:
         a.workspace, a.workspace_bytes = None, 0
         return a, None
@@ -432,56 +440,117 @@ def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional
     return a, ws
 
 
-# Status words of recent partitioned-LSTM launches: (event, pinned host copy).  A launch
-# whose cross-workgroup wait timed out leaves 1 there; the next recurrent call (or
-# rnn_sync_check) raises once the copy has landed, without ever blocking the stream.
+# The partitioned LSTM's bounded cross-workgroup waits report a give-up (its outputs are
+# then invalid) in a status word.  Every launch made through rnn_forward /
+# rnn_forward_noalloc is given this device's own word, which the library never clears:
+# it collects the verdict of every eager launch and of every replay of a captured graph
+# until rnn_sync_check reads it, raises, and clears it.  After an eager launch a copy of
+# the word is queued to pinned host memory behind an event, so a later check raises
+# without blocking the stream; replays of captured launches queue no copy of their own,
+# so the next check queues one for every device whose word a capture used.
+_status_words: Dict[int, Tensor] = {}
+_status_captured: set = set()
 _rnn_pending: List = []
 
 
-def _rnn_watch(a: _RnnArgs, ws: Tensor) -> None:
-    off = int(lib().wc_rnn_status_offset(ctypes.byref(a)))
-    if off < 0 or torch.cuda.is_current_stream_capturing():
-        return
+def rnn_status_word(device: torch.device) -> Tensor:
+    """This device's status word (created, zeroed, at the first recurrent call outside
+    graph capture)."""
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    w = _status_words.get(idx)
+    if w is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise WideKernelError("wide_compiler: run a recurrent layer once outside graph capture before "
+                                  "capturing it (its status word is created then)")
+        w = _status_words[idx] = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", idx))
+    return w
+
+
+def _queue_status_copy(word: Tensor) -> None:
     host = torch.empty(1, dtype=torch.int32, pin_memory=True)
-    host.copy_(ws[off:off + 4].view(torch.int32), non_blocking=True)
+    host.copy_(word, non_blocking=True)
     ev = torch.cuda.Event()
-    ev.record(torch.cuda.current_stream(ws.device))
-    _rnn_pending.append((ev, host))
+    ev.record(torch.cuda.current_stream(word.device))
+    _rnn_pending.append((ev, host, word))
+
+
+def _rnn_watch(word: Tensor) -> None:
+    if torch.cuda.is_current_stream_capturing():
+        _status_captured.add(word.device.index)
+    else:
+        _queue_status_copy(word)
 
 
 def rnn_sync_check(block: bool = False) -> None:
-    """Raise WideKernelError if a finished partitioned-LSTM launch reported a timed-out
-    cross-workgroup wait (its outputs are then invalid).  block=True waits for every
-    launch still in flight."""
+    """Raise WideKernelError if a finished partitioned-LSTM launch or graph replay reported
+    a bounded wait that gave up (its outputs are then invalid), and clear the word.
+    block=True waits for every launch still in flight; otherwise launches whose status
+    has not landed yet are checked by a later call."""
     global _rnn_pending
-    if not _rnn_pending or torch.cuda.is_current_stream_capturing():
+    if torch.cuda.is_current_stream_capturing():
         return                       # events cannot be queried while a graph is captured
-    keep, failed = [], 0
-    for ev, host in _rnn_pending:
+    for idx in _status_captured:
+        _queue_status_copy(_status_words[idx])
+    if not _rnn_pending:
+        return
+    keep, failed = [], []
+    for ev, host, word in _rnn_pending:
         if block:
             ev.synchronize()
         if ev.query():
-            failed += int(host[0]) != 0
+            if int(host[0]) != 0 and all(word is not f for f in failed):
+                failed.append(word)
         else:
-            keep.append((ev, host))
+            keep.append((ev, host, word))
     _rnn_pending = keep
     if failed:
-        raise WideKernelError("wc_rnn_recurrence: a cross-workgroup wait of the partitioned LSTM timed out; "
-                              "the outputs of that launch are invalid")
+        for word in failed:
+            word.zero_()
+        # copies still in flight may hold the verdict just reported
+        _rnn_pending = [e for e in _rnn_pending if all(e[2] is not f for f in failed)]
+        raise WideKernelError("wc_rnn_recurrence: a cross-workgroup wait of the partitioned LSTM gave up; "
+                              "the outputs of that launch (or graph replay) are invalid")
+
+
+def rnn_set_spin_limit(polls: int) -> int:
+    """Poll rounds after which a partitioned-LSTM wait gives up for launches made from now
+    on (0: at the first wait; < 0: the default); returns the previous value."""
+    return int(lib().wc_rnn_set_spin_limit(int(polls)))
+
+
+def _part_status(a: _RnnArgs, x: Tensor) -> Optional[Tensor]:
+    """This device's status word, set in ``a``, when these sizes run the partitioned LSTM
+    (the one recurrent kernel with cross-workgroup waits); None otherwise."""
+    if int(lib().wc_rnn_status_offset(ctypes.byref(a))) < 0:
+        return None
+    word = rnn_status_word(x.device)
+    a.status = word.data_ptr()
+    return word
 
 
 def rnn_forward(**kw) -> None:
+    """wc_rnn_forward with a fresh workspace (and, on the partitioned plan, this device's
+    status word); a give-up of an earlier launch is raised here (non-blocking), or by
+    rnn_sync_check."""
     rnn_sync_check()
     a, ws = rnn_args(**kw)
+    word = _part_status(a, kw["x"])
     _check(lib().wc_rnn_forward(ctypes.byref(a), stream_of(kw["x"])), "wc_rnn_forward")
-    _rnn_watch(a, ws)
+    if word is not None:
+        _rnn_watch(word)
 
 
 def rnn_forward_noalloc(**kw) -> None:
     """wc_rnn_forward_noalloc: the same forward with the workspace in the library's static
-    per-device scratch; nothing is allocated for the call."""
+    per-device scratch; nothing is allocated for the call (the status word is this
+    device's persistent one)."""
+    rnn_sync_check()
     a, _ = rnn_args(allocate=False, **kw)
+    word = _part_status(a, kw["x"])
     _check(lib().wc_rnn_forward_noalloc(ctypes.byref(a), stream_of(kw["x"])), "wc_rnn_forward_noalloc")
+    if word is not None:
+        _rnn_watch(word)
 
 
 def rnn_phase(a: _RnnArgs, phase: str, like: Tensor) -> None:
@@ -612,6 +681,6 @@ def exported_symbols() -> List[str]:
 # code for the hot path.
 for _name in ("pack_rows", "swap01", "embedding_gather", "layernorm", "bn_eval", "group_norm", "grouped_gemm",
               "mlp2", "mlp2_args", "mlp2_launch", "embedding_layernorm", "rnn_forward", "rnn_forward_noalloc", "rnn_phase", "conv_pack_weights", "conv2d", "conv3d",
-              "attention", "self_attention", "rnn_sync_check"):
+              "attention", "self_attention", "rnn_sync_check", "rnn_status_word", "rnn_set_spin_limit"):
     globals()[_name] = torch.compiler.disable(globals()[_name])
 del _name

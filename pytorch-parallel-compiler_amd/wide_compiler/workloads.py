@@ -158,11 +158,15 @@ class WideSeqModel(nn.Module):
         self.lstm = WideLSTM.from_modules([m.lstm for m in models])
         self.fc = WideLinear.from_modules([m.fc for m in models])
 
-    def forward(self, ids: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """ids [N, B, T] (model i uses row i) -> logits [N, B, T, V]."""
+    def forward(self, ids: torch.Tensor, out: Optional[torch.Tensor] = None, return_state: bool = False):
+        """ids [N, B, T] (model i uses row i) -> logits [N, B, T, V]; with ``return_state``
+        (logits, lstm_out [N, B, T, H], (h_n, c_n)) from the same launches.  The launches
+        are asynchronous: a bounded wait of the LSTM recurrence that gave up is raised by
+        ``wide_compiler._hip.rnn_sync_check(block=True)`` (or the next recurrent call)."""
         x = self.emb.forward_layernorm(ids, self.ln, per_model=True)   # = self.ln(self.emb(ids, ...))
-        h, _ = self.lstm(x)
-        return self.fc.forward_into(h, out)
+        h, state = self.lstm(x)
+        y = self.fc.forward_into(h, out)
+        return (y, h, state) if return_state else y
 
 
 def seq_n64(n: int = 64, batch: int = 16, steps: int = 128, vocab: int = 8192, dim: int = 256,

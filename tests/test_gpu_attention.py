@@ -232,3 +232,49 @@ def test_attention_config_n16(hip):
                                    c(wide.q_weight), c(wide.kv_weight), c(wide.out_weight), c(wide.q_bias),
                                    c(wide.kv_bias), c(wide.out_bias), h)
         assert rel_err(y[k:k + 1], exact) <= TOL_BF16
+
+
+def test_resident_attention_repeatable_on_fresh_inputs(hip):
+    """Guard for the resident-KV kernels' softmax exchange between the wave's lane halves (the
+    running max and the row sums; a stale word there would corrupt whole output rows): fresh
+    inputs, instantiations interleaved (the fused-projection kernel and the resident kernel,
+    causal and not, 4- and 8-wave tiles, head dims 32 and 64), three launches each, all
+    bit-identical."""
+    from wide_compiler import _hip
+    g = torch.Generator(device=DEV).manual_seed(430)
+    bf = torch.bfloat16
+    cfgs = [(4, 4, 512, 256, 8), (3, 2, 256, 128, 4), (2, 3, 384, 128, 2), (2, 2, 200, 64, 1)]
+    for _ in range(6):
+        for n, b, s, d, heads in cfgs:
+            dh = d // heads
+            scale = dh ** -0.5
+            for causal in (False, True):
+                runs = []
+                if dh == 32:
+                    x = torch.randn(n, b, s, d, device=DEV, generator=g).to(bf)
+                    qw = (torch.randn(n, d, d, device=DEV, generator=g) * d ** -0.5).to(bf)
+                    kvw = (torch.randn(n, 2 * d, d, device=DEV, generator=g) * d ** -0.5).to(bf)
+                    qb = (torch.randn(n, d, device=DEV, generator=g) * 0.1).to(bf)
+                    kvb = (torch.randn(n, 2 * d, device=DEV, generator=g) * 0.1).to(bf)
+
+                    def fused(o, x=x, qw=qw, kvw=kvw, qb=qb, kvb=kvb, causal=causal, heads=heads, scale=scale):
+                        _hip.self_attention(x=x, q_weight=qw, kv_weight=kvw, q_bias=qb, kv_bias=kvb, o=o,
+                                            heads=heads, scale=scale, causal=causal)
+                    runs.append(fused)
+                q, k, v = (torch.randn(n * b, s, d, device=DEV, generator=g).to(bf) for _ in range(3))
+
+                def resident(o, q=q, k=k, v=v, causal=causal, heads=heads, dh=dh, scale=scale, s=s, d=d):
+                    st = (s * d, d)
+                    _hip.attention(q=q, k=k, v=v, o=o.view(n * b, s, d), nb=n * b, heads=heads, sq=s, skv=s,
+                                   head_dim=dh, q_strides=st, k_strides=st, v_strides=st, o_strides=st,
+                                   scale=scale, causal=causal)
+                runs.append(resident)
+                for run in runs:
+                    outs = []
+                    for _ in range(3):
+                        o = torch.full((n, b, s, d), float("nan"), dtype=bf, device=DEV)
+                        run(o)
+                        outs.append(o)
+                    assert not torch.isnan(outs[0]).any(), (n, b, s, d, heads, causal, run.__name__)
+                    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2]), \
+                        (n, b, s, d, heads, causal, run.__name__)

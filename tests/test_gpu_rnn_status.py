@@ -1,0 +1,109 @@
+"""The partitioned on-chip LSTM (bf16, hidden 256 / 384 / 512) under graph capture and when its
+bounded cross-workgroup waits give up.
+
+A give-up is forced from the host: wc_rnn_set_spin_limit(0) makes every wait give up before
+its first poll, so every workgroup records the status word and leaves normally (no kernel is
+made to hang).  The verdict must reach the caller in each way the layer runs: an eager call,
+replays of a captured graph, and the no-alloc entry point."""
+
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import wide_ref
+from tests._util import TOL_BF16, gen, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _wide_lstm(n, i, h, seed):
+    import wide_compiler as wc
+    torch.manual_seed(seed)
+    mods = [nn.LSTM(i, h, batch_first=True) for _ in range(n)]
+    return wc.WideLSTM.from_modules(mods).to(DEV, torch.bfloat16)
+
+
+def _x(shape, seed):
+    return torch.randn(shape, generator=gen(seed)).to(torch.bfloat16).to(DEV)
+
+
+def test_captured_lstm_replays_match_eager_bit_for_bit(hip):
+    """torch.cuda.graph capture of a partitioned WideLSTM (8 models, hidden 512, bf16): four
+    replays on new inputs copied into the captured input buffer, with eager forwards between
+    the replays, each equal to the eager forward of the same input bit for bit, and the status
+    word clear after every replay."""
+    n, b, t, i, h = 8, 16, 40, 64, 512
+    wide = _wide_lstm(n, i, h, 611)
+    static_x = _x((n, b, t, i), 612)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.no_grad():
+        wide(static_x)                                   # warm-up, outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    hip.rnn_sync_check(block=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        g_out, (g_hn, g_cn) = wide(static_x)
+    for k in range(4):
+        xk = _x((n, b, t, i), 620 + k)
+        static_x.copy_(xk)
+        graph.replay()
+        torch.cuda.synchronize()
+        hip.rnn_sync_check(block=True)
+        with torch.no_grad():
+            e_out, (e_hn, e_cn) = wide(xk)
+        hip.rnn_sync_check(block=True)
+        assert torch.equal(g_out, e_out) and torch.equal(g_hn, e_hn) and torch.equal(g_cn, e_cn), k
+    # and the eager result is the LSTM's (per timestep, against the fp64 oracle)
+    p = [getattr(wide, a).detach().cpu().double() for a in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    eo, _ = wide_ref.lstm(xk.cpu().double(), *p)
+    assert max(rel_err(e_out.cpu()[:, :, s_], eo[:, :, s_]) for s_ in range(t)) <= TOL_BF16
+
+
+def test_give_up_is_raised_in_every_mode(hip):
+    n, b, t, i, h = 4, 8, 12, 32, 512
+    wide = _wide_lstm(n, i, h, 630)
+    x = _x((n, b, t, i), 631)
+    w = dict(cell=hip.CELL_LSTM, x=x, w_ih=wide.weight_ih.detach(), w_hh=wide.weight_hh.detach(),
+             b_ih=wide.bias_ih.detach(), b_hh=wide.bias_hh.detach(), h0=None, c0=None)
+    with torch.no_grad():
+        ref_out, _ = wide(x)                             # a clean run first
+    hip.rnn_sync_check(block=True)
+    ref_out = ref_out.clone()
+    prev = hip.rnn_set_spin_limit(0)
+    try:
+        # eager
+        with torch.no_grad():
+            wide(x)
+        with pytest.raises(hip.WideKernelError, match="gave up"):
+            hip.rnn_sync_check(block=True)
+        hip.rnn_sync_check(block=True)                   # reported once, then cleared
+        # graph replays: the capture keeps the spin limit it was captured with
+        graph = torch.cuda.CUDAGraph()
+        with torch.no_grad(), torch.cuda.graph(graph):
+            wide(x)
+        hip.rnn_set_spin_limit(prev)
+        for _ in range(2):
+            graph.replay()
+            with pytest.raises(hip.WideKernelError, match="gave up"):
+                hip.rnn_sync_check(block=True)
+        del graph
+        # the no-alloc entry point
+        hip.rnn_set_spin_limit(0)
+        out = torch.empty(n, b, t, h, device=DEV, dtype=torch.bfloat16)
+        hip.rnn_forward_noalloc(out=out, h_n=None, c_n=None, **w)
+        with pytest.raises(hip.WideKernelError, match="gave up"):
+            hip.rnn_sync_check(block=True)
+    finally:
+        hip.rnn_set_spin_limit(-1)
+    assert hip.rnn_set_spin_limit(-1) == 1 << 21
+    # with the default limit the layer runs clean again, and equals the first run
+    with torch.no_grad():
+        again, _ = wide(x)
+    hip.rnn_sync_check(block=True)
+    assert torch.equal(again, ref_out)
+    out = torch.empty(n, b, t, h, device=DEV, dtype=torch.bfloat16)
+    hip.rnn_forward_noalloc(out=out, h_n=None, c_n=None, **w)
+    hip.rnn_sync_check(block=True)
+    assert torch.equal(out, ref_out)

@@ -74,36 +74,43 @@ def test_seq_model_out_of_range_id_raises(hip):
         wide.emb.index_error()
 
 
-# Per-timestep bar against the reference's own bf16 path: that path keeps its cell state and
-# gates in bf16 and drifts up to ~0.02 from fp64 itself (measured ~0.016-0.02 per timestep on
-# this configuration), while this build stays within ~0.006 of fp64; two approximations on
+# Per-timestep bar of the recurrent outputs (LSTM output at every t, final cell state)
+# against the reference's own bf16 path: that path keeps its cell state and gates in bf16
+# and drifts up to ~0.02 from fp64 itself (measured ~0.016-0.02 per timestep on this
+# configuration), while this build stays within ~0.006 of fp64; two approximations on
 # either side of the exact answer can differ by the sum, so the bar is 3e-2 per timestep.
+# The logits are not a recurrent output: they are held to the bf16 bar (2e-2) against
+# fp64, against the reference's bf16 path end to end, and against the reference's bf16
+# Linear applied to this build's own LSTM output.
 TOL_BF16_PATH = 3e-2
 
 
 def test_seq_config_n64(hip):
-    """The sequence configuration at full size: N=64, B=16, T=128, vocab 8192, 256 -> 512, bf16.
-    Every model (the wide path has no cross-model terms) against the fp64 oracle (2e-2 at every
-    timestep of the LSTM output, the final cell state and the logits) and against the
-    reference's own bf16 path (bf16 gates and bf16 cell state, wide_lstm.py:205-229; 3e-2 per
-    timestep, TOL_BF16_PATH); the bf16 path's own distance from fp64 is checked too."""
+    """The sequence configuration at full size: N=64, B=16, T=128, vocab 8192, 256 -> 512, bf16,
+    through WideSeqModel.forward (the launches the benchmark times: gather with the LayerNorm
+    applied as rows are gathered, partitioned LSTM, vocabulary GEMM), which also returns the
+    LSTM output and state.  Every model (the wide path has no cross-model terms) against the
+    fp64 oracle (2e-2 at every timestep of the LSTM output, the final cell state and the
+    logits) and against the reference's own bf16 path (bf16 gates and bf16 cell state,
+    wide_lstm.py:205-229; recurrent outputs 3e-2 per timestep, TOL_BF16_PATH; logits 2e-2);
+    the bf16 path's own distance from fp64 is checked too."""
     from wide_compiler.workloads import WideSeqModel, seq_n64, seq_params
     wl = seq_n64()
     ids = wl.inputs["ids"]
     wide = WideSeqModel([m.to(DEV) for m in wl.models])
     with torch.no_grad():
-        x = wide.ln(wide.emb(ids.to(DEV), per_model=True))
-        hs, (hn, cn) = wide.lstm(x)
-        y = wide.fc(hs)
+        y, hs, (hn, cn) = wide(ids.to(DEV), return_state=True)
+    hip.rnn_sync_check(block=True)
     wide.emb.index_error()
-    assert y.shape == (64, 16, 128, 8192)
-    worst = {"fp64": 0.0, "bf16": 0.0, "bf16 path vs fp64": 0.0}
+    assert y.shape == (64, 16, 128, 8192) and hs.shape == (64, 16, 128, 512)
+    worst = {"h fp64": 0.0, "h bf16 path": 0.0, "h bf16 path vs fp64": 0.0,
+             "logits fp64": 0.0, "logits bf16 path": 0.0, "logits bf16 linear of own h": 0.0}
     for k in range(64):
         pb = seq_params([wl.models[k].cpu()])
         pd = {kk: (vv.double() if torch.is_tensor(vv) else vv) for kk, vv in pb.items()}
         got_h, got_c, got_y = hs[k:k + 1].cpu(), cn[k:k + 1].cpu(), y[k:k + 1].cpu()
         ref = {}
-        for name, p in (("fp64", pd), ("bf16", pb)):
+        for name, p in (("fp64", pd), ("bf16 path", pb)):
             e = wide_ref.layernorm(wide_ref.embedding_per_model(p["emb.weight"], ids[k:k + 1]), p["ln.weight"],
                                    p["ln.bias"], 1, p["ln.eps"])
             eo, (eh, ec) = wide_ref.lstm(e, p["lstm.weight_ih"], p["lstm.weight_hh"], p["lstm.bias_ih"],
@@ -111,10 +118,15 @@ def test_seq_config_n64(hip):
             ref[name] = eo
             bar = TOL_BF16 if name == "fp64" else TOL_BF16_PATH
             step_err = max(rel_err(got_h[:, :, s], eo[:, :, s]) for s in range(128))
-            worst[name] = max(worst[name], step_err)
+            worst["h " + name] = max(worst["h " + name], step_err)
             assert step_err <= bar, (k, name, step_err)
             assert rel_err(got_c, ec) <= bar, (k, name)
-            assert rel_err(got_y, wide_ref.linear(eo, p["fc.weight"], p["fc.bias"])) <= bar, (k, name)
-        drift = max(rel_err(ref["bf16"][:, :, s], ref["fp64"][:, :, s]) for s in range(128))
-        worst["bf16 path vs fp64"] = max(worst["bf16 path vs fp64"], drift)
-    print("worst per-timestep LSTM error", worst)
+            y_err = rel_err(got_y, wide_ref.linear(eo, p["fc.weight"], p["fc.bias"]))
+            worst["logits " + name] = max(worst["logits " + name], y_err)
+            assert y_err <= TOL_BF16, (k, name, y_err)
+        own = rel_err(got_y, wide_ref.linear(got_h, pb["fc.weight"], pb["fc.bias"]))
+        worst["logits bf16 linear of own h"] = max(worst["logits bf16 linear of own h"], own)
+        assert own <= TOL_BF16, (k, own)
+        drift = max(rel_err(ref["bf16 path"][:, :, s], ref["fp64"][:, :, s]) for s in range(128))
+        worst["h bf16 path vs fp64"] = max(worst["h bf16 path vs fp64"], drift)
+    print("worst errors over the 64 models", worst)
