@@ -817,12 +817,13 @@ __global__ __launch_bounds__(kXlThreads, 1) void gemm_xlp_kernel(GemmParams p, i
 // Persistent XL bf16 kernel, two waves per SIMD (bf16 output, no residual).
 // The tile walk, the K-stage ring, the LDS layout of a stage and its LDS-DMA
 // staging are those of gemm_xlp_kernel; the 256 x 256 tile is split over 8
-// waves (2 x 4) of 128 x 64 each, as 8 x 4 MFMA 16x16x32 blocks (128 AGPR
+// waves (2 x 4) of 128 x 64 each, as 8 x 4 MFMA 16x16x32 blocks (128
 // accumulators per lane).  Two waves per SIMD keep v_mfma_f32_16x16x32_bf16
 // issuing every ~19 cycles where one wave manages ~28.  Wave w moves 4 of a
 // stage's W row blocks and 4 of its A row blocks (8 rows x 128 bytes each),
-// reads 8 W and 4 A fragments per 32-wide half stage, and stores its output
-// through a 16-row x 64-column LDS half strip.
+// streams its 8 W and 4 A fragments per 32-wide half stage through registers
+// a few MFMA groups ahead of their use (see the main loop), and stores its
+// output through a 16-row x 64-column LDS half strip.
 // ---------------------------------------------------------------------------
 constexpr int kX8Threads = 512;
 constexpr int kX8StripPitch = 64 * 2 + 16;                // bf16 half-strip row: 64 columns (bytes)
@@ -914,18 +915,6 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
   const int fp0 = (((lane >> 4)) ^ (fr & 7)) << 4;
   const int fp1 = ((4 + (lane >> 4)) ^ (fr & 7)) << 4;
   const int wfo = (ow + fr) * 128, afo = kXlHalf + (mw + fr) * 128;
-  // fragment g of a K half: g < 8 is W rows ow + 16 g, g >= 8 A rows mw + 16 (g - 8)
-  auto read_frag = [&](int stage, int fpos, int g, bf16x8 (&wf)[8], bf16x8 (&af)[4]) {
-    const lds_char* st = smem + (stage & 1) * kXlStageBytes + fpos;
-    if (g < 8)
-      wf[g] = *(const lds_bf16x8*)(st + wfo + g * 2048);
-    else
-      af[g - 8] = *(const lds_bf16x8*)(st + afo + (g - 8) * 2048);
-  };
-  auto read_frags = [&](int stage, int fpos, bf16x8 (&wf)[8], bf16x8 (&af)[4]) {
-#pragma unroll
-    for (int g = 0; g < 12; ++g) read_frag(stage, fpos, g, wf, af);
-  };
 
   // ---- bias of a tile: wave w moves the tile's columns [32 w, 32 w + 32) into LDS slot
   // (tile index & 1) with one LDS-DMA load (columns past o read a valid column; the
@@ -1026,57 +1015,65 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
     }
   };
 
-  // ---- prologue: stage 0 landed and its first half read, stage 1 in flight ----
+  // ---- main loop, software-pipelined within each wave.  A stage is 16 groups of 4
+  // MFMAs: group g = 8 h + i multiplies W fragment i of K half h with the 4 A fragments
+  // of that half.  W fragments stream through a ring of 4 registers, read 4 groups ahead
+  // (after group g's MFMAs, fragment g + 4 into g's ring slot); the A fragments of half 1
+  // are read during half 0 and those of the next stage's half 0 after the stage's barrier,
+  // which sits after group 13: by then every fragment of the stage has been read, and the
+  // 8 MFMAs of groups 14 and 15 are issued beside the next stage's first reads and the
+  // DMA of stage s + 2.  A wave therefore rarely waits for its own LDS reads. ----
+  bf16x8 wr[4], a0[4], a1[4];
+  auto rd_w = [&](int stage, int g) {
+    const lds_char* st = smem + (stage & 1) * kXlStageBytes + ((g >> 3) ? fp1 : fp0);
+    wr[g & 3] = *(const lds_bf16x8*)(st + wfo + (g & 7) * 2048);
+  };
+  auto rd_a = [&](int stage, int h, bf16x8 (&a)[4]) {
+    const lds_char* st = smem + (stage & 1) * kXlStageBytes + (h ? fp1 : fp0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a[j] = *(const lds_bf16x8*)(st + afo + j * 2048);
+  };
+  auto group = [&](int g, bf16x8 (&a)[4], bool zero) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[g & 7][j] = mma16<TA>(wr[g & 3], a[j], zero ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[g & 7][j]);
+  };
+  // prologue: stage 0 landed, stage 1 in flight, stage 0's first reads issued
   issue(0);
   load_bias(tile_of(0), 0);
   vm_lgkm_wait<0>();
   bare_barrier();
   issue(1);
-  // One fragment set (8 W + 4 A), read at the start of each half: the other wave on the
-  // SIMD issues its MFMAs while this one waits for the reads (two sets would not fit
-  // beside the 128 accumulators in the 256 registers a wave has at two waves per SIMD).
-  bf16x8 wf[8], af[4];
-  auto half = [&](int stage, int fpos, auto first_tag) {
-    constexpr bool kFirst = decltype(first_tag)::value;
 #pragma unroll
-    for (int g = 0; g < 12; ++g) read_frag(stage, fpos, g, wf, af);
+  for (int g = 0; g < 4; ++g) rd_w(0, g);
+  rd_a(0, 0, a0);
+
+  auto stage = [&](int s, bool first, bool after_epi) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int g = 0; g < 16; ++g) {
+      group(g, g < 8 ? a0 : a1, first && g < 8);
+      if (g == 1) rd_a(s, 1, a1);                     // a1 last fed group 15 of stage s - 1
+      if (g + 4 < 16) rd_w(s, g + 4);
+      if (g == 13) {
+        // every read of stage s issued (the last after group 11); stage s + 1 landed:
+        // then slot s & 1 can take stage s + 2 and stage s + 1 can be read
+        if (after_epi) vm_lgkm_wait<E>();
+        else vm_lgkm_wait<0>();
+        bare_barrier();
+        const Dma d = dma_of(s + 2);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = mma16<TA>(wf[i], af[j], kFirst ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
-  };
-  using yes = std::true_type;
-  using no = std::false_type;
-  // stage s: first half; wait for stage s + 1 (behind it only the epilogue of a tile that
-  // ended at s - 1) and for every wave's reads of stage s's first half... and second half:
-  // the second half's fragments are read before the barrier, so slot s & 1 is free after it
-  auto step = [&](bool after_epi, int s, auto first_tag) {
-    half(s, fp0, first_tag);
-#pragma unroll
-    for (int g = 0; g < 12; ++g) read_frag(s, fp1, g, wf, af);
-    if (after_epi) vm_lgkm_wait<E>();
-    else vm_lgkm_wait<0>();
-    bare_barrier();
-    {
-      const Dma d = dma_of(s + 2);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) dma_block(d, q);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = mma16<TA>(wf[i], af[j], acc[i][j]);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);     // one DMA
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);     // four MFMAs
+        for (int q = 0; q < 8; ++q) dma_block(d, q);
+        rd_w(s + 1, 0);
+        rd_w(s + 1, 1);
+        rd_a(s + 1, 0, a0);                           // a0 last fed group 7
+      }
+      if (g == 14) rd_w(s + 1, 2);
+      if (g == 15) rd_w(s + 1, 3);
     }
   };
   for (int ti = 0; ti < my_tiles; ++ti) {
-    step(ti > 0, ti * KS, yes{});
-    for (int ks = 1; ks < KS; ++ks) step(false, ti * KS + ks, no{});
+    stage(ti * KS, true, ti > 0);
+    for (int ks = 1; ks < KS; ++ks) stage(ti * KS + ks, false, false);
     epilogue(tile_of(ti), ti);
     load_bias(tile_of(ti + 1 < my_tiles ? ti + 1 : ti), (ti + 1) & 1);
   }
