@@ -279,7 +279,21 @@ def cfg_mlp(dev, steps, warmup) -> Dict:
     def cpu_run():
         wide_ref.mlp_wide(packed_cpu, n, w1, b1, w2, b2)
 
+    def compiled():
+        """The same forward through compile(..., compile_model=True, compile_mode="reduce-overhead"):
+        torch.compile around the traced model, whose forward is one operator
+        (wide_compiler::module_call) that the cudagraph trees capture."""
+        cm = wc.compile(models, xs[0].to(dev), compile_model=True, compile_mode="reduce-overhead").eval()
+        with torch.inference_mode():
+            y = cm(packed).clone()
+        err = _rel(y, wide_ref.mlp_wide(packed_cpu.double(), n, w1.double(), b1.double(), w2.double(),
+                                        b2.double()))
+        sec = _timed(lambda: cm(packed), steps, max(warmup, 3))
+        return {"mode": "compile_model=True, reduce-overhead", "ms_per_step": sec / steps * 1e3,
+                "value": n * b * steps / sec, "unit": "samples/s", "parity_rel_err_vs_oracle": err}
+
     return {"name": work.name, "n": n, "batch": b, "dtype": "fp32", "step": lambda: wide(packed),
+            "compiled": compiled,
             "parity": parity, "kernels": kernels, "cpu": cpu_run, "cpu_samples": n * b,
             "cpu_sample": "full workload", "extra": {"layers": "Linear(64,128)-ReLU-Linear(128,64)"}}
 
@@ -661,6 +675,8 @@ def main() -> int:
                                         "peak": d["peak"], "unit": d["unit"], "frac": d["frac"],
                                         "us_per_launch": d["us_per_launch"]},
                            "kernels": rc["kernels"]}
+            if "compiled" in c:
+                extra[name]["torch_compile"] = c["compiled"]()
             print(f"bench: {name} {rc['samples_per_s']:.4g} samples/s ({rc['mode']}), {d['kernel'].split()[0]} "
                   f"{d['frac']:.3f}", file=sys.stderr, flush=True)
             del c, rc

@@ -66,10 +66,11 @@ def compile(  # noqa: A001 - public name of the reference API
 
 
 def _compiled(wide: nn.Module, cfg: WideConfig) -> nn.Module:
-    """compile_model=True (api.py:137-147): torch.compile around the model, which leaves each
-    kernel call as an opaque call between compiled regions.  (TracedWideModel.use_graphs() is the
-    explicit way to capture the kernels' own launches; measured on a traced 100-model MLP and a
-    100-model ResBlock it is slower than direct dispatch, so no mode turns it on by itself.)"""
+    """compile_model=True (api.py:137-147): torch.compile around the model.  The traced forward
+    is one operator of the compiled graph (torch.ops.wide_compiler.module_call, whose fake
+    implementation gives its output shape), so mode="reduce-overhead" captures the kernels'
+    launches into its CUDA graph and replays them; other torch code around the model compiles
+    as usual.  (TracedWideModel.use_graphs() captures the launches without torch.compile.)"""
     return torch.compile(wide, mode=cfg.compile_mode, backend=cfg.compile_backend, **cfg.compile_options)
 
 

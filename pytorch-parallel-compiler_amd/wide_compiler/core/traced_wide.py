@@ -21,6 +21,7 @@ beyond floating-point rounding:
 
 from __future__ import annotations
 
+import copy
 import operator
 from dataclasses import dataclass
 from typing import Any, Callable, Dict, List, Optional, Tuple
@@ -31,7 +32,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch import Tensor
 
-from .. import _hip
+from .. import _hip, _ops
 from .ensemble_util import pack_inputs, unpack_outputs  # noqa: F401  (re-exported like upstream)
 from .primitives import (
     WideAttention, WideBatchNorm1d, WideBatchNorm2d, WideConv1d, WideConv2d, WideConv3d, WideEmbedding,
@@ -199,6 +200,16 @@ class TracedWideModel(nn.Module):
         self._mlp2: Dict[str, WideMLP2] = {}
         self._chain_input: Dict[str, str] = {}
         self._skipped: Dict[str, str] = {}
+        # torch.compile: the forward is the operator wide_compiler::module_call on this
+        # handle; its fake implementation runs a meta-device copy of model 0 (kept out of
+        # the module tree), or None when that copy could not run the sample
+        self.__dict__["_op_handle"] = _ops.register(self)
+        self.__dict__["_meta_template"] = None
+
+    def __setstate__(self, state):
+        # a copy (copy.deepcopy, pickle) gets a handle of its own
+        super().__setstate__(state)
+        self.__dict__["_op_handle"] = _ops.register(self)
 
     # ----------------------------------------------------------------------------------
     @classmethod
@@ -301,6 +312,7 @@ class TracedWideModel(nn.Module):
 
         if fuse:
             wide._fuse_epilogues()
+        wide.__dict__["_meta_template"] = _meta_template(template, sample_input, n)
         return wide
 
     # ----------------------------------------------------------------------------------
@@ -461,6 +473,12 @@ class TracedWideModel(nn.Module):
     kMaxGraphs = 8
 
     def forward(self, x: Tensor) -> Tensor:
+        if torch.compiler.is_compiling():
+            # under torch.compile the whole forward is one operator (see _ops); a model whose
+            # output shape cannot be derived on the meta device ends the compiled region here
+            if self.__dict__.get("_meta_template") is not None:
+                return torch.ops.wide_compiler.module_call(self.__dict__["_op_handle"], [x])[0]
+            return self._forward_opaque(x)
         graphs = self.__dict__.get("_graphs")
         if graphs is not None and x.is_cuda and not torch.cuda.is_current_stream_capturing():
             key = (x.data_ptr(), x.shape, x.stride(), x.dtype, x.device, torch.is_grad_enabled(),
@@ -477,6 +495,23 @@ class TracedWideModel(nn.Module):
             graph.replay()
             return y
         return self._forward_launches(x)
+
+    @torch.compiler.disable
+    def _forward_opaque(self, x: Tensor) -> Tensor:
+        return self._forward_launches(x)
+
+    # the operator wide_compiler::module_call (torch.compile)
+    def op_forward(self, x: Tensor) -> List[Tensor]:
+        return [self._forward_launches(x)]
+
+    def op_fake(self, x: Tensor) -> List[Tensor]:
+        """Output of the forward on fake tensors: model 0's output shape on the meta device,
+        for one model's slice [B, C, *S] of the packed input, packed back to [B, N*C', *S']."""
+        from torch._subclasses.fake_tensor import unset_fake_temporarily
+        meta = self.__dict__["_meta_template"]
+        with unset_fake_temporarily():
+            shape, dtype = _meta_out(meta, [int(d) for d in x.shape], x.dtype, self.n)
+        return [x.new_empty(shape, dtype=dtype)]
 
     def _capture(self, x: Tensor) -> Tuple["torch.cuda.CUDAGraph", Tensor]:
         """Warm up once on a side stream (fills the plan and kept launch arguments outside the
@@ -636,6 +671,29 @@ class TracedWideModel(nn.Module):
         lines.append("")
         lines.append(f"Total: {total:,} params ({total // max(self.n, 1):,} per model)")
         return "\n".join(lines)
+
+
+def _meta_out(meta: nn.Module, packed_shape: List[int], dtype: torch.dtype, n: int):
+    """(packed output shape, dtype) of the wide forward on a packed input of this shape,
+    from the meta-device copy of model 0."""
+    b, c = packed_shape[0], packed_shape[1] // n
+    xm = torch.empty((b, c, *packed_shape[2:]), device="meta", dtype=dtype)
+    with torch.no_grad():
+        y = meta.to(dtype=dtype)(xm) if dtype.is_floating_point else meta(xm)
+    if isinstance(y, (tuple, list)):
+        y = y[0]
+    return (y.shape[0], n * y.shape[1], *y.shape[2:]), y.dtype
+
+
+def _meta_template(template: nn.Module, sample: Tensor, n: int) -> Optional[nn.Module]:
+    """A meta-device copy of model 0 that runs one model's slice of the sample, or None."""
+    try:
+        meta = copy.deepcopy(template).to("meta")
+        shape = [sample.shape[0], n * sample.shape[1], *sample.shape[2:]]
+        _meta_out(meta, shape, sample.dtype, n)
+        return meta
+    except Exception:  # noqa: BLE001 - such models run the forward outside the compiled graph
+        return None
 
 
 __all__ = ["TraceNode", "analyze_trace", "print_trace", "FunctionalOp", "BinaryOp", "GetAttrOp",

@@ -182,3 +182,36 @@ def test_self_attention_fusion_rules():
     w64 = wc.WideAttention(2, 128, 2).to(torch.bfloat16)          # head dim 64
     assert not w64._fusable(torch.zeros(2, 3, 40, 128, dtype=torch.bfloat16), None,
                             (w64.q_weight, w64.kv_weight, w64.out_weight, w64.q_bias, w64.kv_bias, w64.out_bias))
+
+
+def test_torch_compile_sees_the_traced_forward_as_one_operator():
+    """Under torch.compile the traced forward is one node, torch.ops.wide_compiler.module_call,
+    whose fake implementation gives the packed output shape (from a meta-device copy of model
+    0) without launching anything; a copy of the model gets a handle of its own."""
+    import copy
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    torch.manual_seed(1)
+    wide = TracedWideModel.from_models([_MLP() for _ in range(5)], torch.randn(4, 8))
+    h = wide.__dict__["_op_handle"]
+    with FakeTensorMode():
+        y = torch.ops.wide_compiler.module_call(h, [torch.empty(7, 40)])
+    assert tuple(y[0].shape) == (7, 20) and y[0].dtype == torch.float32
+    assert copy.deepcopy(wide).__dict__["_op_handle"] != h
+    graphs = []
+
+    class _Captured(Exception):
+        pass
+
+    def backend(gm, example_inputs):
+        graphs.append(gm)
+
+        def run(*args):
+            raise _Captured
+
+        return run
+
+    with pytest.raises(_Captured):
+        torch.compile(wide, backend=backend)(torch.randn(7, 40))
+    ops = [nd.target for nd in graphs[0].graph.nodes if nd.op == "call_function"]
+    assert torch.ops.wide_compiler.module_call.default in ops or torch.ops.wide_compiler.module_call in ops
+    assert len([o for o in ops if "module_call" in str(o)]) == 1

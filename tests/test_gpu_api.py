@@ -36,13 +36,19 @@ def test_compile_model_true_matches_eager(hip, mode):
     eager = wc.compile(models, sample)
     compiled = wc.compile(models, sample, compile_model=True, compile_mode=mode)
     g = gen(301)
-    for _ in range(3):                                  # successive calls with new inputs
-        x = torch.randn(4, 5 * 16, generator=g).to(DEV)
-        with torch.no_grad():
-            ref = eager(x).clone()
-            got = compiled(x).clone()
-        torch.cuda.synchronize()
-        assert rel_err(got, ref) <= TOL_F32
+    import warnings
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        for _ in range(4):                              # successive calls with new inputs
+            x = torch.randn(4, 5 * 16, generator=g).to(DEV)
+            with torch.no_grad():
+                ref = eager(x).clone()
+                got = compiled(x).clone()
+            torch.cuda.synchronize()
+            assert rel_err(got, ref) <= TOL_F32
+    # the forward is one operator in the compiled graph (wide_compiler::module_call), so
+    # reduce-overhead mode captures its kernel launches: no empty CUDA graph
+    assert not [w for w in caught if "Graph is empty" in str(w.message)], [str(w.message) for w in caught]
 
 
 def test_builder_compile_chain_runs(hip):
