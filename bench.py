@@ -173,7 +173,7 @@ def cfg_seq(dev, steps, warmup) -> Dict:
                     "fp32 statistics)", "hbm", t_emb, byts=rows * (8 + 2 * d * 2) + 2 * n * d * 2),
             _kernel("LSTM input projection (part_prep_kernel + gemm_xl8_kernel, 256 -> 2048, bf16 out)",
                     "mfma", t_proj, flops=2.0 * rows * g * d, peak=PEAK["bf16_mfma"]),
-            _kernel("lstm_part_kernel (LSTM recurrence, 128 steps, W_hh on-chip, 4 CUs per model)", "mfma",
+            _kernel("part_kernel<512, bf16, LSTM> (LSTM recurrence, 128 steps, W_hh on-chip, 4 CUs per model)", "mfma",
                     t_rec, flops=2.0 * rows * g * hdim, peak=PEAK["bf16_mfma"]),
             _kernel("gemm_xl8_kernel (vocab projection 512 -> 8192 + bias, bf16)", "mfma", t_fc,
                     flops=2.0 * rows * v * hdim, peak=PEAK["bf16_mfma"]),

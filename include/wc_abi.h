@@ -213,14 +213,15 @@ typedef struct wc_rnn_args {
 } wc_rnn_args;
 
 /* Bytes of workspace wc_rnn_forward needs for these sizes on the current device.
- * Partitioned LSTM plan (see wc_rnn_recurrence): bf16 input projection
- * n*batch*steps*G*2 + fp32 bias n*G*4 + step counters n*128 + a status word, each
- * rounded up to 256 bytes.  Otherwise: fp32 input projection n*batch*steps*G*4 +
- * fp32 cell state n*batch*hidden*4. */
+ * Partitioned plan (see wc_rnn_recurrence), with U = n * ceil(batch / 16) units: 16-bit
+ * input projection n*batch*steps*G*2 + fp32 bias n*G*4 (+ GRU: fp32 b_hn n*hidden*4) +
+ * exchange slots U*2*16*hidden*4 + step counters U*128 + a status word, each rounded up
+ * to 256 bytes.  Otherwise: fp32 input projection n*batch*steps*G*4 + fp32 cell state
+ * n*batch*hidden*4. */
 int64_t wc_rnn_workspace_bytes(const wc_rnn_args* args);
 
-/* Byte offset in the workspace of the int32 status word of the partitioned LSTM
- * plan, or -1 when these sizes use another plan.  wc_rnn_input_projection zeroes
+/* Byte offset in the workspace of the int32 status word of the partitioned plan, or
+ * -1 when these sizes use another plan.  wc_rnn_input_projection zeroes
  * it; the recurrence sets it to 1 if a cross-workgroup wait timed out, in which
  * case out / h_n / c_n are invalid. */
 int64_t wc_rnn_status_offset(const wc_rnn_args* args);
@@ -240,19 +241,21 @@ int32_t wc_rnn_forward(const wc_rnn_args* args, void* stream);
 /* Phase 1: gates_x = x W_ih^T + b_ih for all steps (grouped MFMA GEMM, fp32
  * accumulate) into the workspace as fp32 [n, batch*steps, G] -- the einsum
  * before the reference's time loop (wide_gru.py:168-170, wide_lstm.py:190-193).
- * Partitioned LSTM plan: gates_x = x W_ih^T + (b_ih + b_hh) rounded once to bf16,
- * and the plan's step counters and status word are zeroed. */
+ * Partitioned plan: gates_x = x W_ih^T + (b_ih + b_hh) rounded once to the element type
+ * (GRU: gate n takes b_ih alone; its b_hh is kept in fp32 for the recurrence), and the
+ * plan's step counters and status word are zeroed. */
 int32_t wc_rnn_input_projection(const wc_rnn_args* args, void* stream);
 
 /* Phase 2: the time loop (wide_gru.py:181-211, wide_lstm.py:205-232) reading
  * gates_x from the workspace that phase 1 filled; x and w_ih are not read.
  *  - One model's W_hh fits a workgroup's registers: one persistent launch, one
  *    workgroup per (model, batch row).
- *  - Partitioned LSTM (bf16, hidden 256 / 384 / 512, batch <= 16, n * hidden/128
- *    <= compute units, 16-byte aligned w_hh / h0 / c0 / out / h_n / c_n): one
- *    cooperative launch of hidden/128 workgroups per model, one per compute unit,
- *    that keep the model's W_hh and cell state on-chip for all steps and exchange
- *    h_t through device-coherent memory (an ordinary launch under stream capture).
+ *  - Partitioned plan (LSTM or GRU, bf16 or fp16, hidden 256 / 384 / 512, 16-byte
+ *    aligned w_hh / h0 / c0 / out / h_n / c_n): hidden/128 workgroups per unit of
+ *    (model, 16 batch rows), one per compute unit, that keep the model's W_hh and the
+ *    state on-chip for all steps and exchange h_t through device-coherent memory; a
+ *    cooperative launch per (compute units / (hidden/128)) units (ordinary launches
+ *    under stream capture).
  *  - Otherwise one launch per step (an MFMA gate GEMM fused with the cell update;
  *    hidden % 32 == 0). */
 int32_t wc_rnn_recurrence(const wc_rnn_args* args, void* stream);

@@ -1,44 +1,49 @@
-// Partitioned persistent LSTM recurrence (bf16; hidden 256, 384 or 512; batch <= 16).
+// Partitioned persistent recurrence: LSTM and GRU, bf16 or fp16, hidden 256, 384 or 512.
 //
-// W_hh of one model (4H x H bf16: 2 MB at H = 512) exceeds one compute unit's
-// registers and LDS, so P = H / 128 workgroups share a model, one per compute unit,
-// for all T steps.  Workgroup `part` owns hidden units [128 part, 128 part + 128) and
-// the 512 gate rows (i, f, g, o of each unit) of W_hh that feed them, held on-chip for
-// the whole sequence: the first SL k-steps (32 columns each) in LDS, the next NA in
-// AGPRs (loaded there directly and read in place as MFMA A operands), the rest in
-// VGPRs.  This file is built with -amdgpu-mfma-vgpr-form so that accumulators live in
-// VGPRs and the AGPR file is left to the weights.
+// W_hh of one model (G x H 16-bit values, G = 4H for the LSTM: 2 MB at H = 512) exceeds one
+// compute unit's registers and LDS, so P = H / 128 workgroups share a model, one per compute
+// unit, for all T steps.  Workgroup `part` owns hidden units [128 part, 128 part + 128) and
+// the gate rows of W_hh that feed them, held on-chip for the whole sequence: the first SL
+// k-steps (32 columns each) in LDS, the next NA in AGPRs (loaded there directly and read in
+// place as MFMA A operands), the rest in VGPRs.  This file is built with
+// -amdgpu-mfma-vgpr-form so that accumulators live in VGPRs and the AGPR file is left to
+// the weights.
 //
-// Per step a workgroup forms its gate pre-activations for all batch rows as MFMA tiles
-// (A = W_hh rows, B = h_{t-1}^T read from LDS, C starts from gates_x), applies the
-// cell update in registers (the fp32 cell state never leaves the chip), writes h_t to
-// the output and to an exchange slot, and copies the other parts' slices of h_t from
+// The work is split into units of (model, chunk of up to 16 batch rows): batch rows of a
+// recurrence are independent, so a chunk has its own cell state, exchange slots and step
+// counters.  One launch runs up to (compute units / P) units; more units take several
+// launches in a row on the stream.
+//
+// Per step a workgroup forms its gate pre-activations for the chunk's rows as MFMA tiles
+// (A = W_hh rows, B = h_{t-1}^T read from LDS), applies the cell update in registers (the
+// fp32 state -- the LSTM cell state, the GRU hidden state -- never leaves the chip), writes
+// h_t to the output and to an exchange slot, and copies the other parts' slices of h_t from
 // their exchange slots into its LDS.
 //
-// Lane layout (v_mfma_f32_16x16x32_bf16, wave w of 4, lane = 16 g + fr): row tile j
-// (0..7) of wave w holds A row rho = gate (rho & 3) of unit 32 w + 8 (rho >> 2) + j,
-// so the accumulator of lane (g, fr) holds all four gates of unit 32 w + 8 g + j for
-// batch row fr.  A lane therefore owns 8 consecutive units of one batch row: its
-// gates_x of a gate, its h_t and its cell state are 16-byte vectors, and the cell
-// update needs no data exchange between lanes.
+// Lane layout (v_mfma_f32_16x16x32 on 16-bit operands, wave w of 4, lane = 16 g + fr): row
+// tile j (0..7) of wave w holds A row rho = gate slot (rho & 3) of unit 32 w + 8 (rho >> 2)
+// + j, so the accumulator of lane (g, fr) holds the four gate slots of unit 32 w + 8 g + j
+// for chunk row fr.  LSTM slots are the gates i, f, g, o; GRU slots are r, z, n and a fourth
+// whose W rows repeat those of n and whose result is never read.  A lane therefore owns 8
+// consecutive units of one row: its gates_x of a gate, its h_t and its state are 16-byte
+// vectors, and the cell update needs no data exchange between lanes.
 //
-// Exchange.  Each exchanged value is one 32-bit word, (bf16 bits of h << 16) | tag,
-// where tag = (base + t) mod 2^16 names the step; a reader polls the words it needs
-// with device-scope (sc1) loads until every tag matches, so no separate flag, store
-// fence or extra round trip is needed.  Writers use device-scope stores too, unless
-// every part of the model runs on one XCD (read from HW_REG_XCC_ID at start), in which
-// case plain stores into the shared L2 suffice and are faster.  There are
-// two slots per model (step parity): a part cannot write step t + 2 into a slot before
-// every other part has read step t from it, since it needs their step t + 1 first.
-// `base` lives in the caller's workspace: the input projection zeroes it and fills
-// the slots with tag 0xFFFF, and the last workgroup of a model to finish advances it
-// by T, so a slot's stale tag is always 1 or 2 steps behind the one a reader expects.
-// Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
-// at the first wait without polling) the workgroup records 1 in the status word
-// and leaves (the outputs are then invalid).  The status word is the caller's own
-// when one is passed (never cleared here), else a word of the workspace that the
-// input projection zeroes.  The host launches the grid cooperatively, so all
-// workgroups are co-resident or the launch fails.
+// Exchange.  Each exchanged value is one 32-bit word, (16 bits of h << 16) | tag, where tag =
+// (base + t) mod 2^16 names the step; a reader polls the words it needs with device-scope
+// (sc1) loads until every tag matches, so no separate flag, store fence or extra round trip
+// is needed.  Writers use device-scope stores too, unless every part of the unit runs on one
+// XCD (read from HW_REG_XCC_ID at start), in which case plain stores into the shared L2
+// suffice and are faster.  There are two slots per unit (step parity): a part cannot write
+// step t + 2 into a slot before every other part has read step t from it, since it needs
+// their step t + 1 first.  `base` lives in the caller's workspace: the input projection
+// zeroes it and fills the slots with tag 0xFFFF, and the last workgroup of a unit to finish
+// advances it by T, so a slot's stale tag is always 1 or 2 steps behind the one a reader
+// expects.  Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
+// at the first wait without polling) the workgroup records 1 in the status word and leaves
+// (the outputs are then invalid).  The status word is the caller's own when one is passed
+// (never cleared here), else a word of the workspace that the input projection zeroes.  The
+// host launches the grid cooperatively, so all workgroups are co-resident or the launch
+// fails.
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
@@ -60,18 +65,20 @@ constexpr int kSc1 = 16;               // buffer-op cache policy: device scope (
 constexpr uint32_t kTagFill = 0xFFFFu;
 
 struct PartParams {
-  int n, batch, steps, remap;
-  int spin_limit;     // poll rounds of a wait before it gives up (0: at once)
-  const bf16* gx;     // [n, batch, steps, 4H]: x W_ih^T + b_ih + b_hh, rounded to bf16
-  const bf16* w_hh;   // [n, 4H, H]
-  const bf16* h0;     // [n, batch, H] or null
-  const bf16* c0;     // [n, batch, H] or null
-  bf16* out;          // [n, batch, steps, H]
-  bf16* hn;           // [n, batch, H] or null
-  bf16* cn;           // [n, batch, H] or null
-  uint32_t* xch;      // [n][2][16][H] exchange words
-  int* sync;          // [n][kSyncInts]
-  int* status;        // set to 1 when a wait gave up
+  int n, rows, chunks;  // models, batch rows, 16-row chunks per model
+  int unit0, steps, remap;
+  int spin_limit;       // poll rounds of a wait before it gives up (0: at once)
+  const void* gx;       // [n, rows, steps, G]: x W_ih^T + folded biases, in the element type
+  const void* w_hh;     // [n, G, H]
+  const void* h0;       // [n, rows, H] or null
+  const void* c0;       // LSTM: [n, rows, H] or null
+  const float* bhn;     // GRU: [n, H] fp32 b_hh of gate n, or null
+  void* out;            // [n, rows, steps, H]
+  void* hn;             // [n, rows, H] or null
+  void* cn;             // LSTM: [n, rows, H] or null
+  uint32_t* xch;        // [units][2][16][H] exchange words
+  int* sync;            // [units][kSyncInts]
+  int* status;          // set to 1 when a wait gave up
 };
 
 std::atomic<int> g_spin_limit{kSpinLimit};
@@ -108,7 +115,7 @@ struct KOrder {
 // acc[j] += the k-steps B..E-1 of (W_hh rows of tile j) x h^T for the tiles J0 <= j < J1:
 // A fragments from LDS (wlw, this lane's fragment base), AGPRs (wa) or VGPRs (wv); B fragments
 // from this lane's h row in LDS (hrow, k-step s at hrow + 32 s).
-template <int SL, int NA, int XL, int B, int E, int J0, int J1, int NT, int RA, int RV>
+template <typename T, int SL, int NA, int XL, int B, int E, int J0, int J1, int NT, int RA, int RV>
 __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[NT], const bf16x8 (&wa)[RA][NT],
                                            const bf16x8 (&wv)[RV][NT], const bf16x8* wlw, const bf16* hrow) {
   static_assert(0 <= J0 && J0 < J1 && J1 <= NT, "tile range");
@@ -142,7 +149,7 @@ __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[NT], const bf16x8 (&wa)[
       if (in_lds(s, j)) a = lf[j];
       else if (s < SL + NA) a = wa[s < SL + NA ? s - SL : 0][j];
       else a = wv[s < SL + NA ? 0 : s - SL - NA][j];
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hc, acc[j], 0, 0, 0);
+      acc[j] = mma16<T>(a, hc, acc[j]);
       // two LDS-fed k-steps in a row: refill tile j once its MFMA has taken it
       if (ord.lds[i] && nxt_lds) load_tile(ord.s[i + 1], j);
     }
@@ -159,6 +166,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
+// element j of 8 raw 16-bit lanes of type T, as float; store a float there, rounded
+template <typename T>
+__device__ __forceinline__ float lane_f(const bf16x8& v, int j) {
+  if constexpr (std::is_same<T, f16>::value) return static_cast<float>(__builtin_bit_cast(f16x8, v)[j]);
+  else return static_cast<float>(v[j]);
+}
+template <typename T>
+__device__ __forceinline__ void set_lane(bf16x8& v, int j, float x) {
+  if constexpr (std::is_same<T, f16>::value) {
+    f16x8 t = __builtin_bit_cast(f16x8, v);
+    t[j] = static_cast<f16>(x);
+    v = __builtin_bit_cast(bf16x8, t);
+  } else {
+    v[j] = static_cast<bf16>(x);
+  }
+}
+
 // LDS-only barrier: waits for this wave's LDS traffic, not for its global loads and
 // stores, which stay in flight across it
 __device__ __forceinline__ void lds_barrier() {
@@ -172,14 +196,16 @@ __device__ __forceinline__ void sync_store(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int H>
+template <int H, typename T, int CELL>
 __global__ __launch_bounds__(kPartThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void lstm_part_kernel(PartParams p) {
+void part_kernel(PartParams p) {
+  constexpr bool GRU = CELL == WC_CELL_GRU;
   constexpr int NT = 8, KS = H / 32, P = H / kPartUnits;
   constexpr int SL = PartCfg<H>::SL, NA = PartCfg<H>::NA, XL = PartCfg<H>::XL, NV = KS - SL - NA;
   static_assert(NV >= 0 && P >= 2, "partition");
   constexpr int HP = H + 8;                          // LDS pitch of an h row (elements)
-  constexpr int G = 4 * H;
+  constexpr int G = (GRU ? 3 : 4) * H;
+  constexpr int NG = GRU ? 3 : 4;                    // gates_x vectors a lane reads per step
   constexpr int KPP = kPartUnits / 32;               // k-steps of one part's columns
   constexpr int CPR = (P - 1) * kPartUnits / 4;      // remote 16-byte exchange chunks per row
   constexpr int CPT = (16 * CPR + kPartThreads - 1) / kPartThreads;
@@ -189,28 +215,36 @@ void lstm_part_kernel(PartParams p) {
   // its base, so every read is the base plus an immediate offset
   constexpr int NF = SL * NT + XL;
   bf16x8* wl = reinterpret_cast<bf16x8*>(part_smem);
-  bf16* hs = reinterpret_cast<bf16*>(part_smem + (SL * NT + XL) * 4 * 1024);  // [16][HP] h_{t-1}
+  bf16* hs = reinterpret_cast<bf16*>(part_smem + (SL * NT + XL) * 4 * 1024);  // [16][HP] h_{t-1} (raw 16-bit)
   int* abort_flag = reinterpret_cast<int*>(hs + 16 * HP);
   int* xcd_flag = abort_flag + 1;
 
-  const int nwg = p.n * P;
+  const int nwg = static_cast<int>(gridDim.x);
   int id = blockIdx.x;
-  if (p.remap) id = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);   // a model's parts share an XCD
-  const int mdl = id / P, part = id - mdl * P;
+  if (p.remap) id = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);   // a unit's parts share an XCD
+  const int lu = id / P, part = id - lu * P;
+  const int unit = p.unit0 + lu;                     // (model, chunk) of this workgroup
+  const int mdl = unit / p.chunks, chk = unit - mdl * p.chunks;
+  const int row0 = chk * 16;
+  const int nrows = p.rows - row0 < 16 ? p.rows - row0 : 16;
   const int u0 = part * kPartUnits;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, fr = lane & 15;
   const int ucol = u0 + w * 32 + g * 8;              // first of the lane's 8 units (model column)
-  const bool brow = fr < p.batch;
-  const int64_t mb = static_cast<int64_t>(mdl) * p.batch;
+  const bool brow = fr < nrows;
+  const int64_t mb = static_cast<int64_t>(mdl) * p.rows + row0;   // the chunk's first row
+  const bf16* const h0 = static_cast<const bf16*>(p.h0);
+  const bf16* const c0 = static_cast<const bf16*>(p.c0);
 
-  // ---- W_hh rows of this part in LDS, AGPRs and VGPRs, loaded once ----
+  // ---- W_hh rows of this part in LDS, AGPRs and VGPRs, loaded once (GRU: gate slot 3
+  // repeats the n rows; its accumulator is never read) ----
   bf16x8 wa[NA > 0 ? NA : 1][NT];
   bf16x8 wv[NV > 0 ? NV : 1][NT];
   {
-    const bf16* wb = p.w_hh + static_cast<int64_t>(mdl) * G * H;
+    const bf16* wb = static_cast<const bf16*>(p.w_hh) + static_cast<int64_t>(mdl) * G * H;
+    const int slot = GRU && (fr & 3) == 3 ? 2 : (fr & 3);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      const bf16* row = wb + static_cast<int64_t>((fr & 3) * H + u0 + w * 32 + (fr >> 2) * 8 + j) * H + g * 8;
+      const bf16* row = wb + static_cast<int64_t>(slot * H + u0 + w * 32 + (fr >> 2) * 8 + j) * H + g * 8;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const bf16* src = row + ((s + part * KPP) % KS) * 32;   // rotated k-step s
@@ -233,37 +267,53 @@ void lstm_part_kernel(PartParams p) {
 #pragma unroll
       for (int j = 0; j < NT; ++j) asm volatile("" : "+a"(wa[i][j]));
   }
-  // ---- h_{-1} into LDS (rows >= batch stay zero), c_{-1} and gates_x of step 0 in registers ----
+  // ---- h_{-1} into LDS (rows >= nrows stay zero); the state (LSTM: c_{-1}, GRU: h_{-1}) and
+  // gates_x of step 0 in registers ----
   for (int e = tid; e < 16 * (HP / 8); e += kPartThreads) {
     const int b = e / (HP / 8), col = (e - b * (HP / 8)) * 8;   // LDS column (rotated)
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (p.h0 && b < p.batch && col < H)
-      v = *reinterpret_cast<const uint4*>(p.h0 + (mb + b) * H + (col + u0) % H);
+    if (h0 && b < nrows && col < H)
+      v = *reinterpret_cast<const uint4*>(h0 + (mb + b) * H + (col + u0) % H);
     *reinterpret_cast<uint4*>(hs + b * HP + col) = v;
   }
   if (tid == 0) *abort_flag = 0;
   float c[NT];
   {
+    const bf16* s0 = GRU ? h0 : c0;
     bf16x8 cv = {};
-    if (p.c0 && brow) cv = *reinterpret_cast<const bf16x8*>(p.c0 + (mb + fr) * H + ucol);
+    if (s0 && brow) cv = *reinterpret_cast<const bf16x8*>(s0 + (mb + fr) * H + ucol);
 #pragma unroll
-    for (int j = 0; j < NT; ++j) c[j] = static_cast<float>(cv[j]);
+    for (int j = 0; j < NT; ++j) c[j] = lane_f<T>(cv, j);
   }
-  const __amdgpu_buffer_rsrc_t ors =
-      part_rsrc(p.out + mb * p.steps * H, static_cast<uint32_t>(p.batch) * p.steps * H * 2);
-  const __amdgpu_buffer_rsrc_t grs =
-      part_rsrc(p.gx + mb * p.steps * G, static_cast<uint32_t>(p.batch) * p.steps * G * 2);
-  const __amdgpu_buffer_rsrc_t xrs = part_rsrc(p.xch + static_cast<int64_t>(mdl) * 2 * 16 * H, 2 * 16 * H * 4);
+  float bn[NT];                                      // GRU: b_hh of gate n for the lane's units
+#pragma unroll
+  for (int j = 0; j < NT; ++j) bn[j] = 0.f;
+  if constexpr (GRU) {
+    if (p.bhn) {
+      const f32x4* bp = reinterpret_cast<const f32x4*>(p.bhn + static_cast<int64_t>(mdl) * H + ucol);
+      const f32x4 b0 = bp[0], b1 = bp[1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bn[j] = b0[j];
+        bn[4 + j] = b1[j];
+      }
+    }
+  }
+  const __amdgpu_buffer_rsrc_t ors = part_rsrc(static_cast<bf16*>(p.out) + mb * p.steps * H,
+                                               static_cast<uint32_t>(nrows) * p.steps * H * 2);
+  const __amdgpu_buffer_rsrc_t grs = part_rsrc(static_cast<const bf16*>(p.gx) + mb * p.steps * G,
+                                               static_cast<uint32_t>(nrows) * p.steps * G * 2);
+  const __amdgpu_buffer_rsrc_t xrs = part_rsrc(p.xch + static_cast<int64_t>(unit) * 2 * 16 * H, 2 * 16 * H * 4);
   const uint32_t lane_row = static_cast<uint32_t>(brow ? fr : 0) * p.steps;   // b * steps for this lane
   bf16x8 gxn[4];
   auto load_gx = [&](int t) {
     const uint32_t off = ((lane_row + t) * G + ucol) * 2;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < NG; ++q)
       gxn[q] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(grs, off + q * H * 2, 0, 0));
   };
   load_gx(0);
-  int* my_sync = p.sync + static_cast<int64_t>(mdl) * kSyncInts;
+  int* my_sync = p.sync + static_cast<int64_t>(unit) * kSyncInts;
   const uint32_t base = static_cast<uint32_t>(sync_load(my_sync + kSyncBase));
   __syncthreads();
 
@@ -341,7 +391,7 @@ void lstm_part_kernel(PartParams p) {
       for (int k = 0; k < PG; ++k) {
         int b, col;
         chunk(k0 + k, b, col);
-        if (k0 + k < CPT && b < p.batch) pending |= 1u << k;
+        if (k0 + k < CPT && b < nrows) pending |= 1u << k;
       }
       int spins = 0;
       while (pending) {
@@ -385,23 +435,34 @@ void lstm_part_kernel(PartParams p) {
   f32x4 acc[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  mfma_steps<SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);
+  mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);
   for (int t = 0; t < p.steps && !aborted; ++t) {
-    // gates = h_{t-1} W_hh^T (MFMA; own columns already in acc) + gates_x (x W_ih^T + b_ih
-    // + b_hh, added in the cell update)
-    // in two tile groups, so that the cell update of the first group can run between the
-    // second group's MFMAs (the h fragments are read once per group)
-    mfma_steps<SL, NA, XL, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
-    mfma_steps<SL, NA, XL, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
-    // cell update of the lane's 8 units (i, f, g, o in acc[j][0..3])
+    // gate slots = h_{t-1} W_hh^T (MFMA; own columns already in acc), in two tile groups,
+    // so that the cell update of the first group can run between the second group's MFMAs
+    // (the h fragments are read once per group); gates_x (x W_ih^T + the folded biases) is
+    // added in the cell update
+    mfma_steps<T, SL, NA, XL, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
+    mfma_steps<T, SL, NA, XL, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
+    // cell update of the lane's 8 units
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      const float ig = sigmoid_f(acc[j][0] + static_cast<float>(gxn[0][j]));
-      const float fg = sigmoid_f(acc[j][1] + static_cast<float>(gxn[1][j]));
-      const float gg = tanh_f(acc[j][2] + static_cast<float>(gxn[2][j]));
-      const float og = sigmoid_f(acc[j][3] + static_cast<float>(gxn[3][j]));
-      c[j] = fg * c[j] + ig * gg;
-      hv[j] = static_cast<bf16>(og * tanh_f(c[j]));
+      if constexpr (GRU) {
+        // r, z, n in acc[j][0..2]; gates_x holds b_ir + b_hr, b_iz + b_hz and b_in; b_hn
+        // joins the hidden part of n before r scales it (the torch.nn GRU cell)
+        const float rg = sigmoid_f(acc[j][0] + lane_f<T>(gxn[0], j));
+        const float zg = sigmoid_f(acc[j][1] + lane_f<T>(gxn[1], j));
+        const float nn = tanh_f(lane_f<T>(gxn[2], j) + rg * (acc[j][2] + bn[j]));
+        c[j] = (1.0f - zg) * nn + zg * c[j];
+        set_lane<T>(hv, j, c[j]);
+      } else {
+        // i, f, g, o in acc[j][0..3]
+        const float ig = sigmoid_f(acc[j][0] + lane_f<T>(gxn[0], j));
+        const float fg = sigmoid_f(acc[j][1] + lane_f<T>(gxn[1], j));
+        const float gg = tanh_f(acc[j][2] + lane_f<T>(gxn[2], j));
+        const float og = sigmoid_f(acc[j][3] + lane_f<T>(gxn[3], j));
+        c[j] = fg * c[j] + ig * gg;
+        set_lane<T>(hv, j, og * tanh_f(c[j]));
+      }
     }
     const uint32_t tag = (base + static_cast<uint32_t>(t)) & 0xFFFFu;
     const bool more = t + 1 < p.steps;
@@ -425,7 +486,7 @@ void lstm_part_kernel(PartParams p) {
     lds_barrier();                                     // this part's h_t is in LDS
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    mfma_steps<SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
+    mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
     get(t, tag);
     put_out();
     load_gx(t + 1);                                    // lands during the next step's MFMAs
@@ -435,15 +496,15 @@ void lstm_part_kernel(PartParams p) {
 
   if (!aborted && brow) {
     const int64_t so = (mb + fr) * H + ucol;
-    if (p.hn) *reinterpret_cast<bf16x8*>(p.hn + so) = hv;
-    if (p.cn) {
+    if (p.hn) *reinterpret_cast<bf16x8*>(static_cast<bf16*>(p.hn) + so) = hv;
+    if (!GRU && p.cn) {
       bf16x8 cv;
 #pragma unroll
-      for (int j = 0; j < NT; ++j) cv[j] = static_cast<bf16>(c[j]);
-      *reinterpret_cast<bf16x8*>(p.cn + so) = cv;
+      for (int j = 0; j < NT; ++j) set_lane<T>(cv, j, c[j]);
+      *reinterpret_cast<bf16x8*>(static_cast<bf16*>(p.cn) + so) = cv;
     }
   }
-  // the last part of the model to finish advances the tag base for the next launch
+  // the last part of the unit to finish advances the tag base for the next launch
   __syncthreads();
   if (tid == 0) {
     if (aborted) sync_store(p.status, 1);
@@ -455,21 +516,28 @@ void lstm_part_kernel(PartParams p) {
   }
 }
 
-// counters, tag base and status zeroed; exchange slots filled with tag 0xFFFF;
-// bias = b_ih + b_hh in fp32 (either may be null)
-__global__ void part_prep_kernel(int* sync, int64_t nsync, uint32_t* xch, int64_t nxch, const bf16* b_ih,
-                                 const bf16* b_hh, float* bias, int64_t nbias) {
+// counters, tag base and status zeroed; exchange slots filled with tag 0xFFFF; bias (fp32,
+// [n, G]) = b_ih + b_hh, except that the GRU's gate n (columns >= fold of each model's G)
+// takes b_ih alone and its b_hh goes to bhn (fp32, [n, H]); either bias may be null
+template <typename T>
+__global__ void part_prep_kernel(int* sync, int64_t nsync, uint32_t* xch, int64_t nxch, const T* b_ih,
+                                 const T* b_hh, float* bias, int64_t nbias, int g, int fold, float* bhn,
+                                 int hid) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < nsync) sync_store(sync + i, 0);
   if (i < nxch) __hip_atomic_store(xch + i, kTagFill, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (bias && i < nbias)
-    bias[i] = (b_ih ? static_cast<float>(b_ih[i]) : 0.f) + (b_hh ? static_cast<float>(b_hh[i]) : 0.f);
+  if (bias && i < nbias) {
+    const int col = static_cast<int>(i % g);
+    const float bh = b_hh ? to_f32(b_hh[i]) : 0.f;
+    bias[i] = (b_ih ? to_f32(b_ih[i]) : 0.f) + (col < fold ? bh : 0.f);
+    if (bhn && col >= fold) bhn[(i / g) * hid + (col - fold)] = bh;
+  }
 }
 
-template <int H>
+template <int H, typename T, int CELL>
 bool part_kernel_fits() {
   const size_t lds = part_lds_bytes<H>();
-  const void* fn = reinterpret_cast<const void*>(lstm_part_kernel<H>);
+  const void* fn = reinterpret_cast<const void*>(part_kernel<H, T, CELL>);
   if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
     return false;
   int per_cu = 0;
@@ -479,39 +547,44 @@ bool part_kernel_fits() {
 
 inline int64_t round256(int64_t v) { return (v + 255) & ~static_cast<int64_t>(255); }
 
+inline int64_t part_gates(const wc_rnn_args* a) { return (a->cell == WC_CELL_GRU ? 3 : 4) * a->hidden; }
+inline int64_t part_units(const wc_rnn_args* a) { return a->n * ((a->batch + 15) / 16); }
+
 struct PartLayout {
-  int64_t gx, bias, sync, xch, status, total;   // byte offsets into the workspace
+  int64_t gx, bias, bhn, sync, xch, status, total;   // byte offsets into the workspace
 };
 
 PartLayout part_layout(const wc_rnn_args* a) {
-  const int64_t g = 4 * a->hidden;
+  const int64_t g = part_gates(a), units = part_units(a);
   PartLayout l;
   l.gx = 0;
   l.bias = round256(a->n * a->batch * a->steps * g * 2);
-  l.xch = l.bias + round256(a->n * g * 4);
-  l.sync = l.xch + round256(a->n * 2 * 16 * a->hidden * 4);
-  l.status = l.sync + round256(a->n * kSyncInts * 4);   // the counters and the status word are
-  l.total = l.status + 256;                             // one contiguous int range
+  l.bhn = l.bias + round256(a->n * g * 4);
+  l.xch = l.bhn + (a->cell == WC_CELL_GRU ? round256(a->n * a->hidden * 4) : 0);
+  l.sync = l.xch + round256(units * 2 * 16 * a->hidden * 4);
+  l.status = l.sync + round256(units * kSyncInts * 4);   // the counters and the status word are
+  l.total = l.status + 256;                              // one contiguous int range
   return l;
 }
 
-template <int H>
+template <int H, typename T, int CELL>
 int32_t launch_part(const wc_rnn_args* a, hipStream_t st) {
+  constexpr int P = H / kPartUnits;
   const PartLayout l = part_layout(a);
   char* ws = static_cast<char*>(a->workspace);
   PartParams p;
   p.n = static_cast<int>(a->n);
-  p.batch = static_cast<int>(a->batch);
+  p.rows = static_cast<int>(a->batch);
+  p.chunks = (p.rows + 15) / 16;
   p.steps = static_cast<int>(a->steps);
-  const int nwg = p.n * (H / kPartUnits);
-  p.remap = (nwg % 8 == 0 && (nwg / 8) % (H / kPartUnits) == 0) ? 1 : 0;
-  p.gx = reinterpret_cast<const bf16*>(ws + l.gx);
-  p.w_hh = static_cast<const bf16*>(a->w_hh);
-  p.h0 = static_cast<const bf16*>(a->h0);
-  p.c0 = static_cast<const bf16*>(a->c0);
-  p.out = static_cast<bf16*>(a->out);
-  p.hn = static_cast<bf16*>(a->h_n);
-  p.cn = static_cast<bf16*>(a->c_n);
+  p.gx = ws + l.gx;
+  p.w_hh = a->w_hh;
+  p.h0 = a->h0;
+  p.c0 = CELL == WC_CELL_LSTM ? a->c0 : nullptr;
+  p.bhn = CELL == WC_CELL_GRU && a->b_hh ? reinterpret_cast<const float*>(ws + l.bhn) : nullptr;
+  p.out = a->out;
+  p.hn = a->h_n;
+  p.cn = CELL == WC_CELL_LSTM ? a->c_n : nullptr;
   p.xch = reinterpret_cast<uint32_t*>(ws + l.xch);
   p.sync = reinterpret_cast<int*>(ws + l.sync);
   p.status = a->status ? static_cast<int*>(a->status) : reinterpret_cast<int*>(ws + l.status);
@@ -526,41 +599,66 @@ int32_t launch_part(const wc_rnn_args* a, hipStream_t st) {
     const char* v = getenv("WC_RNN_COOPERATIVE");
     return !(v && v[0] == '0' && v[1] == '\0');
   }();
-  if (cap == hipStreamCaptureStatusNone && cooperative) {
-    // co-residency of the whole grid is guaranteed, or the launch fails here
-    void* args[] = {&p};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(lstm_part_kernel<H>),
-                                                    dim3(nwg), dim3(kPartThreads), args,
-                                                    static_cast<unsigned>(lds), st);
-    if (e != hipSuccess)
-      return set_error(static_cast<int32_t>(e), "wc_rnn_recurrence: cooperative launch of %d workgroups "
-                       "failed: %s", nwg, hipGetErrorString(e));
-    return WC_OK;
+  const void* fn = reinterpret_cast<const void*>(part_kernel<H, T, CELL>);
+  // units of (model, 16-row chunk), at most one workgroup per compute unit per launch
+  const int total = static_cast<int>(part_units(a));
+  const int per_launch = device_cu_count() / P;
+  for (int u = 0; u < total; u += per_launch) {
+    const int units = total - u < per_launch ? total - u : per_launch;
+    const int nwg = units * P;
+    p.unit0 = u;
+    p.remap = (nwg % 8 == 0 && (nwg / 8) % P == 0) ? 1 : 0;
+    if (cap == hipStreamCaptureStatusNone && cooperative) {
+      // co-residency of the whole grid is guaranteed, or the launch fails here
+      void* args[] = {&p};
+      const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(kPartThreads), args,
+                                                      static_cast<unsigned>(lds), st);
+      if (e != hipSuccess)
+        return set_error(static_cast<int32_t>(e), "wc_rnn_recurrence: cooperative launch of %d workgroups "
+                         "failed: %s", nwg, hipGetErrorString(e));
+    } else {
+      // under graph capture (or WC_RNN_COOPERATIVE=0): an ordinary launch (part_plan checked
+      // that one workgroup fits a compute unit, and no launch has more than the device's)
+      part_kernel<H, T, CELL><<<dim3(nwg), dim3(kPartThreads), lds, st>>>(p);
+      const int32_t rc = check_launch("wc_rnn_recurrence(partitioned)");
+      if (rc) return rc;
+    }
   }
-  // under graph capture (or WC_RNN_COOPERATIVE=0): an ordinary launch (part_plan checked
-  // that the grid fits the device one workgroup per compute unit)
-  lstm_part_kernel<H><<<dim3(nwg), dim3(kPartThreads), lds, st>>>(p);
-  return check_launch("wc_rnn_recurrence(partitioned)");
+  return WC_OK;
+}
+
+template <int H>
+bool part_fits(const wc_rnn_args* a) {
+  if (a->dtype == WC_F16)
+    return a->cell == WC_CELL_GRU ? part_kernel_fits<H, f16, WC_CELL_GRU>() : part_kernel_fits<H, f16, WC_CELL_LSTM>();
+  return a->cell == WC_CELL_GRU ? part_kernel_fits<H, bf16, WC_CELL_GRU>() : part_kernel_fits<H, bf16, WC_CELL_LSTM>();
+}
+
+template <int H>
+int32_t part_dispatch(const wc_rnn_args* a, hipStream_t st) {
+  if (a->dtype == WC_F16)
+    return a->cell == WC_CELL_GRU ? launch_part<H, f16, WC_CELL_GRU>(a, st) : launch_part<H, f16, WC_CELL_LSTM>(a, st);
+  return a->cell == WC_CELL_GRU ? launch_part<H, bf16, WC_CELL_GRU>(a, st) : launch_part<H, bf16, WC_CELL_LSTM>(a, st);
 }
 
 }  // namespace
 
 bool part_plan(const wc_rnn_args* a) {
-  if (a->cell != WC_CELL_LSTM || a->dtype != WC_BF16 || a->batch < 1 || a->batch > 16 || a->steps < 1 ||
-      a->steps > 0xFFFF)
+  if ((a->cell != WC_CELL_LSTM && a->cell != WC_CELL_GRU) || (a->dtype != WC_BF16 && a->dtype != WC_F16) ||
+      a->batch < 1 || a->steps < 1 || a->steps > 0xFFFF)
     return false;
   if (a->hidden != 256 && a->hidden != 384 && a->hidden != 512) return false;
   const int64_t parts = a->hidden / kPartUnits;
   const int cus = device_cu_count();
-  if (cus <= 0 || a->n * parts > cus) return false;
-  // per-model blocks of gates_x and out are addressed with 32-bit byte offsets
-  if (a->batch * a->steps * 4 * a->hidden * 2 >= 0x7fffffffll) return false;
+  if (cus <= 0 || parts > cus) return false;
+  // a unit's block of gates_x (16 rows) is addressed with 32-bit byte offsets
+  if (16 * a->steps * part_gates(a) * 2 >= 0x7fffffffll) return false;
   for (const void* q : {a->w_hh, a->h0, a->c0, static_cast<const void*>(a->out),
                         static_cast<const void*>(a->h_n), static_cast<const void*>(a->c_n)})
     if (q && !aligned(q, 16)) return false;
-  if (a->hidden == 256) return part_kernel_fits<256>();
-  if (a->hidden == 384) return part_kernel_fits<384>();
-  return part_kernel_fits<512>();
+  if (a->hidden == 256) return part_fits<256>(a);
+  if (a->hidden == 384) return part_fits<384>(a);
+  return part_fits<512>(a);
 }
 
 int64_t part_workspace_bytes(const wc_rnn_args* a) { return part_layout(a).total; }
@@ -574,22 +672,33 @@ int32_t part_set_spin_limit(int32_t polls) {
 int32_t part_prepare(const wc_rnn_args* a, hipStream_t st, void** bias_f32) {
   const PartLayout l = part_layout(a);
   char* ws = static_cast<char*>(a->workspace);
-  const int64_t g = 4 * a->hidden;
+  const int64_t g = part_gates(a);
   const int64_t nsync = (l.total - l.sync) / 4;
   const int64_t nxch = (l.sync - l.xch) / 4;
   const int64_t nbias = (a->b_ih || a->b_hh) ? a->n * g : 0;
+  const bool gru = a->cell == WC_CELL_GRU;
   *bias_f32 = nbias ? ws + l.bias : nullptr;
+  float* bhn = gru && a->b_hh ? reinterpret_cast<float*>(ws + l.bhn) : nullptr;
+  const int fold = static_cast<int>(gru ? 2 * a->hidden : g);
   const int64_t items = std::max(std::max(nsync, nxch), nbias);
-  part_prep_kernel<<<static_cast<uint32_t>(cdiv(items, 256)), 256, 0, st>>>(
-      reinterpret_cast<int*>(ws + l.sync), nsync, reinterpret_cast<uint32_t*>(ws + l.xch), nxch,
-      static_cast<const bf16*>(a->b_ih), static_cast<const bf16*>(a->b_hh), static_cast<float*>(*bias_f32), nbias);
+  const dim3 grid(static_cast<uint32_t>(cdiv(items, 256)));
+  if (a->dtype == WC_F16)
+    part_prep_kernel<f16><<<grid, 256, 0, st>>>(
+        reinterpret_cast<int*>(ws + l.sync), nsync, reinterpret_cast<uint32_t*>(ws + l.xch), nxch,
+        static_cast<const f16*>(a->b_ih), static_cast<const f16*>(a->b_hh), static_cast<float*>(*bias_f32), nbias,
+        static_cast<int>(g), fold, bhn, static_cast<int>(a->hidden));
+  else
+    part_prep_kernel<bf16><<<grid, 256, 0, st>>>(
+        reinterpret_cast<int*>(ws + l.sync), nsync, reinterpret_cast<uint32_t*>(ws + l.xch), nxch,
+        static_cast<const bf16*>(a->b_ih), static_cast<const bf16*>(a->b_hh), static_cast<float*>(*bias_f32),
+        nbias, static_cast<int>(g), fold, bhn, static_cast<int>(a->hidden));
   return check_launch("wc_rnn_input_projection(prep)");
 }
 
 int32_t part_recurrence(const wc_rnn_args* a, hipStream_t st) {
-  if (a->hidden == 256) return launch_part<256>(a, st);
-  if (a->hidden == 384) return launch_part<384>(a, st);
-  return launch_part<512>(a, st);
+  if (a->hidden == 256) return part_dispatch<256>(a, st);
+  if (a->hidden == 384) return part_dispatch<384>(a, st);
+  return part_dispatch<512>(a, st);
 }
 
 }  // namespace wc

@@ -412,7 +412,7 @@ def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional
              allocate: bool = True, status: Optional[Tensor] = None):
     """Fill the wc_rnn_args struct; allocates the workspace unless one is given or
     allocate is False (then the struct carries no workspace).  ``status`` is an optional
-    int32 device word that a give-up of the partitioned LSTM's bounded waits sets (never
+    int32 device word that a give-up of the partitioned recurrence's bounded waits sets (never
     cleared by the library).  Returns (args, workspace)."""
     n, batch, steps, in_size = x.shape
     hidden = w_hh.shape[-1]
@@ -440,7 +440,7 @@ def rnn_args(*, cell: int, x: Tensor, w_ih: Tensor, w_hh: Tensor, b_ih: Optional
     return a, ws
 
 
-# The partitioned LSTM's bounded cross-workgroup waits report a give-up (its outputs are
+# The partitioned recurrence's bounded cross-workgroup waits report a give-up (its outputs are
 # then invalid) in a status word.  Every launch made through rnn_forward /
 # rnn_forward_noalloc is given this device's own word, which the library never clears:
 # it collects the verdict of every eager launch and of every replay of a captured graph
@@ -483,7 +483,7 @@ def _rnn_watch(word: Tensor) -> None:
 
 
 def rnn_sync_check(block: bool = False) -> None:
-    """Raise WideKernelError if a finished partitioned-LSTM launch or graph replay reported
+    """Raise WideKernelError if a finished partitioned-recurrence launch or graph replay reported
     a bounded wait that gave up (its outputs are then invalid), and clear the word.
     block=True waits for every launch still in flight; otherwise launches whose status
     has not landed yet are checked by a later call."""
@@ -509,18 +509,18 @@ def rnn_sync_check(block: bool = False) -> None:
             word.zero_()
         # copies still in flight may hold the verdict just reported
         _rnn_pending = [e for e in _rnn_pending if all(e[2] is not f for f in failed)]
-        raise WideKernelError("wc_rnn_recurrence: a cross-workgroup wait of the partitioned LSTM gave up; "
+        raise WideKernelError("wc_rnn_recurrence: a cross-workgroup wait of the partitioned recurrence gave up; "
                               "the outputs of that launch (or graph replay) are invalid")
 
 
 def rnn_set_spin_limit(polls: int) -> int:
-    """Poll rounds after which a partitioned-LSTM wait gives up for launches made from now
+    """Poll rounds after which a partitioned-recurrence wait gives up for launches made from now
     on (0: at the first wait; < 0: the default); returns the previous value."""
     return int(lib().wc_rnn_set_spin_limit(int(polls)))
 
 
 def _part_status(a: _RnnArgs, x: Tensor) -> Optional[Tensor]:
-    """This device's status word, set in ``a``, when these sizes run the partitioned LSTM
+    """This device's status word, set in ``a``, when these sizes run the partitioned recurrence
     (the one recurrent kernel with cross-workgroup waits); None otherwise."""
     if int(lib().wc_rnn_status_offset(ctypes.byref(a))) < 0:
         return None

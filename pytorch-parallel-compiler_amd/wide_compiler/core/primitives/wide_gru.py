@@ -6,9 +6,13 @@ WideGRU: N independent single-layer nn.GRU(batch_first=True)
 
 Parameters keep the reference layout: weight_ih [N, 3H, I], weight_hh [N, 3H, H],
 bias_ih / bias_hh [N, 3H], gate order (r, z, n).  The forward is wc_rnn_forward: one
-grouped MFMA GEMM for the input projection of all T steps, then one persistent kernel in
-which each workgroup carries one (model, batch row) through all T steps with its W_hh
-slice held in registers (no per-step launches, no per-step HBM traffic for W_hh).
+grouped MFMA GEMM for the input projection of all T steps, then one persistent recurrence
+that keeps W_hh on-chip for all T steps (no per-step launches, no per-step HBM traffic for
+W_hh): for small hidden sizes each workgroup carries one (model, batch row) with its W_hh
+slice in registers; for bf16 / fp16 at hidden 256 / 384 / 512, hidden / 128 workgroups
+share a (model, 16-row chunk) and exchange h_t each step.  The launches are asynchronous; a
+bounded wait of the shared recurrence that gave up is raised by
+``wide_compiler._hip.rnn_sync_check(block=True)`` or by the next recurrent call.
 """
 
 from __future__ import annotations

@@ -122,8 +122,8 @@ class WideLSTM(nn.Module):
                 ) -> Tuple[Tensor, Tuple[Tensor, Tensor]]:
         """x [N, B, T, I] -> (out [N, B, T, H], (h_n, c_n)), as wide_lstm.py:137-156.
 
-        The launch is asynchronous.  On the partitioned on-chip plan (bf16, hidden 256 /
-        384 / 512) the recurrence's cross-workgroup waits are bounded; a wait that gives up
+        The launch is asynchronous.  On the partitioned on-chip plan (bf16 or fp16, hidden
+        256 / 384 / 512) the recurrence's cross-workgroup waits are bounded; a wait that gives up
         leaves the outputs invalid and is raised by the next recurrent call or by
         ``wide_compiler._hip.rnn_sync_check(block=True)``, which a caller that must trust
         these outputs (or a graph replay of this forward) calls before reading them."""

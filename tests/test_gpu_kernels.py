@@ -375,8 +375,13 @@ def _per_step_err(out, exact):
                                        (2, 1, 3, 130, 24), (4, 2, 6, 16, 64),
                                        # fused projection: several 16-step chunks, partial last chunk
                                        (3, 2, 37, 12, 64), (2, 3, 33, 64, 128),
+                                       # bf16: partitioned on-chip recurrence (hidden / 128
+                                       # workgroups per (model, 16-row chunk)); fp32: streamed
+                                       (3, 5, 6, 24, 256), (3, 16, 9, 32, 512), (2, 33, 7, 16, 384),
+                                       # 66 x 4 workgroups: two launches of the partitioned kernel
+                                       (66, 2, 4, 8, 512),
                                        # streamed (one launch per step): W_hh beyond one workgroup
-                                       (3, 5, 6, 24, 256), (2, 20, 4, 8, 288)])
+                                       (2, 20, 4, 8, 288)])
 @pytest.mark.parametrize("with_h0", [False, True])
 def test_gru(hip, dtype, n, b, t, i, h, with_h0):
     import wide_compiler as wc
@@ -407,7 +412,10 @@ def test_gru(hip, dtype, n, b, t, i, h, with_h0):
                                        # bf16: partitioned on-chip recurrence (hidden / 128
                                        # workgroups per model); fp32: streamed
                                        (3, 16, 9, 32, 512), (2, 5, 7, 16, 256), (2, 1, 6, 24, 384),
-                                       (2, 16, 130, 32, 512)])
+                                       (2, 16, 130, 32, 512),
+                                       # batch 33: chunks of 16, 16 and 1 rows; 70 x 4 workgroups:
+                                       # two launches of the partitioned kernel
+                                       (3, 33, 6, 16, 256), (70, 3, 5, 16, 512)])
 @pytest.mark.parametrize("with_state", [False, True])
 def test_lstm(hip, dtype, n, b, t, i, h, with_state):
     import wide_compiler as wc
@@ -438,11 +446,13 @@ def test_lstm(hip, dtype, n, b, t, i, h, with_state):
 
 @pytest.mark.parametrize("cell,n,b,t,i,h", [("gru", 32, 4, 32, 64, 128), ("gru", 3, 2, 5, 8, 16),
                                              ("lstm", 3, 16, 9, 32, 512), ("lstm", 4, 3, 7, 20, 64),
-                                             ("gru", 2, 18, 5, 16, 512)])
+                                             ("gru", 2, 18, 5, 16, 512), ("lstm", 2, 20, 6, 16, 256),
+                                             ("gru", 3, 16, 9, 32, 384), ("lstm", 2, 3, 5, 8, 288)])
 def test_rnn_fp16(hip, cell, n, b, t, i, h):
     """fp16 recurrences: fp16 input projection GEMM, the persistent kernel (W_hh in registers,
-    fp32 math) for small hidden sizes, the streamed kernel (fp16 MFMA per step) for 512; the
-    per-timestep bar of fp16 at every step."""
+    fp32 math) for small hidden sizes, the partitioned on-chip kernel (fp16 MFMA) for 256 / 384 /
+    512, the streamed kernel (fp16 MFMA per step) otherwise; the per-timestep bar of fp16 at
+    every step."""
     import wide_compiler as wc
     g = gen(119)
     cls, wcls, ref = (nn.GRU, wc.WideGRU, wide_ref.gru) if cell == "gru" else (nn.LSTM, wc.WideLSTM, wide_ref.lstm)

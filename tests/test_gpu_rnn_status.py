@@ -107,3 +107,22 @@ def test_give_up_is_raised_in_every_mode(hip):
     hip.rnn_forward_noalloc(out=out, h_n=None, c_n=None, **w)
     hip.rnn_sync_check(block=True)
     assert torch.equal(out, ref_out)
+
+
+@pytest.mark.parametrize("cell,dtype,n,b,h,part", [
+    ("lstm", torch.bfloat16, 64, 16, 512, True), ("lstm", torch.bfloat16, 70, 33, 512, True),
+    ("lstm", torch.float16, 3, 20, 256, True), ("gru", torch.bfloat16, 8, 16, 512, True),
+    ("gru", torch.float16, 2, 40, 384, True), ("gru", torch.bfloat16, 4, 4, 128, False),
+    ("lstm", torch.float32, 2, 4, 512, False), ("gru", torch.bfloat16, 2, 4, 288, False)])
+def test_partitioned_plan_is_taken(hip, cell, dtype, n, b, h, part):
+    """Which sizes run the partitioned on-chip recurrence (a status word exists only there):
+    LSTM and GRU, bf16 and fp16, hidden 256 / 384 / 512, any batch and any number of models."""
+    import ctypes
+    x = torch.empty(n, b, 3, 8, device=DEV, dtype=dtype)
+    g = (4 if cell == "lstm" else 3) * h
+    a, _ = hip.rnn_args(cell=hip.CELL_LSTM if cell == "lstm" else hip.CELL_GRU, x=x,
+                        w_ih=torch.empty(n, g, 8, device=DEV, dtype=dtype),
+                        w_hh=torch.empty(n, g, h, device=DEV, dtype=dtype), b_ih=None, b_hh=None, h0=None,
+                        c0=None, out=torch.empty(n, b, 3, h, device=DEV, dtype=dtype), h_n=None, c_n=None,
+                        allocate=False)
+    assert (hip.lib().wc_rnn_status_offset(ctypes.byref(a)) >= 0) == part
