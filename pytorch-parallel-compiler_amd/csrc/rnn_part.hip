@@ -28,17 +28,21 @@
 // consecutive units of one row: its gates_x of a gate, its h_t and its state are 16-byte
 // vectors, and the cell update needs no data exchange between lanes.
 //
-// Exchange.  Each exchanged value is one 32-bit word, (16 bits of h << 16) | tag, where tag =
-// (base + t) mod 2^16 names the step; a reader polls the words it needs with device-scope
-// (sc1) loads until every tag matches, so no separate flag, store fence or extra round trip
-// is needed.  Writers use device-scope stores too, unless every part of the unit runs on one
-// XCD (read from HW_REG_XCC_ID at start), in which case plain stores into the shared L2
+// Exchange.  Every exchanged value carries the step it belongs to, so a reader polls the
+// values it needs with device-scope (sc1) loads until every tag matches, and no separate
+// flag, store fence or extra round trip is needed.  LSTM: h = o tanh(c) lies in [-1, 1], so
+// bit 14 of its 16-bit form (the top exponent bit) is free and holds a 1-bit tag; the values
+// travel 8 to a 16-byte chunk.  GRU (whose h follows h0, which may exceed 1): each value is
+// one 32-bit word, (16 bits of h << 16) | tag with a 16-bit tag.  Under load the exchange
+// costs in proportion to its bytes (the LSTM form halved a c5 step's poll round, 3.5k ->
+// 1.6k cycles).  Writers use device-scope stores too, unless every part of the unit runs on
+// one XCD (read from HW_REG_XCC_ID at start), in which case plain stores into the shared L2
 // suffice and are faster.  There are two slots per unit (step parity): a part cannot write
 // step t + 2 into a slot before every other part has read step t from it, since it needs
 // their step t + 1 first.  `base` lives in the caller's workspace: the input projection
-// zeroes it and fills the slots with tag 0xFFFF, and the last workgroup of a unit to finish
-// advances it by T, so a slot's stale tag is always 1 or 2 steps behind the one a reader
-// expects.  Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
+// zeroes it and fills the slots with all-ones words (word tag 0xFFFF, bit 14 set in every
+// 16-bit half), and the last workgroup of a unit to finish advances it by T, so a slot's
+// stale tag is always 1 or 2 steps behind the one a reader expects.  Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
 // at the first wait without polling) the workgroup records 1 in the status word and leaves
 // (the outputs are then invalid).  The status word is the caller's own when one is passed
 // (never cleared here), else a word of the workspace that the input projection zeroes.  The
@@ -62,7 +66,9 @@ constexpr int kSyncBase = 17;          //   tag of this launch's step 0
 constexpr int kSyncXcc = 20;           //   per part: (tag of step 0 << 16) | (XCD + 1)
 constexpr int kSpinLimit = 1 << 21;    // default poll rounds (each >= ~0.5 us) before giving up
 constexpr int kSc1 = 16;               // buffer-op cache policy: device scope (sc1)
-constexpr uint32_t kTagFill = 0xFFFFu;
+constexpr uint32_t kTagFill = 0xFFFFFFFFu;  // word tag 0xFFFF; both halves with bit 14 set
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 struct PartParams {
   int n, rows, chunks;  // models, batch rows, 16-row chunks per model
@@ -76,7 +82,7 @@ struct PartParams {
   void* out;            // [n, rows, steps, H]
   void* hn;             // [n, rows, H] or null
   void* cn;             // LSTM: [n, rows, H] or null
-  uint32_t* xch;        // [units][2][16][H] exchange words
+  uint32_t* xch;        // [units][2][16][H] exchange words (LSTM: 16-bit values in the first half)
   int* sync;            // [units][kSyncInts]
   int* status;          // set to 1 when a wait gave up
 };
@@ -354,7 +360,111 @@ void part_kernel(PartParams p) {
   }
 
   bf16x8 hv = {};
-  // One step's exchange with cache policy POL: write the lane's 8 values of h_t, then
+  // LSTM exchange: h_t travels as its own 16-bit values, 8 to a 16-byte chunk.  |h| =
+  // |o tanh(c)| <= 1, so bit 14 (the top exponent bit of bf16 and of fp16) is 0 in every h;
+  // it carries the tag ((g >> 1) & 1) of global step g = base + t, and the slot is g & 1, so
+  // a value left in the slot from step g - 2 always fails the check (the tag base is 16
+  // bits wide, a multiple of the period 4).  A NaN h (exponent bits all ones) travels as
+  // the code 1.5, a value no h takes, which the reader turns back into NaN.  Chunk e of this
+  // workgroup (8 values) is row e / CPR_H, slice r / 16 (skipping our own), units 8 (r % 16)
+  // onward.
+  constexpr uint32_t kTagBits = 0x40004000u;
+  constexpr bool kF16 = std::is_same<T, f16>::value;
+  constexpr uint32_t kHMax = kF16 ? 0x3C00u : 0x3F80u;      // |1.0|
+  constexpr uint32_t kHNanCode = kF16 ? 0x3E00u : 0x3FC0u;  // 1.5
+  constexpr uint32_t kHNan = kF16 ? 0x7E00u : 0x7FC0u;
+  constexpr int CPR_H = (P - 1) * kPartUnits / 8;          // remote chunks per row
+  constexpr int CPT_H = (16 * CPR_H + kPartThreads - 1) / kPartThreads;
+  auto put_h = [&](auto pol, uint32_t g, bool nan_any) {
+    constexpr int POL = decltype(pol)::value;
+    u32x4 hw = __builtin_bit_cast(u32x4, hv);
+    if (nan_any) {                                   // rare: a NaN h becomes the code
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t lo = hw[k] & 0xFFFFu, hi = hw[k] >> 16;
+        if ((lo & 0x7FFFu) > kHMax) lo = kHNanCode;
+        if ((hi & 0x7FFFu) > kHMax) hi = kHNanCode;
+        hw[k] = lo | (hi << 16);
+      }
+    }
+    const uint32_t m = ((g >> 1) & 1u) ? kTagBits : 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hw[k] |= m;
+    const uint32_t xo = (((g & 1u) * 16 + fr) * H + ucol) * 2;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, hw), xrs, xo, 0, POL);
+  };
+  auto chunk_h = [&](int k, int& b, int& col) {
+    const int e = tid + k * kPartThreads;
+    b = e / CPR_H;
+    const int r = e - b * CPR_H;
+    int q = r / (kPartUnits / 8);
+    q += (q >= part) ? 1 : 0;
+    col = q * kPartUnits + (r % (kPartUnits / 8)) * 8;
+  };
+  auto get_h = [&](uint32_t g, auto after) {
+    const uint32_t slot = (g & 1u) * 16;
+    const uint32_t want = ((g >> 1) & 1u) ? kTagBits : 0u;
+    uint32_t pending = 0;
+#pragma unroll
+    for (int k = 0; k < CPT_H; ++k) {
+      int b, col;
+      chunk_h(k, b, col);
+      if (b < nrows) pending |= 1u << k;
+    }
+    int spins = 0;
+    bool after_done = false;
+    while (pending) {
+      if (spins++ >= p.spin_limit) {
+        *abort_flag = 1;
+        break;
+      }
+      asm volatile("" ::: "memory");                 // every round issues its loads anew
+      u32x4 v[CPT_H];
+#pragma unroll
+      for (int k = 0; k < CPT_H; ++k) {
+        int b, col;
+        chunk_h(k, b, col);
+        if (pending & (1u << k))
+          v[k] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ((slot + b) * H + col) * 2, 0, kSc1));
+      }
+      if (!after_done) {
+        after();
+        after_done = true;
+      }
+#pragma unroll
+      for (int k = 0; k < CPT_H; ++k) {
+        if (!(pending & (1u << k))) continue;
+        const uint32_t any = v[k][0] | v[k][1] | v[k][2] | v[k][3];
+        const uint32_t all = v[k][0] & v[k][1] & v[k][2] & v[k][3];
+        if (want ? (all & kTagBits) != kTagBits : (any & kTagBits) != 0u) continue;
+        u32x4 hx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hx[q] = v[k][q] & ~kTagBits;
+        // the largest magnitude of the 8 values: above |1.0| only for the NaN code
+        u16x2 mx = __builtin_bit_cast(u16x2, hx[0] & 0x7FFF7FFFu);
+#pragma unroll
+        for (int q = 1; q < 4; ++q) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2, hx[q] & 0x7FFF7FFFu));
+        if (mx[0] > kHMax || mx[1] > kHMax) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint32_t lo = hx[q] & 0xFFFFu, hi = hx[q] >> 16;
+            if ((lo & 0x7FFFu) > kHMax) lo = kHNan;
+            if ((hi & 0x7FFFu) > kHMax) hi = kHNan;
+            hx[q] = lo | (hi << 16);
+          }
+        }
+        int b, col;
+        chunk_h(k, b, col);
+        *reinterpret_cast<u32x4*>(hs + b * HP + (col - u0 + H) % H) = hx;
+        pending &= ~(1u << k);
+      }
+      if (pending) __builtin_amdgcn_s_sleep(1);
+    }
+    if (!after_done) after();
+  };
+  // GRU exchange (its h may exceed 1 in magnitude when h0 does): one step's exchange with
+  // cache policy POL: write the lane's 8 values of h_t, then
   // copy the other parts' slices of h_t (rows < batch) into LDS.  Chunk e of this
   // workgroup (16 bytes = 4 exchange words) is row e / CPR, slice r / 32 (skipping our
   // own), units 4 (r % 32) onward; a thread polls its chunks in groups of PG.
@@ -381,8 +491,9 @@ void part_kernel(PartParams p) {
     q += (q >= part) ? 1 : 0;
     col = q * kPartUnits + (r % (kPartUnits / 4)) * 4;
   };
-  auto get = [&](int t, uint32_t tag) {
+  auto get = [&](int t, uint32_t tag, auto after) {
     constexpr int PG = CPT;
+    bool after_done = false;
     const uint32_t slot = static_cast<uint32_t>(t & 1) * 16;
 #pragma unroll
     for (int k0 = 0; k0 < CPT; k0 += PG) {
@@ -409,6 +520,10 @@ void part_kernel(PartParams p) {
             v[k] = __builtin_bit_cast(
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ((slot + b) * H + col) * 4, 0, kSc1));
         }
+        if (!after_done) {
+          after();
+          after_done = true;
+        }
 #pragma unroll
         for (int k = 0; k < PG; ++k) {
           if (!(pending & (1u << k))) continue;
@@ -424,6 +539,7 @@ void part_kernel(PartParams p) {
         if (pending) __builtin_amdgcn_s_sleep(1);
       }
     }
+    if (!after_done) after();
   };
 
   bool aborted = *abort_flag != 0;
@@ -443,7 +559,8 @@ void part_kernel(PartParams p) {
     // added in the cell update
     mfma_steps<T, SL, NA, XL, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
     mfma_steps<T, SL, NA, XL, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
-    // cell update of the lane's 8 units
+    // cell update of the lane's 8 units (hsum: NaN exactly when some h of the lane is)
+    float hsum = 0.f;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       if constexpr (GRU) {
@@ -461,16 +578,24 @@ void part_kernel(PartParams p) {
         const float gg = tanh_f(acc[j][2] + lane_f<T>(gxn[2], j));
         const float og = sigmoid_f(acc[j][3] + lane_f<T>(gxn[3], j));
         c[j] = fg * c[j] + ig * gg;
-        set_lane<T>(hv, j, og * tanh_f(c[j]));
+        const float h = og * tanh_f(c[j]);
+        hsum += h;
+        set_lane<T>(hv, j, h);
       }
     }
     const uint32_t tag = (base + static_cast<uint32_t>(t)) & 0xFFFFu;
     const bool more = t + 1 < p.steps;
     if (brow && more) {
-      if (local) put(std::integral_constant<int, 0>{}, t, tag);
-      else put(std::integral_constant<int, kSc1>{}, t, tag);
+      if constexpr (GRU) {
+        if (local) put(std::integral_constant<int, 0>{}, t, tag);
+        else put(std::integral_constant<int, kSc1>{}, t, tag);
+      } else {
+        const bool nan_any = !(hsum == hsum);
+        if (local) put_h(std::integral_constant<int, 0>{}, base + t, nan_any);
+        else put_h(std::integral_constant<int, kSc1>{}, base + t, nan_any);
+      }
     }
-    // the output row goes out after the exchange: vmcnt counts stores and loads in
+    // the output row goes out after the exchange loads: vmcnt counts stores and loads in
     // order, so an earlier store would hold up the exchange loads' wait
     auto put_out = [&]() {
       if (brow)
@@ -487,9 +612,15 @@ void part_kernel(PartParams p) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
     mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
-    get(t, tag);
-    put_out();
-    load_gx(t + 1);                                    // lands during the next step's MFMAs
+    // the output row and the next step's gates_x go out once the exchange loads are in
+    // flight: the cell update of step t + 1 reads gates_x between that step's MFMAs, and a
+    // load issued at the end of the step would still be on its way from HBM there
+    auto out_and_gx = [&]() {
+      put_out();
+      load_gx(t + 1);
+    };
+    if constexpr (GRU) get(t, tag, out_and_gx);
+    else get_h(base + t, out_and_gx);
     lds_barrier();
     aborted = *abort_flag != 0;
   }

@@ -467,6 +467,37 @@ def test_rnn_fp16(hip, cell, n, b, t, i, h):
     assert max(_per_step_err(out, eo)) <= 5e-3, _per_step_err(out, eo)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("h", [256, 384, 512])
+def test_lstm_nan_crosses_the_exchange(hip, dtype, h):
+    """A NaN that starts in one workgroup's units reaches the others through the exchange:
+    c0 is NaN at one unit of part 0 (model 1, row 2) and at one unit of the last part (model 2,
+    row 17, in the second 16-row chunk).  As in the reference (torch ops throughout), that
+    unit's h is NaN at t = 0 and the whole row is NaN from t = 1 on, in every part; every other
+    row stays finite and within the bar."""
+    import wide_compiler as wc
+    from wide_compiler import _hip
+    n, b, t, i = 3, 18, 6, 16
+    g = gen(131)
+    mods = _rnn_modules(nn.LSTM, n, i, h, 131, torch.float32)
+    wide = wc.WideLSTM.from_modules(mods).to(DEV, dtype)
+    x = _rand((n, b, t, i), g, dtype)
+    h0, c0 = _rand((n, b, h), g, dtype), _rand((n, b, h), g, dtype)
+    c0[1, 2, 5] = float("nan")
+    c0[2, 17, h - 3] = float("nan")
+    with torch.no_grad():
+        out, (hn, cn) = wide(x.to(DEV), (h0.to(DEV), c0.to(DEV)))
+    _hip.rnn_sync_check(block=True)
+    out = out.cpu()
+    p = [getattr(wide, k).detach().cpu().double() for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    eo, _ = wide_ref.lstm(x.double(), *p, hx=(h0.double(), c0.double()))
+    assert torch.equal(out.isnan(), eo.isnan())
+    assert out[1, 2, 0].isnan().sum() == 1 and out[1, 2, 1:].isnan().all()
+    assert out[2, 17, 0].isnan().sum() == 1 and out[2, 17, 1:].isnan().all()
+    fin = ~eo.isnan()
+    assert rel_err(out[fin], eo[fin]) <= (tol(dtype) if dtype == torch.bfloat16 else 5e-3)
+
+
 def test_gru_matches_nn_gru_per_model(hip):
     """The kernel against torch.nn.GRU itself (the reference's validation target)."""
     import wide_compiler as wc
