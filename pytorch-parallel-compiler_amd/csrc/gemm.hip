@@ -1049,9 +1049,22 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
   rd_a(0, 0, a0);
 
   auto stage = [&](int s, bool first, bool after_epi) {
+    Dma d;
 #pragma unroll
     for (int g = 0; g < 16; ++g) {
-      group(g, g < 8 ? a0 : a1, first && g < 8);
+      if (g < 14) {
+        group(g, g < 8 ? a0 : a1, first && g < 8);
+      } else {
+        // groups 14 and 15: one of stage s + 2's 8 LDS-DMA loads after each MFMA (issued
+        // back to back they stall the wave while the address unit drains them)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[g & 7][j] = mma16<TA>(wr[g & 3], a1[j], acc[g & 7][j]);
+          __builtin_amdgcn_sched_barrier(0);
+          dma_block(d, 4 * (g - 14) + j);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
       if (g == 1) rd_a(s, 1, a1);                     // a1 last fed group 15 of stage s - 1
       if (g + 4 < 16) rd_w(s, g + 4);
       if (g == 13) {
@@ -1060,17 +1073,16 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
         if (after_epi) vm_lgkm_wait<E>();
         else vm_lgkm_wait<0>();
         bare_barrier();
-        const Dma d = dma_of(s + 2);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) dma_block(d, q);
+        rd_a(s + 1, 0, a0);                           // a0 last fed group 7
         rd_w(s + 1, 0);
         rd_w(s + 1, 1);
-        rd_a(s + 1, 0, a0);                           // a0 last fed group 7
+        d = dma_of(s + 2);
       }
       if (g == 14) rd_w(s + 1, 2);
       if (g == 15) rd_w(s + 1, 3);
     }
   };
+
   for (int ti = 0; ti < my_tiles; ++ti) {
     stage(ti * KS, true, ti > 0);
     for (int ks = 1; ks < KS; ++ks) stage(ti * KS + ks, false, false);
