@@ -41,8 +41,10 @@
 // step t + 2 into a slot before every other part has read step t from it, since it needs
 // their step t + 1 first.  `base` lives in the caller's workspace: the input projection
 // zeroes it and fills the slots with all-ones words (word tag 0xFFFF, bit 14 set in every
-// 16-bit half), and the last workgroup of a unit to finish advances it by T, so a slot's
-// stale tag is always 1 or 2 steps behind the one a reader expects.  Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
+// 16-bit half), and the last workgroup of a unit to finish advances it by T.  So a stale
+// LSTM value is always exactly 2 steps old (every step is published, the last one of a launch
+// included, and the tag base is 16 bits wide, a multiple of the tag's period 4), and a stale
+// GRU word 1 or 2 steps behind the one a reader expects.  Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
 // at the first wait without polling) the workgroup records 1 in the status word and leaves
 // (the outputs are then invalid).  The status word is the caller's own when one is passed
 // (never cleared here), else a word of the workspace that the input projection zeroes.  The
@@ -364,7 +366,9 @@ void part_kernel(PartParams p) {
   // |o tanh(c)| <= 1, so bit 14 (the top exponent bit of bf16 and of fp16) is 0 in every h;
   // it carries the tag ((g >> 1) & 1) of global step g = base + t, and the slot is g & 1, so
   // a value left in the slot from step g - 2 always fails the check (the tag base is 16
-  // bits wide, a multiple of the period 4).  A NaN h (exponent bits all ones) travels as
+  // bits wide, a multiple of the period 4).  A value from step g - 4 would pass: hence every
+  // step is published, a launch's last one included, and a slot never holds one that old.
+  // A NaN h (exponent bits all ones) travels as
   // the code 1.5, a value no h takes, which the reader turns back into NaN.  Chunk e of this
   // workgroup (8 values) is row e / CPR_H, slice r / 16 (skipping our own), units 8 (r % 16)
   // onward.
@@ -585,15 +589,18 @@ void part_kernel(PartParams p) {
     }
     const uint32_t tag = (base + static_cast<uint32_t>(t)) & 0xFFFFu;
     const bool more = t + 1 < p.steps;
-    if (brow && more) {
-      if constexpr (GRU) {
+    if constexpr (GRU) {
+      if (brow && more) {
         if (local) put(std::integral_constant<int, 0>{}, t, tag);
         else put(std::integral_constant<int, kSc1>{}, t, tag);
-      } else {
-        const bool nan_any = !(hsum == hsum);
-        if (local) put_h(std::integral_constant<int, 0>{}, base + t, nan_any);
-        else put_h(std::integral_constant<int, kSc1>{}, base + t, nan_any);
       }
+    } else if (brow) {
+      // the last step is published too, although no part of this launch reads it: the
+      // 1-bit tag repeats every 4 steps, so the next launch's step 1 (global step B + 1 with
+      // B = base + steps) must find B - 1 in its slot, two steps old, not B - 3
+      const bool nan_any = !(hsum == hsum);
+      if (local) put_h(std::integral_constant<int, 0>{}, base + t, nan_any);
+      else put_h(std::integral_constant<int, kSc1>{}, base + t, nan_any);
     }
     // the output row goes out after the exchange loads: vmcnt counts stores and loads in
     // order, so an earlier store would hold up the exchange loads' wait

@@ -126,3 +126,33 @@ def test_partitioned_plan_is_taken(hip, cell, dtype, n, b, h, part):
                         c0=None, out=torch.empty(n, b, 3, h, device=DEV, dtype=dtype), h_n=None, c_n=None,
                         allocate=False)
     assert (hip.lib().wc_rnn_status_offset(ctypes.byref(a)) >= 0) == part
+
+
+def test_partitioned_lstm_repeated_launches_bit_identical(hip):
+    """The partitioned LSTM at the sequence workload's size (64 models x 16 rows = 256
+    workgroups, hidden 512, bf16), its recurrence launched four more times on the same gates
+    without re-preparing the workspace (the exchange tag base advances across launches, the
+    slots keep the previous launch's last values), then a whole forward again: every launch's
+    output equals the first forward's bit for bit.  Tolerance tests cannot see a race in the
+    h_t exchange that changes a few values; this one does."""
+    from wide_compiler import _hip
+    n, b, t, i, h = 64, 16, 128, 256, 512
+    wide = _wide_lstm(n, i, h, 631)
+    x = _x((n, b, t, i), 632)
+    with torch.no_grad():
+        ref, _ = wide(x)
+        _hip.rnn_sync_check(block=True)
+        ref = ref.clone()
+        out = torch.empty_like(ref)
+        a, ws = _hip.rnn_args(cell=_hip.CELL_LSTM, x=x, w_ih=wide.weight_ih, w_hh=wide.weight_hh,
+                              b_ih=wide.bias_ih, b_hh=wide.bias_hh, h0=None, c0=None, out=out, h_n=None,
+                              c_n=None, status=_hip.rnn_status_word(x.device))
+        _hip.rnn_phase(a, "input_projection", x)
+        for k in range(4):
+            out.fill_(float("nan"))
+            _hip.rnn_phase(a, "recurrence", x)
+            _hip.rnn_sync_check(block=True)
+            assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"launch {k}"
+        again, _ = wide(x)
+        _hip.rnn_sync_check(block=True)
+    assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
