@@ -191,6 +191,12 @@ __device__ __forceinline__ void set_lane(bf16x8& v, int j, float x) {
   }
 }
 
+// gates i, f, g, o of the lane's unit j from the four gates_x vectors, as an accumulator
+template <typename T>
+__device__ __forceinline__ f32x4 gx_acc(const bf16x8* gx, int j) {
+  return f32x4{lane_f<T>(gx[0], j), lane_f<T>(gx[1], j), lane_f<T>(gx[2], j), lane_f<T>(gx[3], j)};
+}
+
 // LDS-only barrier: waits for this wave's LDS traffic, not for its global loads and
 // stores, which stay in flight across it
 __device__ __forceinline__ void lds_barrier() {
@@ -553,14 +559,22 @@ void part_kernel(PartParams p) {
   const bf16x8* wlw = wl + w * NF * 64 + lane;       // this lane's LDS fragments
   const bf16* hrow = hs + fr * HP + g * 8;           // this lane's h columns
   f32x4 acc[NT];
+  // LSTM: the accumulators start from gates_x, which frees its registers a whole step
+  // before the next cell update, so gates_x of step t + 1 is loaded at the top of step t,
+  // ahead of every exchange load of the step (vmcnt retires loads in order: a load issued
+  // behind the exchange polls would hold up every poll round after the first).  GRU keeps
+  // gates_x apart from the hidden part of n, so it loads one step ahead in the exchange.
 #pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NT; ++j) acc[j] = GRU ? f32x4{0.f, 0.f, 0.f, 0.f} : gx_acc<T>(gxn, j);
   mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);
   for (int t = 0; t < p.steps && !aborted; ++t) {
+    if constexpr (!GRU) {
+      if (t + 1 < p.steps) load_gx(t + 1);
+    }
     // gate slots = h_{t-1} W_hh^T (MFMA; own columns already in acc), in two tile groups,
     // so that the cell update of the first group can run between the second group's MFMAs
     // (the h fragments are read once per group); gates_x (x W_ih^T + the folded biases) is
-    // added in the cell update
+    // the LSTM's starting accumulator and joins the GRU's gates in the cell update
     mfma_steps<T, SL, NA, XL, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
     mfma_steps<T, SL, NA, XL, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
     // cell update of the lane's 8 units (hsum: NaN exactly when some h of the lane is)
@@ -576,11 +590,11 @@ void part_kernel(PartParams p) {
         c[j] = (1.0f - zg) * nn + zg * c[j];
         set_lane<T>(hv, j, c[j]);
       } else {
-        // i, f, g, o in acc[j][0..3]
-        const float ig = sigmoid_f(acc[j][0] + lane_f<T>(gxn[0], j));
-        const float fg = sigmoid_f(acc[j][1] + lane_f<T>(gxn[1], j));
-        const float gg = tanh_f(acc[j][2] + lane_f<T>(gxn[2], j));
-        const float og = sigmoid_f(acc[j][3] + lane_f<T>(gxn[3], j));
+        // i, f, g, o in acc[j][0..3], gates_x included
+        const float ig = sigmoid_f(acc[j][0]);
+        const float fg = sigmoid_f(acc[j][1]);
+        const float gg = tanh_f(acc[j][2]);
+        const float og = sigmoid_f(acc[j][3]);
         c[j] = fg * c[j] + ig * gg;
         const float h = og * tanh_f(c[j]);
         hsum += h;
@@ -617,17 +631,24 @@ void part_kernel(PartParams p) {
     *reinterpret_cast<bf16x8*>(hs + fr * HP + (ucol - u0)) = hv;
     lds_barrier();                                     // this part's h_t is in LDS
 #pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NT; ++j) acc[j] = GRU ? f32x4{0.f, 0.f, 0.f, 0.f} : gx_acc<T>(gxn, j);
     mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
-    // the output row and the next step's gates_x go out once the exchange loads are in
-    // flight: the cell update of step t + 1 reads gates_x between that step's MFMAs, and a
-    // load issued at the end of the step would still be on its way from HBM there
+    // the output row (and the GRU's next gates_x) go out once the exchange loads are in
+    // flight: the GRU's cell update of step t + 1 reads gates_x between that step's MFMAs,
+    // and a load issued at the end of the step would still be on its way from HBM there
     auto out_and_gx = [&]() {
       put_out();
-      load_gx(t + 1);
+      if constexpr (GRU) load_gx(t + 1);
     };
-    if constexpr (GRU) get(t, tag, out_and_gx);
-    else get_h(base + t, out_and_gx);
+    if constexpr (GRU) {
+      get(t, tag, out_and_gx);
+    } else {
+      get_h(base + t, out_and_gx);
+      // every exchange load has been checked by now; an explicit vmcnt(0) tells the
+      // compiler so (it counts the conditional poll loads as possibly in flight and would
+      // otherwise wait for the next step's gates_x loads at the step's first LDS read)
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0) expcnt(7) lgkmcnt(15)
+    }
     lds_barrier();
     aborted = *abort_flag != 0;
   }
