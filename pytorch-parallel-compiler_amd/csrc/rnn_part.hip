@@ -91,25 +91,31 @@ struct PartParams {
 
 std::atomic<int> g_spin_limit{kSpinLimit};
 
-// Where the (k-step s, row tile j) fragments of W_hh live: s < SL in LDS, s < SL + NA in
-// AGPRs, tiles j < XL of k-step SL + NA in LDS as well, the rest in VGPRs.
+// Where the (storage slot q, row tile j) fragments of W_hh live: q < SL in LDS, q < SL + NA
+// in AGPRs, tiles j < XL of slot SL + NA in LDS as well, the rest in VGPRs.  k-step k (in the
+// rotated order, this part's own columns first) is kept in slot (k + SH) % KS.  The LSTM
+// takes SH = SL, so its own k-steps are register-fed: they run between the exchange store and
+// the exchange poll, where nothing hides an LDS read per MFMA, while the non-own k-steps run
+// beside the cell update (1-2 % per step); the GRU keeps SH = 0 (with SH = SL its H = 512
+// form spills).
 template <int H> struct PartCfg;
 template <> struct PartCfg<256> { static constexpr int SL = 0, NA = 6, XL = 0; };
 template <> struct PartCfg<384> { static constexpr int SL = 1, NA = 8, XL = 0; };
 template <> struct PartCfg<512> { static constexpr int SL = 4, NA = 8, XL = 3; };
 
-// The order in which the k-steps B..E-1 are visited: LDS-fed k-steps (s < SL, and SL + NA
-// when XL > 0) alternate with register-fed ones, so the fragments of the next LDS-fed
-// k-step are read while the MFMAs of a register-fed k-step run.
-template <int SL, int NA, int XL, int B, int E>
+// The order in which the k-steps B..E-1 are visited (s: k-step, q: its storage slot):
+// LDS-fed k-steps (q < SL, and SL + NA when XL > 0) alternate with register-fed ones, so the
+// fragments of the next LDS-fed k-step are read while the MFMAs of a register-fed k-step run.
+template <int SL, int NA, int XL, int KS, int SH, int B, int E>
 struct KOrder {
-  int s[E - B];
+  int s[E - B], q[E - B];
   bool lds[E - B];
-  constexpr KOrder() : s(), lds() {
+  constexpr KOrder() : s(), q(), lds() {
     int ls[E - B] = {}, rs[E - B] = {};
     int nl = 0, nr = 0;
     for (int k = B; k < E; ++k) {
-      if (k < SL || (XL > 0 && k == SL + NA)) ls[nl++] = k;
+      const int qk = (k + SH) % KS;
+      if (qk < SL || (XL > 0 && qk == SL + NA)) ls[nl++] = k;
       else rs[nr++] = k;
     }
     int o = 0, il = 0, ir = 0;
@@ -117,49 +123,51 @@ struct KOrder {
       if (il < nl) { s[o] = ls[il++]; lds[o++] = true; }
       if (ir < nr) { s[o] = rs[ir++]; lds[o++] = false; }
     }
+    for (int i = 0; i < E - B; ++i) q[i] = (s[i] + SH) % KS;
   }
 };
 
 // acc[j] += the k-steps B..E-1 of (W_hh rows of tile j) x h^T for the tiles J0 <= j < J1:
 // A fragments from LDS (wlw, this lane's fragment base), AGPRs (wa) or VGPRs (wv); B fragments
 // from this lane's h row in LDS (hrow, k-step s at hrow + 32 s).
-template <typename T, int SL, int NA, int XL, int B, int E, int J0, int J1, int NT, int RA, int RV>
+template <typename T, int SL, int NA, int XL, int KS, int SH, int B, int E, int J0, int J1, int NT, int RA,
+          int RV>
 __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[NT], const bf16x8 (&wa)[RA][NT],
                                            const bf16x8 (&wv)[RV][NT], const bf16x8* wlw, const bf16* hrow) {
   static_assert(0 <= J0 && J0 < J1 && J1 <= NT, "tile range");
-  constexpr KOrder<SL, NA, XL, B, E> ord;
+  constexpr KOrder<SL, NA, XL, KS, SH, B, E> ord;
   constexpr int N = E - B;
   bf16x8 lf[NT];                                     // LDS-fed fragments of the current / next k-step
-  auto in_lds = [](int s, int j) { return s < SL || (XL > 0 && s == SL + NA && j < XL); };
-  auto load_tile = [&](int s, int j) {
-    if (s < SL) lf[j] = wlw[(s * NT + j) * 64];
-    else if (in_lds(s, j)) lf[j] = wlw[(SL * NT + j) * 64];
+  auto in_lds = [](int q, int j) { return q < SL || (XL > 0 && q == SL + NA && j < XL); };
+  auto load_tile = [&](int q, int j) {
+    if (q < SL) lf[j] = wlw[(q * NT + j) * 64];
+    else if (in_lds(q, j)) lf[j] = wlw[(SL * NT + j) * 64];
   };
   bf16x8 hb = *reinterpret_cast<const bf16x8*>(hrow + ord.s[0] * 32);
   if (ord.lds[0]) {
 #pragma unroll
-    for (int j = J0; j < J1; ++j) load_tile(ord.s[0], j);
+    for (int j = J0; j < J1; ++j) load_tile(ord.q[0], j);
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const int s = ord.s[i];
+    const int q = ord.q[i];
     const bool nxt_lds = i + 1 < N && ord.lds[i + 1];
     const bf16x8 hc = hb;
     if (i + 1 < N) hb = *reinterpret_cast<const bf16x8*>(hrow + ord.s[i + 1] * 32);
     // a register-fed k-step: read all of the next LDS-fed k-step's fragments under its MFMAs
     if (!ord.lds[i] && nxt_lds) {
 #pragma unroll
-      for (int j = J0; j < J1; ++j) load_tile(ord.s[i + 1], j);
+      for (int j = J0; j < J1; ++j) load_tile(ord.q[i + 1], j);
     }
 #pragma unroll
     for (int j = J0; j < J1; ++j) {
       bf16x8 a;
-      if (in_lds(s, j)) a = lf[j];
-      else if (s < SL + NA) a = wa[s < SL + NA ? s - SL : 0][j];
-      else a = wv[s < SL + NA ? 0 : s - SL - NA][j];
+      if (in_lds(q, j)) a = lf[j];
+      else if (q < SL + NA) a = wa[q < SL + NA ? q - SL : 0][j];
+      else a = wv[q < SL + NA ? 0 : q - SL - NA][j];
       acc[j] = mma16<T>(a, hc, acc[j]);
       // two LDS-fed k-steps in a row: refill tile j once its MFMA has taken it
-      if (ord.lds[i] && nxt_lds) load_tile(ord.s[i + 1], j);
+      if (ord.lds[i] && nxt_lds) load_tile(ord.q[i + 1], j);
     }
   }
 }
@@ -217,6 +225,7 @@ void part_kernel(PartParams p) {
   constexpr int NT = 8, KS = H / 32, P = H / kPartUnits;
   constexpr int SL = PartCfg<H>::SL, NA = PartCfg<H>::NA, XL = PartCfg<H>::XL, NV = KS - SL - NA;
   static_assert(NV >= 0 && P >= 2, "partition");
+  constexpr int SH = GRU ? 0 : SL;                   // W_hh storage slot of k-step k: (k + SH) % KS
   constexpr int HP = H + 8;                          // LDS pitch of an h row (elements)
   constexpr int G = (GRU ? 3 : 4) * H;
   constexpr int NG = GRU ? 3 : 4;                    // gates_x vectors a lane reads per step
@@ -261,7 +270,7 @@ void part_kernel(PartParams p) {
       const bf16* row = wb + static_cast<int64_t>(slot * H + u0 + w * 32 + (fr >> 2) * 8 + j) * H + g * 8;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const bf16* src = row + ((s + part * KPP) % KS) * 32;   // rotated k-step s
+        const bf16* src = row + ((s + KS - SH + part * KPP) % KS) * 32;   // slot s: rotated k-step s - SH
         if (s < SL) {
           wl[(w * NF + s * NT + j) * 64 + lane] = *reinterpret_cast<const bf16x8*>(src);
         } else if (s < SL + NA) {
@@ -566,7 +575,7 @@ void part_kernel(PartParams p) {
   // gates_x apart from the hidden part of n, so it loads one step ahead in the exchange.
 #pragma unroll
   for (int j = 0; j < NT; ++j) acc[j] = GRU ? f32x4{0.f, 0.f, 0.f, 0.f} : gx_acc<T>(gxn, j);
-  mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);
+  mfma_steps<T, SL, NA, XL, KS, SH, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);
   for (int t = 0; t < p.steps && !aborted; ++t) {
     if constexpr (!GRU) {
       if (t + 1 < p.steps) load_gx(t + 1);
@@ -575,8 +584,8 @@ void part_kernel(PartParams p) {
     // so that the cell update of the first group can run between the second group's MFMAs
     // (the h fragments are read once per group); gates_x (x W_ih^T + the folded biases) is
     // the LSTM's starting accumulator and joins the GRU's gates in the cell update
-    mfma_steps<T, SL, NA, XL, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
-    mfma_steps<T, SL, NA, XL, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
+    mfma_steps<T, SL, NA, XL, KS, SH, KPP, KS, 0, NT / 2>(acc, wa, wv, wlw, hrow);
+    mfma_steps<T, SL, NA, XL, KS, SH, KPP, KS, NT / 2, NT>(acc, wa, wv, wlw, hrow);
     // cell update of the lane's 8 units (hsum: NaN exactly when some h of the lane is)
     float hsum = 0.f;
 #pragma unroll
@@ -616,8 +625,9 @@ void part_kernel(PartParams p) {
       if (local) put_h(std::integral_constant<int, 0>{}, base + t, nan_any);
       else put_h(std::integral_constant<int, kSc1>{}, base + t, nan_any);
     }
-    // the output row goes out after the exchange loads: vmcnt counts stores and loads in
-    // order, so an earlier store would hold up the exchange loads' wait
+    // the output row goes out after the exchange loads (GRU: behind the first poll round;
+    // LSTM: once the exchange is complete): vmcnt counts stores and loads in order, so an
+    // earlier store would hold up the exchange loads' waits
     auto put_out = [&]() {
       if (brow)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, hv), ors,
@@ -632,22 +642,23 @@ void part_kernel(PartParams p) {
     lds_barrier();                                     // this part's h_t is in LDS
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = GRU ? f32x4{0.f, 0.f, 0.f, 0.f} : gx_acc<T>(gxn, j);
-    mfma_steps<T, SL, NA, XL, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
-    // the output row (and the GRU's next gates_x) go out once the exchange loads are in
-    // flight: the GRU's cell update of step t + 1 reads gates_x between that step's MFMAs,
-    // and a load issued at the end of the step would still be on its way from HBM there
+    mfma_steps<T, SL, NA, XL, KS, SH, 0, KPP, 0, NT>(acc, wa, wv, wlw, hrow);   // own columns of step t + 1
+    // GRU: the output row and the next gates_x go out once the exchange loads are in flight:
+    // the cell update of step t + 1 reads gates_x between that step's MFMAs, and a load
+    // issued at the end of the step would still be on its way from HBM there
     auto out_and_gx = [&]() {
       put_out();
-      if constexpr (GRU) load_gx(t + 1);
+      load_gx(t + 1);
     };
     if constexpr (GRU) {
       get(t, tag, out_and_gx);
     } else {
-      get_h(base + t, out_and_gx);
+      get_h(base + t, [] {});
       // every exchange load has been checked by now; an explicit vmcnt(0) tells the
       // compiler so (it counts the conditional poll loads as possibly in flight and would
       // otherwise wait for the next step's gates_x loads at the step's first LDS read)
       __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0) expcnt(7) lgkmcnt(15)
+      put_out();
     }
     lds_barrier();
     aborted = *abort_flag != 0;
