@@ -57,7 +57,10 @@ def _rel(a, b) -> float:
 def _event_time(fn: Callable[[], None], k: int, w: int) -> float:
     """Average seconds per call of fn (kernel launches on torch's current stream): k calls are
     captured back to back into one HIP graph, so host dispatch does not enter the figure, and
-    the replay is bracketed by HIP events recorded on the stream the graph runs on."""
+    each replay is bracketed by HIP events recorded on the stream the graph runs on.  The
+    graph is replayed until about 40 ms of GPU work have run (the clock climbs for ~25 ms
+    after the GPU idles, e.g. during the capture), then 7 more times; the figure is the
+    median of those 7."""
     import torch
     for _ in range(max(w, 1)):
         fn()
@@ -66,14 +69,22 @@ def _event_time(fn: Callable[[], None], k: int, w: int) -> float:
     with torch.cuda.graph(graph):
         for _ in range(k):
             fn()
-    graph.replay()                      # warm replay
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    graph.replay()
-    e1.record(st)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / k * 1e-3
+
+    def replay() -> float:
+        e0.record(st)
+        graph.replay()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e-3
+
+    warm = 0.0
+    for _ in range(200):                # warm replays
+        warm += replay()
+        if warm >= 0.04:
+            break
+    return _median([replay() for _ in range(7)]) / k
 
 
 def _step_times(fn: Callable[[], None], k: int, flush=None) -> list:
