@@ -342,7 +342,8 @@ int32_t wc_mlp2(const wc_mlp2_args* args, void* stream);
  * for c < c_in and 0 for c_in <= c < Ci32 (c_in rounded up to 32).  w is the grouped
  * filter bank [n*c_out, c_in, kh, kw] of WideConv2d.grouped_conv / WideConv1d.op
  * (wide_conv2d.py:149-158, wide_conv1d.py:85-94).  out holds
- * wc_conv_packed_weight_elems(...) elements of `dtype`, 16-byte aligned.
+ * wc_conv_packed_weight_elems(...) elements of `dtype`, 16-byte aligned (-1 for sizes that
+ * are negative, a non-positive c_in / kh / kw, or a count that does not fit in int64).
  */
 int32_t wc_conv_pack_weights(const void* w, int64_t n, int64_t c_out, int64_t c_in, int64_t kh,
                              int64_t kw, int32_t dtype, void* out, void* stream);

@@ -1040,9 +1040,9 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
   WC_REQUIRE(a->q && a->k && a->v && a->o, WC_ERR_NULL, "wc_attention: null pointer");
   const int es = dtype_size(a->dtype);
   const bool al = aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 16) &&
-                  (a->q_stride_nb * es) % 16 == 0 && (a->q_stride_s * es) % 16 == 0 &&
-                  (a->k_stride_nb * es) % 16 == 0 && (a->k_stride_s * es) % 16 == 0 &&
-                  (a->v_stride_nb * es) % 16 == 0 && (a->v_stride_s * es) % 16 == 0;
+                  ubytes(a->q_stride_nb, es) % 16 == 0 && ubytes(a->q_stride_s, es) % 16 == 0 &&
+                  ubytes(a->k_stride_nb, es) % 16 == 0 && ubytes(a->k_stride_s, es) % 16 == 0 &&
+                  ubytes(a->v_stride_nb, es) % 16 == 0 && ubytes(a->v_stride_s, es) % 16 == 0;
   WC_REQUIRE(al, WC_ERR_ALIGN, "wc_attention: q/k/v rows must be 16-byte aligned");
   WC_REQUIRE(a->sq < 0x7fffffffll && a->skv < 0x7fffffffll && a->nb < 0x7fffffffll, WC_ERR_LIMIT,
              "wc_attention: sizes too large");
@@ -1078,7 +1078,7 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
   if (!p.mask && a->dtype == WC_BF16 && (a->head_dim == 32 || a->head_dim == 64)) {
     // resident-KV kernel: K and V of one head in LDS, 8-byte aligned output rows
     const int skvp = static_cast<int>(cdiv(a->skv, 32) * 32);
-    const bool o_al = aligned(a->o, 8) && (a->o_stride_nb * es) % 8 == 0 && (a->o_stride_s * es) % 8 == 0;
+    const bool o_al = aligned(a->o, 8) && ubytes(a->o_stride_nb, es) % 8 == 0 && ubytes(a->o_stride_s, es) % 8 == 0;
     if (o_al && res_lds_bytes((int)a->head_dim, skvp) <= 150 * 1024) {
       const bool w8 = a->sq > 256;
       if (a->head_dim == 32)
@@ -1106,7 +1106,7 @@ extern "C" int32_t wc_self_attention(const wc_self_attn_args* a, void* stream) {
              static_cast<long long>(a->s), static_cast<long long>(a->d_model));
   if (a->n == 0 || a->b == 0 || a->s == 0) return WC_OK;
   WC_REQUIRE(a->x && a->q_weight && a->kv_weight && a->o, WC_ERR_NULL, "wc_self_attention: null pointer");
-  WC_REQUIRE(a->n * a->b < 0x7fffffffll && a->x_stride_n >= 0 && a->x_stride_b >= 0 && a->x_stride_s >= 0 &&
+  WC_REQUIRE(mul_sat({a->n, a->b}) < 0x7fffffffll && a->x_stride_n >= 0 && a->x_stride_b >= 0 && a->x_stride_s >= 0 &&
                  a->o_stride_nb >= 0 && a->o_stride_s >= 0 && a->q_weight_stride_n >= 0 &&
                  a->kv_weight_stride_n >= 0 && a->q_bias_stride_n >= 0 && a->kv_bias_stride_n >= 0,
              WC_ERR_ARG, "wc_self_attention: negative stride or too many rows");

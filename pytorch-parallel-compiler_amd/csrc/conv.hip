@@ -1306,6 +1306,9 @@ extern "C" int32_t wc_conv_pack_weights(const void* w, int64_t n, int64_t c_out,
   WC_REQUIRE(n >= 0 && c_out >= 0 && c_in > 0 && kh > 0 && kw > 0, WC_ERR_SHAPE, "wc_conv_pack_weights: bad sizes");
   if (n == 0 || c_out == 0) return WC_OK;
   WC_REQUIRE(w && out, WC_ERR_NULL, "wc_conv_pack_weights: null pointer");
+  // one thread per packed element, in a grid of at most 2^31 workgroups
+  WC_REQUIRE(c_in < 0x7fffffe0ll && mul_sat({n, c_out, kh, kw, c_in + 31}) < (int64_t{1} << 39), WC_ERR_LIMIT,
+             "wc_conv_pack_weights: sizes too large");
   const int ci32 = round32(static_cast<int>(c_in));
   const int64_t total = n * c_out * kh * kw * ci32;
   const dim3 grid(static_cast<uint32_t>(cdiv(total, 256)));
@@ -1325,14 +1328,19 @@ extern "C" int32_t wc_conv_pack_weights(const void* w, int64_t n, int64_t c_out,
 }
 
 extern "C" int64_t wc_conv_packed_weight_elems(int64_t n, int64_t c_out, int64_t c_in, int64_t kh, int64_t kw) {
-  return n * c_out * kh * kw * round32(static_cast<int>(c_in));
+  if (n < 0 || c_out < 0 || c_in <= 0 || kh <= 0 || kw <= 0 || c_in >= 0x7fffffe0ll) return -1;
+  const int64_t e = mul_sat({n, c_out, kh, kw, round32(static_cast<int>(c_in))});
+  return e == INT64_MAX ? -1 : e;
 }
 
 extern "C" int32_t wc_conv2d_direct_weights(const wc_conv_args* a) {
   if (!a || a->dtype != WC_BF16 || !a->weight || a->n <= 0 || a->batch <= 0 || a->c_out <= 0 || a->h <= 0 ||
       a->w <= 0 || a->stride_h <= 0 || a->stride_w <= 0 || a->dil_h <= 0 || a->dil_w <= 0)
     return 0;
-  if (a->c_in * a->h * a->w >= 0x7fffffffll || a->n * a->c_out >= 0x7fffffffll) return 0;
+  if (!fits_i32({a->n, a->batch, a->c_in, a->c_out, a->h, a->w, a->kh, a->kw, a->stride_h, a->stride_w,
+                 a->pad_h, a->pad_w, a->dil_h, a->dil_w, a->h_out, a->w_out}) ||
+      mul_sat({a->c_in, a->h, a->w}) >= 0x7fffffffll || mul_sat({a->n, a->c_out}) >= 0x7fffffffll)
+    return 0;
   ConvParams p = {};
   p.ci = (int)a->c_in;
   p.co = (int)a->c_out;
@@ -1372,6 +1380,9 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
                  a->kh > 0 && a->kw > 0 && a->stride_h > 0 && a->stride_w > 0 && a->pad_h >= 0 &&
                  a->pad_w >= 0 && a->dil_h > 0 && a->dil_w > 0,
              WC_ERR_SHAPE, "wc_conv2d: bad sizes");
+  WC_REQUIRE(fits_i32({a->n, a->batch, a->c_in, a->c_out, a->h, a->w, a->kh, a->kw, a->stride_h, a->stride_w,
+                       a->pad_h, a->pad_w, a->dil_h, a->dil_w}),
+             WC_ERR_LIMIT, "wc_conv2d: sizes too large");
   const int64_t ho = (a->h + 2 * a->pad_h - a->dil_h * (a->kh - 1) - 1) / a->stride_h + 1;
   const int64_t wo = (a->w + 2 * a->pad_w - a->dil_w * (a->kw - 1) - 1) / a->stride_w + 1;
   WC_REQUIRE(ho == a->h_out && wo == a->w_out, WC_ERR_SHAPE,
@@ -1379,8 +1390,8 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
              (long long)a->w_out, (long long)ho, (long long)wo);
   if (a->n == 0 || a->batch == 0 || a->c_out == 0 || ho <= 0 || wo <= 0) return WC_OK;
   WC_REQUIRE(a->x && a->y && (a->packed_weight || a->weight), WC_ERR_NULL, "wc_conv2d: null pointer");
-  WC_REQUIRE(a->c_in * a->h * a->w < 0x7fffffffll && a->c_out * ho * wo < 0x7fffffffll &&
-                 a->n * a->c_out < 0x7fffffffll,
+  WC_REQUIRE(mul_sat({a->c_in, a->h, a->w}) < 0x7fffffffll && mul_sat({a->c_out, ho, wo}) < 0x7fffffffll &&
+                 mul_sat({a->n, a->c_out}) < 0x7fffffffll,
              WC_ERR_LIMIT, "wc_conv2d: sizes too large");
   ConvParams p;
   p.n = (int)a->n;
@@ -1434,8 +1445,8 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   p.tiles_co = static_cast<int>(cdiv(p.co, 64));
   const int es = f32 ? 4 : 2;
   const int ve = 16 / es;
-  const bool yal = aligned(p.y, 16) && (p.y_sn * es) % 16 == 0 && (p.y_sb * es) % 16 == 0;
-  const bool ral = !p.res || (aligned(p.res, 16) && (p.r_sn * es) % 16 == 0 && (p.r_sb * es) % 16 == 0);
+  const bool yal = aligned(p.y, 16) && ubytes(p.y_sn, es) % 16 == 0 && ubytes(p.y_sb, es) % 16 == 0;
+  const bool ral = !p.res || (aligned(p.res, 16) && ubytes(p.r_sn, es) % 16 == 0 && ubytes(p.r_sb, es) % 16 == 0);
   p.vec_out = (yal && ral && p.tc % ve == 0 && p.wo % ve == 0) ? 1 : 0;
   if (p.wn) {
     // the filter bank itself: only the resident-weight kernel reads that layout
@@ -1459,7 +1470,7 @@ extern "C" int32_t wc_conv2d(const wc_conv_args* a, void* stream) {
   }
   // fast path: weights and input chunk both staged in LDS (bf16, stride 1, W % 8 == 0)
   if (!f32 && !f16m && p.sh == 1 && p.sw == 1 && p.kh * p.kw <= kFastTaps && p.w % 8 == 0 && aligned(p.x, 16) &&
-      (p.x_sn * es) % 16 == 0 && (p.x_sb * es) % 16 == 0 && (static_cast<int64_t>(p.h) * p.w * es) % 16 == 0) {
+      ubytes(p.x_sn, es) % 16 == 0 && ubytes(p.x_sb, es) % 16 == 0 && (static_cast<int64_t>(p.h) * p.w * es) % 16 == 0) {
     ConvParams q = p;
     if (conv_fast_plan(q)) {
       q.tiles_r = static_cast<int>(cdiv(q.ho, q.tr));
@@ -1504,6 +1515,9 @@ extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
                  a->kd > 0 && a->kh > 0 && a->kw > 0 && a->stride_d > 0 && a->stride_h > 0 && a->stride_w > 0 &&
                  a->pad_d >= 0 && a->pad_h >= 0 && a->pad_w >= 0 && a->dil_d > 0 && a->dil_h > 0 && a->dil_w > 0,
              WC_ERR_SHAPE, "wc_conv3d: bad sizes");
+  WC_REQUIRE(fits_i32({a->n, a->batch, a->c_in, a->c_out, a->d, a->h, a->w, a->kd, a->kh, a->kw, a->stride_d,
+                       a->stride_h, a->stride_w, a->pad_d, a->pad_h, a->pad_w, a->dil_d, a->dil_h, a->dil_w}),
+             WC_ERR_LIMIT, "wc_conv3d: sizes too large");
   const int64_t dout = (a->d + 2 * a->pad_d - a->dil_d * (a->kd - 1) - 1) / a->stride_d + 1;
   const int64_t ho = (a->h + 2 * a->pad_h - a->dil_h * (a->kh - 1) - 1) / a->stride_h + 1;
   const int64_t wo = (a->w + 2 * a->pad_w - a->dil_w * (a->kw - 1) - 1) / a->stride_w + 1;
@@ -1512,8 +1526,9 @@ extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
              (long long)a->h_out, (long long)a->w_out, (long long)dout, (long long)ho, (long long)wo);
   if (a->n == 0 || a->batch == 0 || a->c_out == 0 || dout <= 0 || ho <= 0 || wo <= 0) return WC_OK;
   WC_REQUIRE(a->x && a->packed_weight && a->y, WC_ERR_NULL, "wc_conv3d: null pointer");
-  WC_REQUIRE(a->c_in * a->d * a->h * a->w < 0x7fffffffll && a->c_out * dout * ho * wo < 0x7fffffffll &&
-                 a->n * a->c_out < 0x7fffffffll && a->kd * a->kh * a->kw < 0x10000,
+  WC_REQUIRE(mul_sat({a->c_in, a->d, a->h, a->w}) < 0x7fffffffll &&
+                 mul_sat({a->c_out, dout, ho, wo}) < 0x7fffffffll && mul_sat({a->n, a->c_out}) < 0x7fffffffll &&
+                 mul_sat({a->kd, a->kh, a->kw}) < 0x10000,
              WC_ERR_LIMIT, "wc_conv3d: sizes too large");
   ConvParams p;
   p.n = (int)a->n;
@@ -1566,8 +1581,8 @@ extern "C" int32_t wc_conv3d(const wc_conv3d_args* a, void* stream) {
   p.tiles_co = static_cast<int>(cdiv(p.co, 64));
   const int es = f32 ? 4 : 2;
   const int ve = 16 / es;
-  const bool yal = aligned(p.y, 16) && (p.y_sn * es) % 16 == 0 && (p.y_sb * es) % 16 == 0 &&
-                   (p.y_cs * es) % 16 == 0 && (static_cast<int64_t>(p.ho) * p.wo * es) % 16 == 0;
+  const bool yal = aligned(p.y, 16) && ubytes(p.y_sn, es) % 16 == 0 && ubytes(p.y_sb, es) % 16 == 0 &&
+                   ubytes(p.y_cs, es) % 16 == 0 && (static_cast<int64_t>(p.ho) * p.wo * es) % 16 == 0;
   p.vec_out = (yal && p.tc % ve == 0 && p.wo % ve == 0) ? 1 : 0;
   WC_REQUIRE(aligned(p.wp, 16), WC_ERR_ALIGN, "wc_conv3d: packed weights not 16-byte aligned");
   const int64_t nblk = static_cast<int64_t>(p.n) * p.batch * p.dout * p.tiles_r * p.tiles_c * p.tiles_co;

@@ -1178,11 +1178,11 @@ bool xl_shape_ok(const GemmParams& p) {
   const int64_t es = sizeof(TC);
   if (p.k % 64 != 0 || p.m % 16 != 0 || p.o % 16 != 0 || p.a_ri.d % 16 != 0 || p.c_ri.d % 16 != 0) return false;
   if (p.a_so < 0 || p.a_si < 0 || p.c_so < 0 || p.c_si < 0 || p.r_so < 0 || p.r_si < 0) return false;
-  const bool c_ok = common_vec_bytes({reinterpret_cast<uintptr_t>(p.c), static_cast<uint64_t>(p.c_sn * es),
-                                      static_cast<uint64_t>(p.c_so * es), static_cast<uint64_t>(p.c_si * es)}) >= 16;
-  const bool r_ok = !p.r || common_vec_bytes({reinterpret_cast<uintptr_t>(p.r), static_cast<uint64_t>(p.r_sn * es),
-                                              static_cast<uint64_t>(p.r_so * es),
-                                              static_cast<uint64_t>(p.r_si * es)}) >= 16;
+  const bool c_ok = common_vec_bytes({reinterpret_cast<uintptr_t>(p.c), ubytes(p.c_sn, es),
+                                      ubytes(p.c_so, es), ubytes(p.c_si, es)}) >= 16;
+  const bool r_ok = !p.r || common_vec_bytes({reinterpret_cast<uintptr_t>(p.r), ubytes(p.r_sn, es),
+                                              ubytes(p.r_so, es),
+                                              ubytes(p.r_si, es)}) >= 16;
   if (!c_ok || !r_ok) return false;
   const int64_t lim = 0x7fffffffll;
   const int64_t a_end = xl_span(p, p.a_so, p.a_si, p.a_ri.d, p.k) * 2;
@@ -1218,9 +1218,9 @@ int32_t grouped_gemm(const GemmParams& p0, int32_t dtype, int32_t out_dtype, int
   GemmParams p = p0;
   const int es = dtype_size(dtype);
   const bool vec = common_vec_bytes({reinterpret_cast<uintptr_t>(p.a), reinterpret_cast<uintptr_t>(p.w),
-                                     static_cast<uint64_t>(p.k * es), static_cast<uint64_t>(p.a_sn * es),
-                                     static_cast<uint64_t>(p.a_so * es), static_cast<uint64_t>(p.a_si * es),
-                                     static_cast<uint64_t>(p.w_sn * es)}) >= 16;
+                                     ubytes(p.k, es), ubytes(p.a_sn, es),
+                                     ubytes(p.a_so, es), ubytes(p.a_si, es),
+                                     ubytes(p.w_sn, es)}) >= 16;
   if (dtype == WC_F32) {
     if (out_dtype != WC_F32 || (p.bias && bias_dtype != WC_F32))
       return set_error(WC_ERR_DTYPE, "wc_grouped_gemm: f32 inputs need f32 output and bias");
@@ -1267,6 +1267,8 @@ extern "C" int32_t wc_grouped_gemm(const wc_gemm_args* g, void* stream) {
              WC_ERR_LIMIT, "wc_grouped_gemm: sizes too large");
   WC_REQUIRE(g->a_rows_inner > 0 && g->c_rows_inner > 0, WC_ERR_ARG,
              "wc_grouped_gemm: rows_inner must be positive");
+  WC_REQUIRE(g->a_rows_inner < 0x7fffffffll && g->c_rows_inner < 0x7fffffffll, WC_ERR_LIMIT,
+             "wc_grouped_gemm: rows_inner too large");
   WC_REQUIRE(g->residual == nullptr || g->out_dtype == g->dtype || g->out_dtype == WC_F32,
              WC_ERR_DTYPE, "wc_grouped_gemm: residual dtype");
   GemmParams p;

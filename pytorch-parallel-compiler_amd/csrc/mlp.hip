@@ -316,12 +316,14 @@ extern "C" int32_t wc_mlp2(const wc_mlp2_args* a, void* stream) {
   if (a->n == 0 || a->m == 0) return WC_OK;
   WC_REQUIRE(a->x && a->w1 && a->w2 && a->y, WC_ERR_NULL, "wc_mlp2: null pointer");
   WC_REQUIRE(a->x_rows_inner > 0 && a->y_rows_inner > 0, WC_ERR_ARG, "wc_mlp2: rows_inner must be positive");
+  WC_REQUIRE(a->x_rows_inner < 0x7fffffffll && a->y_rows_inner < 0x7fffffffll, WC_ERR_LIMIT,
+             "wc_mlp2: rows_inner too large");
   WC_REQUIRE(a->m < 0x7fffffffll && a->n < 0x7fffffffll, WC_ERR_LIMIT, "wc_mlp2: sizes too large");
   const int es = dtype_size(a->dtype);
   WC_REQUIRE(common_vec_bytes({reinterpret_cast<uintptr_t>(a->x), reinterpret_cast<uintptr_t>(a->w1),
-                               reinterpret_cast<uintptr_t>(a->w2), static_cast<uint64_t>(a->x_stride_n * es),
-                               static_cast<uint64_t>(a->x_stride_outer * es),
-                               static_cast<uint64_t>(a->x_stride_inner * es)}) >= 16,
+                               reinterpret_cast<uintptr_t>(a->w2), ubytes(a->x_stride_n, es),
+                               ubytes(a->x_stride_outer, es),
+                               ubytes(a->x_stride_inner, es)}) >= 16,
              WC_ERR_ALIGN, "wc_mlp2: x / weight rows must be 16-byte aligned");
   MlpParams p;
   p.n = (int)a->n;

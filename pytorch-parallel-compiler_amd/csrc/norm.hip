@@ -301,9 +301,9 @@ int32_t launch_layernorm(const void* x, int64_t xms, int64_t xrs, const void* g,
   const int es = sizeof(T);
   const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(y),
                                    reinterpret_cast<uintptr_t>(g), reinterpret_cast<uintptr_t>(b),
-                                   static_cast<uint64_t>(dim * es),
-                                   static_cast<uint64_t>(xms * es), static_cast<uint64_t>(xrs * es),
-                                   static_cast<uint64_t>(yms * es), static_cast<uint64_t>(yrs * es),
+                                   ubytes(dim, es),
+                                   ubytes(xms, es), ubytes(xrs, es),
+                                   ubytes(yms, es), ubytes(yrs, es),
                                    static_cast<uint64_t>(dim * sizeof(P))});
   const bool vec_ok = vb >= 16;
   if (vec_ok && dim % VMAX == 0 && dim <= 4 * 64 * VMAX) {
@@ -351,7 +351,7 @@ int32_t launch_emb_layernorm(const void* w, int64_t n, int64_t vocab, int64_t di
   const int es = sizeof(T);
   const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(w), reinterpret_cast<uintptr_t>(y),
                                    reinterpret_cast<uintptr_t>(g), reinterpret_cast<uintptr_t>(b),
-                                   static_cast<uint64_t>(dim * es), static_cast<uint64_t>(dim * sizeof(P))});
+                                   ubytes(dim, es), static_cast<uint64_t>(dim * sizeof(P))});
   if (!(vb >= 16 && dim % VMAX == 0 && dim <= 4 * 64 * VMAX))
     return set_error(WC_ERR_LIMIT, "wc_embedding_layernorm: dim %lld or alignment outside the fused kernel "
                      "(16-byte rows, dim a multiple of %d up to %d)", static_cast<long long>(dim), VMAX,
@@ -388,13 +388,13 @@ int32_t launch_bn(const void* x, int64_t xsn, int64_t xsb, const void* w, const 
   constexpr int VMAX = 16 / sizeof(T);
   const int es = sizeof(T);
   const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(x), reinterpret_cast<uintptr_t>(y),
-                                   static_cast<uint64_t>(hw * es), static_cast<uint64_t>(xsn * es),
-                                   static_cast<uint64_t>(xsb * es)});
+                                   ubytes(hw, es), ubytes(xsn, es),
+                                   ubytes(xsb, es)});
   const int v = (vb >= 16) ? VMAX : 1;
-  const uint64_t planes = static_cast<uint64_t>(n * b * c);
+  const uint64_t planes = static_cast<uint64_t>(mul_sat({n, b, c}));
   const uint64_t cpp = static_cast<uint64_t>(hw / v);
-  const uint64_t total = planes * cpp;
-  if (total >= 0x7fffffffull) return set_error(WC_ERR_LIMIT, "wc_bn_eval: tensor too large");
+  const uint64_t total = static_cast<uint64_t>(mul_sat({static_cast<int64_t>(planes), static_cast<int64_t>(cpp)}));
+  if (total >= 0x7fffffffull || cpp == 0) return set_error(WC_ERR_LIMIT, "wc_bn_eval: tensor too large");
   const dim3 grid(static_cast<uint32_t>(cdiv(total, kNormBlock)));
   const FastDiv fcpp = make_fastdiv(static_cast<uint32_t>(cpp));
   const FastDiv fc = make_fastdiv(static_cast<uint32_t>(c));
@@ -569,9 +569,9 @@ int32_t launch_gn(const void* x, void* y, const void* w, const void* b, int64_t 
                   int64_t s, int64_t groups, float eps, int act, hipStream_t st) {
   constexpr int VMAX = 16 / sizeof(T);
   const int64_t cpg = c / groups;
-  const int64_t r = cpg * s;
-  const int64_t rows = n * bt * groups;
-  if (r >= 0x7fffffffll || rows >= 0x7fffffffll || s >= 0x7fffffffll || n * c >= 0x7fffffffll)
+  const int64_t r = mul_sat({cpg, s});
+  const int64_t rows = mul_sat({n, bt, groups});
+  if (r >= 0x7fffffffll || rows >= 0x7fffffffll || s >= 0x7fffffffll || mul_sat({n, c}) >= 0x7fffffffll)
     return set_error(WC_ERR_LIMIT, "wc_group_norm: tensor too large");
   GnParams p;
   p.rows = static_cast<uint32_t>(rows);
@@ -607,7 +607,7 @@ extern "C" int32_t wc_layernorm(const void* x, int64_t x_model_stride, int64_t x
   WC_REQUIRE(n >= 0 && rows_per_model >= 0 && dim >= 0, WC_ERR_SHAPE, "wc_layernorm: negative size");
   if (n == 0 || rows_per_model == 0 || dim == 0) return WC_OK;
   WC_REQUIRE(x && y && gamma, WC_ERR_NULL, "wc_layernorm: null pointer");
-  WC_REQUIRE(n * rows_per_model < 0x7fffffffll, WC_ERR_LIMIT, "wc_layernorm: too many rows");
+  WC_REQUIRE(mul_sat({n, rows_per_model}) < 0x7fffffffll, WC_ERR_LIMIT, "wc_layernorm: too many rows");
   hipStream_t st = as_stream(stream);
   if (dtype == WC_F32 && param_dtype == WC_F32)
     return launch_layernorm<float, float>(x, x_model_stride, x_row_stride, gamma, beta, y,
@@ -634,7 +634,7 @@ extern "C" int32_t wc_embedding_layernorm(const void* weight, int64_t n, int64_t
              "wc_embedding_layernorm: negative size");
   if (n == 0 || rows == 0 || dim == 0) return WC_OK;
   WC_REQUIRE(weight && ids && gamma && out, WC_ERR_NULL, "wc_embedding_layernorm: null pointer");
-  WC_REQUIRE(rows < 0x7fffffffll && n * rows < 0x7fffffffll, WC_ERR_LIMIT,
+  WC_REQUIRE(rows < 0x7fffffffll && mul_sat({n, rows}) < 0x7fffffffll, WC_ERR_LIMIT,
              "wc_embedding_layernorm: too many rows");
   hipStream_t st = as_stream(stream);
   const int shared = ids_shared ? 1 : 0;

@@ -230,8 +230,8 @@ extern "C" int32_t wc_embedding_gather(const void* weight, int64_t n, int64_t vo
              "wc_embedding_gather: negative size");
   if (n == 0 || rows == 0 || dim == 0) return WC_OK;
   WC_REQUIRE(weight && ids && out, WC_ERR_NULL, "wc_embedding_gather: null pointer");
-  WC_REQUIRE(rows < 0x7fffffffll && n * rows < 0x7fffffffll, WC_ERR_LIMIT,
-             "wc_embedding_gather: too many rows");
+  WC_REQUIRE(rows < 0x7fffffffll && mul_sat({n, rows}) < 0x7fffffffll && dim < (int64_t{1} << 40),
+             WC_ERR_LIMIT, "wc_embedding_gather: too many rows");
   const int64_t row_bytes = dim * es;
   const int vb = common_vec_bytes({reinterpret_cast<uintptr_t>(weight),
                                    reinterpret_cast<uintptr_t>(out),

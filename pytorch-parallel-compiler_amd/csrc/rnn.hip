@@ -549,6 +549,22 @@ static bool rnn_plan(int gates, int hid, RnnParams& p) {
   return best >= 0;
 }
 
+// every size in int32 range and every buffer of the problem (states, gates_x, x; counted in
+// 8-byte elements) addressable in int64 bytes; the size arithmetic below runs only on such args
+static bool rnn_sizes_fit(const wc_rnn_args* a) {
+  const int64_t lim = 0x7fffffffll;
+  if (a->n < 0 || a->batch < 0 || a->steps < 0 || a->hidden < 0 || a->input_size < 0) return false;
+  if (a->n > lim || a->batch > lim || a->steps > lim || a->hidden > lim || a->input_size > lim) return false;
+  int64_t nb, rows, e;
+  if (__builtin_mul_overflow(a->n, a->batch, &nb) || __builtin_mul_overflow(nb, 4 * a->hidden, &e) ||
+      __builtin_mul_overflow(e, int64_t{8}, &e))
+    return false;                                    // h0 / c0 / h_n / c_n and the cell state
+  if (__builtin_mul_overflow(nb, a->steps, &rows)) return false;
+  if (__builtin_mul_overflow(rows, 4 * a->hidden, &e) || __builtin_mul_overflow(e, int64_t{8}, &e)) return false;
+  if (__builtin_mul_overflow(rows, a->input_size, &e) || __builtin_mul_overflow(e, int64_t{8}, &e)) return false;
+  return true;
+}
+
 static int64_t rnn_ws_bytes(const wc_rnn_args* a) {
   if (part_plan(a)) return part_workspace_bytes(a);
   const int64_t gates = a->cell == WC_CELL_GRU ? 3 : 4;
@@ -605,12 +621,12 @@ static int32_t streamed_recurrence(const wc_rnn_args* a, const RnnParams& rp, hi
 }
 
 extern "C" int64_t wc_rnn_workspace_bytes(const wc_rnn_args* a) {
-  if (!a || a->n < 0 || a->batch < 0 || a->steps < 0 || a->hidden < 0) return -1;
+  if (!a || !rnn_sizes_fit(a)) return -1;
   return rnn_ws_bytes(a);
 }
 
 extern "C" int64_t wc_rnn_status_offset(const wc_rnn_args* a) {
-  if (!a || a->n < 0 || a->batch < 0 || a->steps < 0 || a->hidden < 0) return -1;
+  if (!a || !rnn_sizes_fit(a)) return -1;
   return part_plan(a) ? part_status_offset(a) : -1;
 }
 
@@ -625,8 +641,8 @@ static int32_t rnn_check(const wc_rnn_args* a, const char* what, RnnParams& p, i
   WC_REQUIRE(a->n >= 0 && a->batch >= 0 && a->steps >= 0 && a->input_size > 0 && a->hidden > 0,
              WC_ERR_SHAPE, "%s: bad sizes", what);
   gates = a->cell == WC_CELL_GRU ? 3 : 4;
-  WC_REQUIRE(a->n * a->batch < 0x7fffffffll && a->batch * a->steps < 0x7fffffffll &&
-                 gates * a->hidden < 0x7fffffffll && a->input_size < 0x7fffffffll,
+  WC_REQUIRE(rnn_sizes_fit(a) && a->n * a->batch < 0x7fffffffll && a->batch * a->steps < 0x7fffffffll &&
+                 gates * a->hidden < 0x7fffffffll,
              WC_ERR_LIMIT, "%s: sizes too large", what);
   p.n = (int)a->n;
   p.batch = (int)a->batch;
@@ -709,7 +725,7 @@ static int32_t persistent_recurrence(const wc_rnn_args* a, RnnParams p, int gate
   if (p.xt > p.steps) p.xt = p.steps;
   const int threads = round_up(((p.hid + p.upg - 1) / p.upg) * p.lg, 64);
   const int es = dtype_size(a->dtype);
-  p.wvec = (aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && (p.kl * es) % 16 == 0) ? 1 : 0;
+  p.wvec = (aligned(a->w_hh, 16) && ubytes(p.hid, es) % 16 == 0 && ubytes(p.kl, es) % 16 == 0) ? 1 : 0;
   const dim3 grid(nwg), block(threads);
   const size_t lds = fixed + per_step * static_cast<size_t>(p.xt);
   if (a->dtype == WC_F32) {
@@ -736,7 +752,7 @@ extern "C" int32_t wc_rnn_recurrence(const wc_rnn_args* a, void* stream) {
   if (!rnn_plan(gates, p.hid, p)) {
     // W_hh of one model does not fit a workgroup's registers: one launch per step
     const int es = dtype_size(a->dtype);
-    WC_REQUIRE(aligned(a->w_hh, 16) && (p.hid * es) % 16 == 0 && p.hid % 32 == 0 &&
+    WC_REQUIRE(aligned(a->w_hh, 16) && ubytes(p.hid, es) % 16 == 0 && p.hid % 32 == 0 &&
                    (!a->h0 || aligned(a->h0, 16)) && aligned(a->out, 16),
                WC_ERR_ALIGN, "wc_rnn_recurrence: hidden=%d needs hidden %% 32 == 0 and 16-byte aligned "
                "W_hh / h0 / out for the streamed recurrence", p.hid);

@@ -31,6 +31,26 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// elements * element size as unsigned bytes, for alignment tests of caller strides: the value
+// mod 16 is exact however large the stride (unsigned arithmetic wraps by definition)
+inline uint64_t ubytes(int64_t elems, int es) { return static_cast<uint64_t>(elems) * static_cast<uint64_t>(es); }
+
+// every value within int32 range: checked before sizes enter derived arithmetic
+inline bool fits_i32(std::initializer_list<int64_t> f) {
+  for (int64_t x : f)
+    if (x < -0x7fffffffll || x > 0x7fffffffll) return false;
+  return true;
+}
+
+// product of sizes known to be >= 0, saturated at INT64_MAX: a limit check on it fails for
+// sizes whose product does not fit instead of comparing a wrapped value
+inline int64_t mul_sat(std::initializer_list<int64_t> f) {
+  int64_t r = 1;
+  for (int64_t x : f)
+    if (__builtin_mul_overflow(r, x, &r)) return INT64_MAX;
+  return r;
+}
+
 inline int dtype_size(int32_t dt) {
   switch (dt) {
     case WC_F32: return 4;
@@ -125,9 +145,16 @@ struct FastDiv {
   uint32_t d, mul, shift;
 };
 
+// d > 0 (entry points reject zero divisors; d == 0 gives a divisor that divides nothing
+// rather than a host division by zero)
 inline FastDiv make_fastdiv(uint32_t d) {
   FastDiv f;
   f.d = d;
+  if (d == 0) {
+    f.mul = 0;
+    f.shift = 0;
+    return f;
+  }
   uint32_t s = 0;
   while ((1ull << s) < d) ++s;
   f.shift = s;

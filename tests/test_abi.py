@@ -75,6 +75,41 @@ def test_gemm_arg_checks(hip):
     assert hip.lib().wc_grouped_gemm(ctypes.byref(g), None) == -6
 
 
+def test_oversized_arguments_rejected_without_overflow(hip):
+    """Sizes whose products do not fit are rejected, not wrapped (cases the sanitizer probe
+    found: tests/test_abi_sanitized.py)."""
+    lib = hip.lib()
+    big = (1 << 63) - 1
+    # packed filter count: -1 for sizes that cannot be counted
+    assert lib.wc_conv_packed_weight_elems(1, 64, 64, 3, 3) == 64 * 9 * 64
+    assert lib.wc_conv_packed_weight_elems(big, big, 64, 3, 3) == -1
+    assert lib.wc_conv_packed_weight_elems(1, 1, (1 << 31) - 1, 1, 1) == -1
+    # workspace of a problem with zero steps whose state buffers (n * batch * hidden) overflow
+    a = hip._RnnArgs()
+    a.cell, a.dtype = hip.CELL_LSTM, hip.F32
+    a.n, a.batch, a.steps, a.input_size, a.hidden = 7 * ((1 << 31) - 1), 1, 0, 8, (1 << 31) - 1
+    assert lib.wc_rnn_workspace_bytes(ctypes.byref(a)) == -1
+    # a rows_inner of 2^32 was truncated to a zero divisor on the host (a SIGFPE)
+    g = hip._GemmArgs()
+    g.dtype = g.out_dtype = g.bias_dtype = hip.F32
+    g.n, g.m, g.o, g.k = 1, 4, 4, 4
+    g.a = g.w = g.c = 16
+    g.a_rows_inner, g.c_rows_inner = 1 << 32, 4
+    assert lib.wc_grouped_gemm(ctypes.byref(g), None) == -5
+    assert "rows_inner" in hip.last_error()
+    # row counts whose product overflows int64
+    assert lib.wc_layernorm(16, 0, 0, 16, 16, 16, 0, 0, 1 << 62, 4, 8, ctypes.c_float(1e-5), hip.F32, hip.F32,
+                            None) == -5
+    # conv geometry beyond int32 (the output size formula itself would overflow)
+    c = hip._ConvArgs()
+    c.dtype = c.param_dtype = hip.F32
+    c.n, c.batch, c.c_in, c.c_out, c.h, c.w, c.kh, c.kw = 1, 1, 4, 4, 8, 8, 3, 3
+    c.stride_h = c.stride_w = c.dil_w = 1
+    c.dil_h = big
+    c.x = c.y = c.packed_weight = 16
+    assert lib.wc_conv2d(ctypes.byref(c), None) == -5
+
+
 def test_empty_problems_are_noops(hip):
     lib = hip.lib()
     assert lib.wc_swap01(None, 0, 5, 0, 0, 16, None, None) == 0
