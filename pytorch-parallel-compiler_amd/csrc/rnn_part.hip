@@ -3,11 +3,12 @@
 // W_hh of one model (G x H 16-bit values, G = 4H for the LSTM: 2 MB at H = 512) exceeds one
 // compute unit's registers and LDS, so P = H / 128 workgroups share a model, one per compute
 // unit, for all T steps.  Workgroup `part` owns hidden units [128 part, 128 part + 128) and
-// the gate rows of W_hh that feed them, held on-chip for the whole sequence: the first SL
-// k-steps (32 columns each) in LDS, the next NA in AGPRs (loaded there directly and read in
-// place as MFMA A operands), the rest in VGPRs.  This file is built with
-// -amdgpu-mfma-vgpr-form so that accumulators live in VGPRs and the AGPR file is left to
-// the weights.
+// the gate rows of W_hh that feed them, held on-chip for the whole sequence, k-step by
+// k-step (32 columns each) in storage slots: the first SL slots in LDS, the next NA in AGPRs
+// (loaded there directly and read in place as MFMA A operands), the rest in VGPRs; k-step k
+// sits in slot (k + SH) % KS, where the LSTM's SH = SL puts its own k-steps in registers.
+// This file is built with -amdgpu-mfma-vgpr-form so that accumulators live in VGPRs and the
+// AGPR file is left to the weights.
 //
 // The work is split into units of (model, chunk of up to 16 batch rows): batch rows of a
 // recurrence are independent, so a chunk has its own cell state, exchange slots and step
@@ -15,7 +16,8 @@
 // launches in a row on the stream.
 //
 // Per step a workgroup forms its gate pre-activations for the chunk's rows as MFMA tiles
-// (A = W_hh rows, B = h_{t-1}^T read from LDS), applies the cell update in registers (the
+// (A = W_hh rows, B = h_{t-1}^T read from LDS; the LSTM's accumulators start from gates_x,
+// the GRU adds gates_x in the cell update), applies the cell update in registers (the
 // fp32 state -- the LSTM cell state, the GRU hidden state -- never leaves the chip), writes
 // h_t to the output and to an exchange slot, and copies the other parts' slices of h_t from
 // their exchange slots into its LDS.
@@ -44,8 +46,9 @@
 // 16-bit half), and the last workgroup of a unit to finish advances it by T.  So a stale
 // LSTM value is always exactly 2 steps old (every step is published, the last one of a launch
 // included, and the tag base is 16 bits wide, a multiple of the tag's period 4), and a stale
-// GRU word 1 or 2 steps behind the one a reader expects.  Every wait is bounded: past the limit (poll rounds, set by the host; 0 gives up
-// at the first wait without polling) the workgroup records 1 in the status word and leaves
+// GRU word 1 or 2 steps behind the one a reader expects.  Every wait is bounded: past the
+// limit (poll rounds, set by the host; 0 gives up at the first wait without polling) the
+// workgroup records 1 in the status word and leaves
 // (the outputs are then invalid).  The status word is the caller's own when one is passed
 // (never cleared here), else a word of the workspace that the input projection zeroes.  The
 // host launches the grid cooperatively, so all workgroups are co-resident or the launch
