@@ -6,7 +6,9 @@ kernel path is exercised across shapes as well as the kernels.  Bars (normwise):
 fp16 2e-3, bf16 2e-2; the embedding gather is bit-exact.  Reference: for every model i,
 torch.nn module i on input i (wide_linear.py, wide_conv2d.py, wide_conv1d.py,
 wide_attention.py, wide_lstm.py, wide_gru.py, the norm and embedding primitives are the
-reference's restatements of exactly these stacks)."""
+reference's restatements of exactly these stacks).  Beyond single-input modules: cross-attention
+under boolean and additive masks, recurrences from given initial states, strided input views, and
+random MLP / CNN stacks through the traced compile path."""
 
 import random
 
@@ -184,3 +186,170 @@ def test_random_embedding_bit_exact(hip):
             y = wide(ids.to(DEV), per_model=per) if per else wide(ids.to(DEV))
             ref = torch.stack([m.to(dt)(ids[q] if per else ids) for q, m in enumerate(mods)])
         assert torch.equal(y.cpu(), ref), (n, b, t, v, d, dt, per)
+
+
+def test_random_masked_cross_attention(hip):
+    """Separate query / key / value inputs of different lengths, with a boolean mask (the
+    scaled_dot_product_attention convention the reference passes through at
+    wide_attention.py:222-228: True = attend; nn.MultiheadAttention takes the complement) or an
+    additive float mask."""
+    import wide_compiler as wc
+    rng = random.Random(18)
+    torch.manual_seed(18)
+    for _ in range(CASES):
+        n, b, heads = rng.randint(1, 4), rng.randint(1, 3), rng.choice([1, 2, 4])
+        d, sq, skv = rng.choice([16, 32, 64]) * heads, rng.randint(1, 120), rng.randint(1, 120)
+        dt, kind = _dt(rng, half=False), rng.choice(["bool", "float", "none"])
+        cfg = (n, b, d, heads, sq, skv, dt, kind)
+        mods = [nn.MultiheadAttention(d, heads, batch_first=True) for _ in range(n)]
+        for m in mods:
+            nn.init.uniform_(m.in_proj_bias, -0.1, 0.1)
+        wide = wc.WideAttention.from_modules(mods).to(DEV, dt).eval()
+        q, k, v = (torch.randn(n, b, s, d).to(dt) for s in (sq, skv, skv))
+        mask, ref_mask = None, None
+        if kind == "bool":
+            mask = torch.rand(sq, skv) > 0.3
+            mask[:, 0] = True                     # every query row attends to at least one key
+            ref_mask = ~mask
+        elif kind == "float":
+            mask = torch.randn(sq, skv) * 2
+            ref_mask = mask.double()
+        with torch.no_grad():
+            y, _ = wide(q.to(DEV), k.to(DEV), v.to(DEV), attn_mask=None if mask is None else mask.to(DEV))
+            ref = torch.stack([m.double()(q[i].double(), k[i].double(), v[i].double(), need_weights=False,
+                                          attn_mask=ref_mask)[0] for i, m in enumerate(mods)])
+        _check(y, ref, dt, cfg)
+
+
+@pytest.mark.parametrize("kind", ["lstm", "gru"])
+def test_random_recurrences_with_initial_state(hip, kind):
+    """h0 (and c0) given: the final states as well as the output sequence."""
+    import wide_compiler as wc
+    from wide_compiler import _hip
+    rng = random.Random(19 if kind == "lstm" else 20)
+    torch.manual_seed(19)
+    for _ in range(CASES // 2):
+        n, b, t = rng.randint(1, 5), rng.choice([1, 3, 16, 20]), rng.randint(1, 30)
+        i, h, dt = rng.choice([8, 64, 256]), rng.choice([32, 128, 256, 512]), _dt(rng)
+        cfg = (n, b, t, i, h, dt)
+        cls, wcls = (nn.LSTM, wc.WideLSTM) if kind == "lstm" else (nn.GRU, wc.WideGRU)
+        mods = [cls(i, h, batch_first=True) for _ in range(n)]
+        wide = wcls.from_modules(mods).to(DEV, dt)
+        x = (torch.randn(n, b, t, i) * 0.5).to(dt)
+        h0, c0 = ((torch.randn(n, b, h) * 0.5).to(dt) for _ in range(2))
+        with torch.no_grad():
+            if kind == "lstm":
+                y, (hn, cn) = wide(x.to(DEV), (h0.to(DEV), c0.to(DEV)))
+                refs = [m.double()(x[q].double(), (h0[q].double()[None], c0[q].double()[None]))
+                        for q, m in enumerate(mods)]
+                _hip.rnn_sync_check(block=True)
+                _check(cn, torch.stack([r[1][1][0] for r in refs]), dt, cfg)
+                hn_ref = torch.stack([r[1][0][0] for r in refs])
+            else:
+                y, hn = wide(x.to(DEV), h0.to(DEV))
+                refs = [m.double()(x[q].double(), h0[q].double()[None]) for q, m in enumerate(mods)]
+                _hip.rnn_sync_check(block=True)
+                hn_ref = torch.stack([r[1][0] for r in refs])
+        _check(y, torch.stack([r[0] for r in refs]), dt, cfg)
+        _check(hn, hn_ref, dt, cfg)
+
+
+def test_random_strided_inputs(hip):
+    """Inputs that are views with non-unit or padded strides (a sliced feature axis, transposed
+    batch / time axes, a cropped image width)."""
+    import wide_compiler as wc
+    rng = random.Random(21)
+    torch.manual_seed(21)
+    for _ in range(CASES):
+        kind, n, b, dt = rng.choice(["linear", "conv2d", "layernorm"]), rng.randint(1, 6), rng.randint(1, 5), \
+            _dt(rng, half=False)
+        if kind == "linear":
+            i, o, t = rng.randint(1, 200), rng.randint(1, 200), rng.randint(1, 7)
+            mods = [nn.Linear(i, o) for _ in range(n)]
+            wide = wc.WideLinear.from_modules(mods).to(DEV, dt)
+            base = torch.randn(n, t, b, 2 * i).to(dt)
+            view = lambda z: z[..., ::2].transpose(1, 2)          # noqa: E731  [n, b, t, i]
+        elif kind == "conv2d":
+            c, co, hw = rng.choice([3, 8, 16]), rng.choice([4, 16]), rng.randint(3, 16)
+            mods = [nn.Conv2d(c, co, 3, padding=1) for _ in range(n)]
+            wide = wc.WideConv2d.from_modules(mods).to(DEV, dt)
+            base = torch.randn(n, b, c, hw, hw + 3).to(dt)
+            view = lambda z, hw=hw: z[..., 1:hw + 1]                # noqa: E731
+        else:
+            d, t = rng.randint(2, 300), rng.randint(1, 9)
+            mods = [nn.LayerNorm(d) for _ in range(n)]
+            wide = wc.WideLayerNorm.from_modules(mods).to(DEV, dt)
+            base = torch.randn(n, b, t, d + 5).to(dt)
+            view = lambda z, d=d: z[..., 2:d + 2]                   # noqa: E731
+        x = view(base)
+        xd = view(base.to(DEV))
+        cfg = (kind, tuple(x.shape), tuple(x.stride()), dt)
+        with torch.no_grad():
+            y = wide(xd)
+        _check(y, _stack([m.double() for m in mods], [x[q].double() for q in range(n)]), dt, cfg)
+
+
+class _RandMLP(nn.Module):
+    def __init__(self, dims, acts):
+        super().__init__()
+        self.layers = nn.ModuleList([nn.Linear(a, b) for a, b in zip(dims[:-1], dims[1:])])
+        self.acts = acts
+
+    def forward(self, x):
+        for i, layer in enumerate(self.layers):
+            x = layer(x)
+            if i + 1 < len(self.layers):
+                a = self.acts[i]
+                x = torch.relu(x) if a == "relu" else torch.nn.functional.gelu(x) if a == "gelu" else \
+                    torch.tanh(x) if a == "tanh" else x
+        return x
+
+
+class _RandCNN(nn.Module):
+    def __init__(self, c, depth, res, bn, k):
+        super().__init__()
+        self.convs = nn.ModuleList([nn.Conv2d(c, c, k, padding=k // 2) for _ in range(depth)])
+        self.bns = nn.ModuleList([nn.BatchNorm2d(c) for _ in range(depth)]) if bn else None
+        self.res = res
+
+    def forward(self, x):
+        for i, conv in enumerate(self.convs):
+            y = conv(x)
+            if self.bns is not None:
+                y = self.bns[i](y)
+            x = torch.relu(y + x) if self.res else torch.relu(y)
+        return x
+
+
+def test_random_traced_models(hip):
+    """Random MLP and CNN stacks through the public compile / pack / unpack API (the traced
+    path: api.py:36 compile, api.py:310-319 pack / unpack, core/traced_wide.py), fp32."""
+    import wide_compiler as wc
+    rng = random.Random(22)
+    torch.manual_seed(22)
+    for _ in range(CASES):
+        if rng.random() < 0.5:
+            n, depth, b = rng.randint(1, 20), rng.randint(1, 4), rng.randint(1, 40)
+            dims = [rng.choice([3, 8, 16, 32, 64, 100, 128, 256]) for _ in range(depth + 1)]
+            acts = [rng.choice(["relu", "gelu", "tanh", "none"]) for _ in range(depth)]
+            cfg = ("mlp", n, dims, acts, b)
+            models = [_RandMLP(dims, acts).to(DEV).eval() for _ in range(n)]
+            ins = [torch.randn(b, dims[0], device=DEV) for _ in range(n)]
+        else:
+            n, c, depth = rng.randint(1, 6), rng.choice([4, 8, 16, 32, 64]), rng.randint(1, 3)
+            res, bn, k, hw, b = rng.random() < 0.5, rng.random() < 0.6, rng.choice([1, 3]), rng.randint(3, 20), \
+                rng.randint(1, 3)
+            cfg = ("cnn", n, c, depth, res, bn, k, hw, b)
+            models = []
+            for _ in range(n):
+                m = _RandCNN(c, depth, res, bn, k)
+                for q in (m.bns or []):
+                    q.running_mean.uniform_(-0.5, 0.5)
+                    q.running_var.uniform_(0.5, 2.0)
+                models.append(m.to(DEV).eval())
+            ins = [torch.randn(b, c, hw, hw, device=DEV) for _ in range(n)]
+        wide = wc.compile(models, ins[0]).eval()
+        with torch.no_grad():
+            outs = wc.unpack(wide(wc.pack(ins)), n)
+            for q in range(n):
+                _check(outs[q], models[q].double()(ins[q].double()), torch.float32, cfg)
