@@ -1005,9 +1005,11 @@ __global__ __launch_bounds__(kX8Threads, 1) void gemm_xl8_kernel(GemmParams p, i
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const int lr = 8 * q + rr;
-          // non-temporal (nt): the output streams past the L2s, which keep the operand tiles
+          // non-temporal at device scope (nt | sc1): the output streams past the L2s, which keep
+          // the operand tiles (vocabulary-shape launch 1099-1101 against 1104-1111 µs with nt
+          // alone, and the kernels after it in a step find more of their operands cached)
           __builtin_amdgcn_raw_buffer_store_b128(
-              raw[q], crs, strip_ok ? cbase + static_cast<uint32_t>(lr * p.c_si) * 2u : kXlOob, 0, 2);
+              raw[q], crs, strip_ok ? cbase + static_cast<uint32_t>(lr * p.c_si) * 2u : kXlOob, 0, 18);
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);          // strip reads done before it is rewritten
         __builtin_amdgcn_wave_barrier();
