@@ -21,7 +21,10 @@ ids [64, 16, 128] uniform in [0, 8192).  --config selects another configuration 
   bf16 2516.6 TFLOP/s; HBM 8 TB/s).  "traffic" is the counter-measured HBM bytes per launch
   of that kernel (profiles/traffic_<config>.json) when one was recorded for it.
 * configs = the other configurations (value, ms per step, dominant kernel and its fraction),
-  plus "pack": the boundary pack and transpose kernels in GB/s.
+  plus "pack": the boundary pack and transpose kernels in GB/s.  Each is timed like the headline
+  but with at least 50 ms of untimed warm-up steps and at least 30 ms of timed steps (more than
+  K / W when its steps are short: the shader clock takes ~25 ms of work to ramp up after the
+  idle set-up); the step counts used are in its entry.
 * cache regimes: per-step GPU times (HIP events around each step, in the mode used) over K
   steps, median reported hot (steps back to back) and cold (a 512 MiB buffer rewritten before
   every step, so the 256 MB Infinity Cache and the L2s hold none of the step's data).
@@ -500,8 +503,11 @@ def _graph_of(step):
     return graph, same
 
 
-def _run_config(cfg: Dict, steps: int, warmup: int, mode: str) -> Dict:
-    """value / mode / parity / kernels of one configuration."""
+def _run_config(cfg: Dict, steps: int, warmup: int, mode: str, min_warm_s: float = 0.0,
+                min_timed_s: float = 0.0) -> Dict:
+    """value / mode / parity / kernels of one configuration.  With min_warm_s / min_timed_s the
+    warm-up and timed step counts are raised (never lowered) to cover that much time, from a
+    step time estimated over 3 steps."""
     import torch
     from wide_compiler import _hip
     n, b = cfg["n"], cfg["batch"]
@@ -510,6 +516,10 @@ def _run_config(cfg: Dict, steps: int, warmup: int, mode: str) -> Dict:
     # any launch or graph replay since the last check (the status word collects them all)
     parity = cfg["parity"]()
     _hip.rnn_sync_check(block=True)
+    if min_warm_s > 0 or min_timed_s > 0:
+        est = _timed(step, 3, 1) / 3
+        warmup = max(warmup, int(min_warm_s / est) + 1)
+        steps = max(steps, int(min_timed_s / est) + 1)
     eager_s = _timed(step, steps, warmup)
     _hip.rnn_sync_check(block=True)
     graph_s, graph = None, None
@@ -529,8 +539,10 @@ def _run_config(cfg: Dict, steps: int, warmup: int, mode: str) -> Dict:
         kernels = cfg["kernels"]()
     dom = max(kernels, key=lambda k: k["us_per_launch"] * k["launches_per_step"])
     return {"wall": wall, "mode": used, "eager_s": eager_s, "graph_s": graph_s, "graph": graph,
-            "parity": parity, "kernels": kernels, "dominant": dom,
-            "samples_per_s": n * b * steps / wall, "ms_per_step": wall / steps * 1e3}
+            "parity": parity, "kernels": kernels, "dominant": dom, "steps": steps, "warmup": warmup,
+            "samples_per_s": n * b * steps / wall, "ms_per_step": wall / steps * 1e3,
+            "eager_ms_per_step": eager_s / steps * 1e3,
+            "graph_ms_per_step": None if graph_s is None else graph_s / steps * 1e3}
 
 
 def _pack_leg(dev) -> Dict:
@@ -677,10 +689,13 @@ def main() -> int:
             if name == args.config:
                 continue
             c = CONFIGS[name](dev, args.steps, args.warmup)
-            rc = _run_config(c, args.steps, args.warmup, args.mode)
+            rc = _run_config(c, args.steps, args.warmup, args.mode, min_warm_s=0.05, min_timed_s=0.03)
             d = rc["dominant"]
             extra[name] = {"workload": c["name"], "value": rc["samples_per_s"], "unit": "samples/s",
                            "ms_per_step": rc["ms_per_step"], "mode": rc["mode"], "dtype": c["dtype"],
+                           "steps": rc["steps"], "warmup": rc["warmup"],
+                           "eager_ms_per_step": rc["eager_ms_per_step"],
+                           "graph_ms_per_step": rc["graph_ms_per_step"],
                            "parity_rel_err_vs_oracle": rc["parity"],
                            "roofline": {"kernel": d["kernel"], "bound": d["bound"], "achieved": d["achieved"],
                                         "peak": d["peak"], "unit": d["unit"], "frac": d["frac"],
