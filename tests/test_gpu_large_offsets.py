@@ -38,3 +38,32 @@ def test_linear_input_beyond_2gib_per_model(hip):
             assert e <= 2e-2, (q, r0, e)
     del x, y
     torch.cuda.empty_cache()
+
+
+def test_embedding_table_beyond_2gib_per_model(hip):
+    """Gather (and gather + LayerNorm in one launch) from a per-model table larger than 2^31 bytes:
+    ids past row 2^20 lie beyond the offset.  The gather is bit-exact against torch indexing
+    (wide_embedding.py:93-131), and the fused launch bit-identical to gather then LayerNorm."""
+    import wide_compiler as wc
+    n, d = 2, 1024
+    vocab = (1 << 31) // (d * 2) + 64
+    torch.manual_seed(1)
+    with torch.device("meta"):                  # no 8.6 GB fp32 table on the host
+        emb = wc.WideEmbedding(n, vocab, d)
+    emb = emb.to_empty(device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        emb.weight.normal_()
+    assert emb.weight[0].numel() * emb.weight.element_size() > (1 << 31)
+    ln = wc.WideLayerNorm.from_modules([nn.LayerNorm(d) for _ in range(n)]).to(DEV, torch.bfloat16)
+    ids = torch.randint(0, vocab, (n, 4, 64), device=DEV)
+    ids[:, :, :8] = torch.randint(vocab - 64, vocab, (n, 4, 8), device=DEV)      # past the 2^31-byte row
+    with torch.no_grad():
+        y = emb(ids, per_model=True)
+        ref = torch.stack([emb.weight[q][ids[q]] for q in range(n)])
+        assert torch.equal(y, ref)
+        y_shared = emb(ids[0])
+        assert torch.equal(y_shared, torch.stack([emb.weight[q][ids[0]] for q in range(n)]))
+        fused = emb.forward_layernorm(ids, ln, per_model=True)
+        assert torch.equal(fused, ln(y))
+    del emb, y, ref, y_shared, fused
+    torch.cuda.empty_cache()
