@@ -909,7 +909,6 @@ __global__ __launch_bounds__(W * 64, 4) void attn_qkv_kernel(QkvParams p) {   //
       }
   };
   using yes = std::integral_constant<bool, true>;
-  using no = std::integral_constant<bool, false>;
   project(0, yes{}, yes{});
   project(1, yes{}, yes{});
   __syncthreads();                                   // every wave is done with the weights

@@ -197,7 +197,6 @@ template <typename T>
 __global__ __launch_bounds__(kConvThreads) void conv_kernel(ConvParams p) {
   constexpr int FM = ConvTraits<T>::kFM;
   constexpr int PAD = ConvTraits<T>::kPad;
-  constexpr int TPIX = 4 * FM * 16;                   // pixels per tile
   extern __shared__ float4 smem4[];
   T* xs = reinterpret_cast<T*>(smem4);
   const int cip = p.cc + PAD;                         // LDS channel pitch

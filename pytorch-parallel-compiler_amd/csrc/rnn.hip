@@ -32,7 +32,6 @@
 namespace wc {
 namespace {
 
-constexpr int kRnnMaxThreads = 1024;
 constexpr int kRnnLdsBudget = 144 * 1024;   // of gfx950's 160 KB per workgroup
 
 struct RnnParams {
@@ -307,7 +306,6 @@ int32_t launch_rec(const RnnParams& p, dim3 grid, dim3 block, size_t lds, hipStr
                    p.upg, p.kl);
 }
 
-inline int round4(int v) { return (v + 3) & ~3; }
 inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 // ---------------------------------------------------------------------------
