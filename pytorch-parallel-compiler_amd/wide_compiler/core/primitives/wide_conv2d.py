@@ -18,7 +18,6 @@ from typing import List, Optional, Tuple, Union
 import torch
 from torch import Tensor, nn
 
-from ... import _hip
 from ._conv_common import conv_forward
 
 

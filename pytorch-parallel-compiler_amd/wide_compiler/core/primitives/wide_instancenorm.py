@@ -14,7 +14,7 @@ tracking would update buffers and raises (forward-only build).
 from __future__ import annotations
 
 from enum import Enum
-from typing import List, Union
+from typing import Union
 
 import torch
 from torch import Tensor, nn
