@@ -1,6 +1,7 @@
 // N-first normalisation kernels: LayerNorm with per-model affine, and
 // eval-mode BatchNorm per (model, channel).  Both are HBM-bound: one read and
-// one write of the activation, statistics in fp32 registers.
+// one write of the activation, statistics in fp32 registers (LayerNorm rows
+// longer than one wave holds are read three times by one workgroup each).
 #include "wc_common.h"
 
 namespace wc {
@@ -99,6 +100,70 @@ __global__ __launch_bounds__(kNormBlock) void layernorm_kernel(
       for (int q = 0; q < V; ++q) {
         const float bq = b ? to_f32(b[e + q]) : 0.f;
         o[q] = ((v[it][q] - mean) / denom) * to_f32(g[e + q]) + bq;
+      }
+      LoadV<T, V>::st(yr + e, o);
+    }
+  }
+}
+
+// Sum of `v` over the 256 threads of the workgroup (red: 4 floats of LDS).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = lanes_sum(v, 64);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  const float s = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();                                   // red is reused by the next reduction
+  return s;
+}
+
+// Rows longer than one wave can hold in registers: one workgroup per row (grid-stride over
+// rows), three passes over the row (mean, variance about the mean, normalise), fp32 statistics
+// and the same expression as layernorm_kernel.
+template <typename T, typename P, int V>
+__global__ __launch_bounds__(kNormBlock) void layernorm_rows_kernel(
+    const T* __restrict__ x, int64_t xms, int64_t xrs, const P* __restrict__ gamma,
+    const P* __restrict__ beta, T* __restrict__ y, int64_t yms, int64_t yrs, uint32_t rows_total,
+    FastDiv rows_per_model, int dim, float eps) {
+  static_assert(kNormBlock == 256, "block_sum assumes 4 waves");
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int nv = dim / V;                            // V divides dim
+  for (uint32_t row = blockIdx.x; row < rows_total; row += gridDim.x) {
+    const uint32_t m = fdiv(row, rows_per_model);
+    const uint32_t r = row - m * rows_per_model.d;
+    const T* xr = x + static_cast<int64_t>(m) * xms + static_cast<int64_t>(r) * xrs;
+    T* yr = y + static_cast<int64_t>(m) * yms + static_cast<int64_t>(r) * yrs;
+    const P* g = gamma + static_cast<int64_t>(m) * dim;
+    const P* b = beta ? beta + static_cast<int64_t>(m) * dim : nullptr;
+    float s = 0.f;
+    for (int i = tid; i < nv; i += kNormBlock) {
+      float v[V];
+      LoadV<T, V>::ld(xr + static_cast<int64_t>(i) * V, v);
+#pragma unroll
+      for (int q = 0; q < V; ++q) s += v[q];
+    }
+    const float mean = block_sum(s, red) / static_cast<float>(dim);
+    float s2 = 0.f;
+    for (int i = tid; i < nv; i += kNormBlock) {
+      float v[V];
+      LoadV<T, V>::ld(xr + static_cast<int64_t>(i) * V, v);
+#pragma unroll
+      for (int q = 0; q < V; ++q) {
+        const float d = v[q] - mean;
+        s2 += d * d;
+      }
+    }
+    const float var = block_sum(s2, red) / static_cast<float>(dim);
+    const float denom = sqrtf(var + eps);
+    for (int i = tid; i < nv; i += kNormBlock) {
+      const int64_t e = static_cast<int64_t>(i) * V;
+      float v[V], o[V];
+      LoadV<T, V>::ld(xr + e, v);
+#pragma unroll
+      for (int q = 0; q < V; ++q) {
+        const float bq = b ? to_f32(b[e + q]) : 0.f;
+        o[q] = ((v[q] - mean) / denom) * to_f32(g[e + q]) + bq;
       }
       LoadV<T, V>::st(yr + e, o);
     }
@@ -334,9 +399,23 @@ int32_t launch_layernorm(const void* x, int64_t xms, int64_t xrs, const void* g,
     return launch_layernorm_v<T, P, VMAX>(static_cast<const T*>(x), xms, xrs,
                                           static_cast<const P*>(g), static_cast<const P*>(b),
                                           static_cast<T*>(y), yms, yrs, n, rpm, (int)dim, eps, st);
-  return launch_layernorm_v<T, P, 1>(static_cast<const T*>(x), xms, xrs, static_cast<const P*>(g),
-                                     static_cast<const P*>(b), static_cast<T*>(y), yms, yrs, n, rpm,
-                                     (int)dim, eps, st);
+  if (!vec_ok && dim <= 16 * 64)
+    return launch_layernorm_v<T, P, 1>(static_cast<const T*>(x), xms, xrs, static_cast<const P*>(g),
+                                       static_cast<const P*>(b), static_cast<T*>(y), yms, yrs, n, rpm,
+                                       (int)dim, eps, st);
+  // longer rows: one workgroup per row (vec_ok implies VMAX divides dim)
+  const uint32_t rows_total = static_cast<uint32_t>(n * rpm);
+  const FastDiv fr = make_fastdiv(static_cast<uint32_t>(rpm));
+  const dim3 grid(rows_total < 65536u ? rows_total : 65536u);
+  if (vec_ok)
+    layernorm_rows_kernel<T, P, VMAX><<<grid, kNormBlock, 0, st>>>(
+        static_cast<const T*>(x), xms, xrs, static_cast<const P*>(g), static_cast<const P*>(b),
+        static_cast<T*>(y), yms, yrs, rows_total, fr, (int)dim, eps);
+  else
+    layernorm_rows_kernel<T, P, 1><<<grid, kNormBlock, 0, st>>>(
+        static_cast<const T*>(x), xms, xrs, static_cast<const P*>(g), static_cast<const P*>(b),
+        static_cast<T*>(y), yms, yrs, rows_total, fr, (int)dim, eps);
+  return check_launch("wc_layernorm");
 }
 
 // Embedding gather + LayerNorm in one pass: the vector-path LayerNorm kernel reading its rows
@@ -608,6 +687,7 @@ extern "C" int32_t wc_layernorm(const void* x, int64_t x_model_stride, int64_t x
   if (n == 0 || rows_per_model == 0 || dim == 0) return WC_OK;
   WC_REQUIRE(x && y && gamma, WC_ERR_NULL, "wc_layernorm: null pointer");
   WC_REQUIRE(mul_sat({n, rows_per_model}) < 0x7fffffffll, WC_ERR_LIMIT, "wc_layernorm: too many rows");
+  WC_REQUIRE(dim < 0x7fffffffll, WC_ERR_LIMIT, "wc_layernorm: dim %lld too large", static_cast<long long>(dim));
   hipStream_t st = as_stream(stream);
   if (dtype == WC_F32 && param_dtype == WC_F32)
     return launch_layernorm<float, float>(x, x_model_stride, x_row_stride, gamma, beta, y,

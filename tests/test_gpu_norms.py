@@ -139,3 +139,26 @@ def test_instance_norm_running_stats_eval(hip, kind):
         assert rel_err(y[i], mods[i].eval()(x[i])) <= tol(torch.float32)
     with torch.no_grad(), pytest.raises(RuntimeError, match="eval"):
         wide.train()(x.to(DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [1025, 2047, 4100, 8200, 20000, 65536])
+def test_layernorm_long_rows(hip, dtype, d):
+    """Rows longer than one wave holds in registers (one workgroup per row, three passes): the
+    vector form when 16-byte loads apply, the scalar one otherwise (odd widths), and a strided
+    view; against the per-model nn.LayerNorm in fp64 (wide_layernorm.py:41-67)."""
+    import wide_compiler as wc
+    n, b, t = 3, 2, 3
+    torch.manual_seed(d)
+    mods = [nn.LayerNorm(d) for _ in range(n)]
+    for m in mods:
+        nn.init.uniform_(m.weight, 0.5, 1.5)
+        nn.init.uniform_(m.bias, -0.5, 0.5)
+    wide = wc.WideLayerNorm.from_modules(mods).to(DEV, dtype)
+    base = (torch.randn(n, b, t, d + 8, device=DEV) * 2 + 0.5).to(dtype)
+    bar = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3}[dtype]
+    for x in (base[..., :d].contiguous(), base[..., 8:]):
+        with torch.no_grad():
+            y = wide(x)
+            ref = torch.stack([m.to(DEV).double()(x[q].double()) for q, m in enumerate(mods)])
+        assert rel_err(y, ref) <= bar, (d, dtype, x.is_contiguous())
