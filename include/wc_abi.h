@@ -428,7 +428,10 @@ int32_t wc_conv3d(const wc_conv3d_args* args, void* stream);
  * 215-231):  O = softmax(Q K^T * scale [+ causal mask]) V  per (n*b, head).
  * Q/K/V/O rows live at base + nb*stride_nb + s*stride_s + head*head_dim, i.e. the
  * [N*B, S, heads*head_dim] layout of the projection outputs, read in place.
- * head_dim in {16, 32, 64, 128}; dtype WC_F32, WC_BF16 or WC_F16; fp32 softmax / accumulation.
+ * dtype WC_F32, WC_BF16 or WC_F16; fp32 softmax / accumulation.  Any head_dim >= 1 up to 256
+ * (16-bit types) or 128 (fp32), else WC_ERR_LIMIT; pointers aligned to the element size (else
+ * WC_ERR_ALIGN).  Head dims 16/32/64/128 with 16-byte aligned rows run vector loads; others run
+ * element loads with the head dim zero-padded, and past 128 one launch per 128 output columns.
  */
 typedef struct wc_attn_args {
   int32_t dtype, causal;

@@ -39,6 +39,9 @@ struct AttnParams {
   // (general kernel only; NULL = none)
   const float* mask;
   int64_t m_sb, m_sh, m_sq;
+  // head dims other than the kernel's own (attn_kernel with GEN): the true head dim, and the
+  // first head-dim column of the output chunk this launch computes
+  int dh, oc0;
 };
 
 constexpr int kAttnThreads = 256;
@@ -48,28 +51,37 @@ constexpr int kBK = 64;    // keys per tile
 __device__ __forceinline__ float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, 64)); }
 __device__ __forceinline__ float xor_sum(float v, int m) { return v + __shfl_xor(v, m, 64); }
 
-template <typename T, int DH>
+// DH: the head dim of the scores (a multiple of 16, padded to 32 inside); DO: the head-dim
+// columns of V and O one launch computes (DH unless GEN).  GEN: the true head dim p.dh may be
+// any value up to DH, its rows need no alignment, and this launch computes output columns
+// [p.oc0, p.oc0 + DO) of each head: every load and store is element-wise, with the columns
+// past p.dh read as zero and not written.
+template <typename T, int DH, bool GEN = false, int DO = DH>
 __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
+  static_assert(GEN || DO == DH, "only the general form splits the output columns");
   constexpr bool BF = sizeof(T) == 2;
   constexpr int DHP = DH < 32 ? 32 : DH;       // head dim padded to the 32-wide S^T k-step
   constexpr int KP = DHP + (BF ? 8 : 4);       // K tile pitch (elements)
   constexpr int VP = kBK + (BF ? 8 : 4);       // V^T tile pitch (elements)
-  constexpr int DT = DH / 16;                  // 16-row tiles of O^T
+  constexpr int DT = DO / 16;                  // 16-row tiles of O^T
   constexpr int NKS = DHP / 32;                // 32-wide head-dim steps of S^T = K Q^T
   extern __shared__ float4 smem4[];
   T* const ks0 = reinterpret_cast<T*>(smem4);   // [2][kBK * KP]  K tiles
-  T* const vt0 = ks0 + 2 * kBK * KP;            // [2][DH * VP]   V^T tiles
+  T* const vt0 = ks0 + 2 * kBK * KP;            // [2][DO * VP]   V^T tiles
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int fr = lane & 15, g = lane >> 4;
   const int qt = blockIdx.x % p.q_tiles;
   const int bh = blockIdx.x / p.q_tiles;
   const int nb = bh / p.heads, h = bh - (bh / p.heads) * p.heads;
-  const T* qb = static_cast<const T*>(p.q) + nb * p.q_sb + h * DH;
-  const T* kb = static_cast<const T*>(p.k) + nb * p.k_sb + h * DH;
-  const T* vb = static_cast<const T*>(p.v) + nb * p.v_sb + h * DH;
-  T* ob = static_cast<T*>(p.o) + nb * p.o_sb + h * DH;
+  const int hd = GEN ? p.dh : DH;               // head stride within a row
+  const int oc0 = GEN ? p.oc0 : 0;              // first V / O column of this launch
+  const T* qb = static_cast<const T*>(p.q) + nb * p.q_sb + h * hd;
+  const T* kb = static_cast<const T*>(p.k) + nb * p.k_sb + h * hd;
+  const T* vb = static_cast<const T*>(p.v) + nb * p.v_sb + h * hd + oc0;
+  T* ob = static_cast<T*>(p.o) + nb * p.o_sb + h * hd + oc0;
   const int q0 = qt * kBQ + wave * 32;           // first query of this wave
+  const T tzero = from_f32<T>(0.f);
 
   // ---- Q^T fragments (B operand of S^T = K Q^T), kept in registers ----
   // lane supplies Q[q = q0 + nt*16 + fr][d = s*32 + g*8 .. +8] (fp32: two 16-byte halves)
@@ -80,37 +92,94 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
       const T* src = qb + q * p.q_ss + s * 32 + g * 8;
-      const bool ok = q < p.sq && s * 32 + g * 8 < DH;   // head-dim padding reads as zero
-      qf[nt][s][0] = ok ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
-      qf[nt][s][1] = (!BF && ok) ? *reinterpret_cast<const uint4*>(src + (BF ? 0 : 4)) : make_uint4(0, 0, 0, 0);
+      if constexpr (GEN) {
+        T t8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t8[j] = (q < p.sq && s * 32 + g * 8 + j < hd) ? src[j] : tzero;
+        __builtin_memcpy(&qf[nt][s][0], t8, 16);
+        if (BF) qf[nt][s][1] = make_uint4(0, 0, 0, 0);
+        else __builtin_memcpy(&qf[nt][s][1], reinterpret_cast<const char*>(t8) + 16, 16);
+      } else {
+        const bool ok = q < p.sq && s * 32 + g * 8 < DH;   // head-dim padding reads as zero
+        qf[nt][s][0] = ok ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+        qf[nt][s][1] = (!BF && ok) ? *reinterpret_cast<const uint4*>(src + (BF ? 0 : 4)) : make_uint4(0, 0, 0, 0);
+      }
     }
   }
 
-  // ---- staging of one K / V tile: each thread moves one 16-byte row piece of each ----
+  // ---- staging of one K / V tile: each thread moves 16-byte row pieces of each ----
   constexpr int VE = 16 / sizeof(T);
-  constexpr int PIECES = kBK * DH / VE;          // 16-byte pieces per tile
-  uint4 kreg[(PIECES + kAttnThreads - 1) / kAttnThreads], vreg[(PIECES + kAttnThreads - 1) / kAttnThreads];
-  constexpr int PPT = (PIECES + kAttnThreads - 1) / kAttnThreads;
-  auto fetch = [&](int k0) {
+  constexpr int KPIECES = kBK * DH / VE;         // 16-byte pieces per K tile
+  constexpr int VPIECES = kBK * DO / VE;         // and per V tile
+  constexpr int KPPT = (KPIECES + kAttnThreads - 1) / kAttnThreads;
+  constexpr int VPPT = (VPIECES + kAttnThreads - 1) / kAttnThreads;
+  uint4 kreg[KPPT], vreg[VPPT];
+  // a piece of `cols` valid columns from `src` (element-wise; the rest zero)
+  auto piece = [&](const T* src, int cols) {
+    T t[VE];
 #pragma unroll
-    for (int u = 0; u < PPT; ++u) {
-      const int e = tid + u * kAttnThreads;
-      const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
-      const bool ok = e < PIECES && k0 + key < p.skv;
-      kreg[u] = ok ? *reinterpret_cast<const uint4*>(kb + (k0 + key) * p.k_ss + c) : make_uint4(0, 0, 0, 0);
-      vreg[u] = ok ? *reinterpret_cast<const uint4*>(vb + (k0 + key) * p.v_ss + c) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < VE; ++j) t[j] = j < cols ? src[j] : tzero;
+    uint4 u;
+    __builtin_memcpy(&u, t, 16);
+    return u;
+  };
+  auto fetch = [&](int k0) {
+    if constexpr (!GEN) {
+      // K and V pieces share their (key, column) here (DO == DH)
+#pragma unroll
+      for (int u = 0; u < KPPT; ++u) {
+        const int e = tid + u * kAttnThreads;
+        const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
+        const bool ok = e < KPIECES && k0 + key < p.skv;
+        kreg[u] = ok ? *reinterpret_cast<const uint4*>(kb + (k0 + key) * p.k_ss + c) : make_uint4(0, 0, 0, 0);
+        vreg[u] = ok ? *reinterpret_cast<const uint4*>(vb + (k0 + key) * p.v_ss + c) : make_uint4(0, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < KPPT; ++u) {
+        const int e = tid + u * kAttnThreads;
+        const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
+        const bool ok = e < KPIECES && k0 + key < p.skv;
+        kreg[u] = ok ? piece(kb + (k0 + key) * p.k_ss + c, hd - c) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < VPPT; ++u) {
+        const int e = tid + u * kAttnThreads;
+        const int key = e / (DO / VE), c = (e - key * (DO / VE)) * VE;
+        const bool ok = e < VPIECES && k0 + key < p.skv;
+        vreg[u] = ok ? piece(vb + (k0 + key) * p.v_ss + c, hd - oc0 - c) : make_uint4(0, 0, 0, 0);
+      }
     }
   };
   auto stash = [&](int buf) {
+    if constexpr (!GEN) {
 #pragma unroll
-    for (int u = 0; u < PPT; ++u) {
-      const int e = tid + u * kAttnThreads;
-      if (e >= PIECES) continue;
-      const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
-      *reinterpret_cast<uint4*>(&ks0[buf * kBK * KP + key * KP + c]) = kreg[u];
-      const T* vv = reinterpret_cast<const T*>(&vreg[u]);
+      for (int u = 0; u < KPPT; ++u) {
+        const int e = tid + u * kAttnThreads;
+        if (e >= KPIECES) continue;
+        const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
+        *reinterpret_cast<uint4*>(&ks0[buf * kBK * KP + key * KP + c]) = kreg[u];
+        const T* vv = reinterpret_cast<const T*>(&vreg[u]);
 #pragma unroll
-      for (int q = 0; q < VE; ++q) vt0[buf * DH * VP + (c + q) * VP + key] = vv[q];
+        for (int q = 0; q < VE; ++q) vt0[buf * DH * VP + (c + q) * VP + key] = vv[q];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < KPPT; ++u) {
+        const int e = tid + u * kAttnThreads;
+        if (e >= KPIECES) continue;
+        const int key = e / (DH / VE), c = (e - key * (DH / VE)) * VE;
+        *reinterpret_cast<uint4*>(&ks0[buf * kBK * KP + key * KP + c]) = kreg[u];
+      }
+#pragma unroll
+      for (int u = 0; u < VPPT; ++u) {
+        const int e = tid + u * kAttnThreads;
+        if (e >= VPIECES) continue;
+        const int key = e / (DO / VE), c = (e - key * (DO / VE)) * VE;
+        const T* vv = reinterpret_cast<const T*>(&vreg[u]);
+#pragma unroll
+        for (int q = 0; q < VE; ++q) vt0[buf * DO * VP + (c + q) * VP + key] = vv[q];
+      }
     }
   };
 
@@ -143,7 +212,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
     const int k0 = kt * kBK;
     if (kt + 1 < ntiles) fetch(k0 + kBK);
     const T* kt_s = ks0 + buf * kBK * KP;
-    const T* vt_s = vt0 + buf * DH * VP;
+    const T* vt_s = vt0 + buf * DO * VP;
 
     // ---- S^T = K Q^T : [64 keys x 32 queries] per wave ----
     f32x4 sacc[4][2];
@@ -279,7 +348,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
     for (int dt = 0; dt < DT; ++dt) {
       T* dst = ob + q * p.o_ss + dt * 16 + g * 4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(acc_o[dt][nt][e] * inv);
+      for (int e = 0; e < 4; ++e)
+        if (!GEN || oc0 + dt * 16 + g * 4 + e < hd) dst[e] = from_f32<T>(acc_o[dt][nt][e] * inv);
     }
   }
 }
@@ -991,12 +1061,13 @@ int32_t launch_qkv(QkvParams p, bool causal, hipStream_t st) {
   return check_launch("wc_self_attention");
 }
 
-template <typename T, int DH>
+template <typename T, int DH, bool GEN = false, int DO = DH>
 int32_t launch_attn_dh(const AttnParams& p, dim3 grid, hipStream_t st) {
   constexpr bool BF = sizeof(T) == 2;
   constexpr size_t lds = sizeof(T) * 2 * (static_cast<size_t>(kBK) * ((DH < 32 ? 32 : DH) + (BF ? 8 : 4)) +
-                                          static_cast<size_t>(DH) * (kBK + (BF ? 8 : 4)));
-  auto kernel = attn_kernel<T, DH>;
+                                          static_cast<size_t>(DO) * (kBK + (BF ? 8 : 4)));
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto kernel = attn_kernel<T, DH, GEN, DO>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -1008,18 +1079,42 @@ int32_t launch_attn_dh(const AttnParams& p, dim3 grid, hipStream_t st) {
   return check_launch("wc_attention");
 }
 
+// Head dims 16, 32, 64 and 128 with 16-byte aligned rows take the vector form; any other head
+// dim (up to 256 for 16-bit types, 128 for fp32, whose 256-wide K tiles would not fit in LDS),
+// or unaligned rows, the general form: the head dim padded to the next of those sizes, output
+// columns in chunks of at most 128, one launch per chunk (each recomputes the scores).
 template <typename T>
-int32_t launch_attn(const AttnParams& p, int dh, hipStream_t st) {
+int32_t launch_attn(AttnParams p, int dh, bool aligned_rows, hipStream_t st) {
   const int64_t blocks = static_cast<int64_t>(p.nb) * p.heads * p.q_tiles;
   if (blocks >= 0x7fffffffll) return set_error(WC_ERR_LIMIT, "wc_attention: too many tiles");
   const dim3 grid(static_cast<uint32_t>(blocks));
-  switch (dh) {
-    case 16: return launch_attn_dh<T, 16>(p, grid, st);
-    case 32: return launch_attn_dh<T, 32>(p, grid, st);
-    case 64: return launch_attn_dh<T, 64>(p, grid, st);
-    case 128: return launch_attn_dh<T, 128>(p, grid, st);
-    default: return set_error(WC_ERR_LIMIT, "wc_attention: head dim %d unsupported (16, 32, 64, 128)", dh);
+  if (aligned_rows) {
+    switch (dh) {
+      case 16: return launch_attn_dh<T, 16>(p, grid, st);
+      case 32: return launch_attn_dh<T, 32>(p, grid, st);
+      case 64: return launch_attn_dh<T, 64>(p, grid, st);
+      case 128: return launch_attn_dh<T, 128>(p, grid, st);
+      default: break;
+    }
   }
+  constexpr int kMaxDh = sizeof(T) == 2 ? 256 : 128;
+  if (dh > kMaxDh)
+    return set_error(WC_ERR_LIMIT, "wc_attention: head dim %d above %d unsupported for %s", dh, kMaxDh,
+                     sizeof(T) == 2 ? "16-bit types" : "fp32");
+  p.dh = dh;
+  p.oc0 = 0;
+  if (dh <= 16) return launch_attn_dh<T, 16, true, 16>(p, grid, st);
+  if (dh <= 32) return launch_attn_dh<T, 32, true, 32>(p, grid, st);
+  if (dh <= 64) return launch_attn_dh<T, 64, true, 64>(p, grid, st);
+  if (dh <= 128) return launch_attn_dh<T, 128, true, 128>(p, grid, st);
+  if constexpr (sizeof(T) == 2) {
+    for (int oc0 = 0; oc0 < dh; oc0 += 128) {
+      p.oc0 = oc0;
+      const int32_t rc = launch_attn_dh<T, 256, true, 128>(p, grid, st);
+      if (rc != WC_OK) return rc;
+    }
+  }
+  return WC_OK;
 }
 
 }  // namespace
@@ -1042,7 +1137,9 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
                   ubytes(a->q_stride_nb, es) % 16 == 0 && ubytes(a->q_stride_s, es) % 16 == 0 &&
                   ubytes(a->k_stride_nb, es) % 16 == 0 && ubytes(a->k_stride_s, es) % 16 == 0 &&
                   ubytes(a->v_stride_nb, es) % 16 == 0 && ubytes(a->v_stride_s, es) % 16 == 0;
-  WC_REQUIRE(al, WC_ERR_ALIGN, "wc_attention: q/k/v rows must be 16-byte aligned");
+  WC_REQUIRE(aligned(a->q, es) && aligned(a->k, es) && aligned(a->v, es) && aligned(a->o, es), WC_ERR_ALIGN,
+             "wc_attention: q/k/v/o must be aligned to their element size");
+  WC_REQUIRE(a->head_dim < 0x7fffffffll, WC_ERR_LIMIT, "wc_attention: head dim too large");
   WC_REQUIRE(a->sq < 0x7fffffffll && a->skv < 0x7fffffffll && a->nb < 0x7fffffffll, WC_ERR_LIMIT,
              "wc_attention: sizes too large");
   AttnParams p;
@@ -1074,7 +1171,9 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
                "wc_attention: negative mask stride");
     WC_REQUIRE(!a->causal, WC_ERR_ARG, "wc_attention: a mask and causal masking are exclusive");
   }
-  if (!p.mask && a->dtype == WC_BF16 && (a->head_dim == 32 || a->head_dim == 64)) {
+  p.dh = (int)a->head_dim;
+  p.oc0 = 0;
+  if (al && !p.mask && a->dtype == WC_BF16 && (a->head_dim == 32 || a->head_dim == 64)) {
     // resident-KV kernel: K and V of one head in LDS, 8-byte aligned output rows
     const int skvp = static_cast<int>(cdiv(a->skv, 32) * 32);
     const bool o_al = aligned(a->o, 8) && ubytes(a->o_stride_nb, es) % 8 == 0 && ubytes(a->o_stride_s, es) % 8 == 0;
@@ -1085,9 +1184,9 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
       return w8 ? launch_res<64, 8>(p, skvp, as_stream(stream)) : launch_res<64, 4>(p, skvp, as_stream(stream));
     }
   }
-  if (a->dtype == WC_BF16) return launch_attn<bf16>(p, (int)a->head_dim, as_stream(stream));
-  if (a->dtype == WC_F16) return launch_attn<f16>(p, (int)a->head_dim, as_stream(stream));
-  return launch_attn<float>(p, (int)a->head_dim, as_stream(stream));
+  if (a->dtype == WC_BF16) return launch_attn<bf16>(p, (int)a->head_dim, al, as_stream(stream));
+  if (a->dtype == WC_F16) return launch_attn<f16>(p, (int)a->head_dim, al, as_stream(stream));
+  return launch_attn<float>(p, (int)a->head_dim, al, as_stream(stream));
 }
 
 extern "C" int32_t wc_self_attention(const wc_self_attn_args* a, void* stream) {

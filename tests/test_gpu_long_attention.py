@@ -57,3 +57,45 @@ def test_long_cross_attention(hip, dtype):
         ref = torch.stack([m.to(DEV).double()(q_in[i].double(), k_in[i].double(), v_in[i].double(),
                                                need_weights=False)[0] for i, m in enumerate(mods)])
     assert rel_err(y, ref) <= BAR[dtype]
+
+
+@pytest.mark.parametrize("dh", [1, 8, 20, 24, 40, 48, 80, 96, 112, 160, 200, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", ["plain", "causal", "mask", "cross"])
+def test_any_head_dim(hip, dh, dtype, mode):
+    """Head dims outside the vector kernel's 16 / 32 / 64 / 128 (scaled_dot_product_attention takes
+    any, and the reference passes every head dim to it, wide_attention.py:212-231): the general
+    form pads the scores' head dim and splits output columns past 128 into launches.  fp32 stops
+    at 128 (its 256-wide K tiles would not fit in LDS) and says so."""
+    import wide_compiler as wc
+    from wide_compiler import _hip
+    heads = 3 if dh <= 128 else 2
+    d = heads * dh
+    n, b, sq = 2, 2, 70
+    skv = 45 if mode == "cross" else sq
+    mods = _mods(n, d, heads, dh)
+    wide = wc.WideAttention.from_modules(mods).to(DEV, dtype).eval()
+    q_in = torch.randn(n, b, sq, d, device=DEV).to(dtype)
+    k_in = torch.randn(n, b, skv, d, device=DEV).to(dtype) if mode == "cross" else q_in
+    v_in = torch.randn(n, b, skv, d, device=DEV).to(dtype) if mode == "cross" else q_in
+    mask = (torch.randn(sq, skv, device=DEV) * 2) if mode == "mask" else None
+    if dtype == torch.float32 and dh > 128:
+        with pytest.raises(_hip.WideKernelError, match="head dim"):
+            with torch.no_grad():
+                wide(q_in, is_causal=mode == "causal", attn_mask=mask)
+        return
+    with torch.no_grad():
+        if mode == "cross":
+            y, _ = wide(q_in, k_in, v_in)
+        else:
+            y = wide(q_in, is_causal=mode == "causal", attn_mask=mask)
+        ref_mask = None
+        if mode == "causal":
+            ref_mask = torch.triu(torch.full((sq, sq), float("-inf"), device=DEV, dtype=torch.float64), 1)
+        elif mode == "mask":
+            ref_mask = mask.double()
+        ref = torch.stack([m.to(DEV).double()(q_in[i].double(), k_in[i].double(), v_in[i].double(),
+                                               need_weights=False, attn_mask=ref_mask)[0]
+                           for i, m in enumerate(mods)])
+    bar = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3}[dtype]
+    assert rel_err(y, ref) <= bar
