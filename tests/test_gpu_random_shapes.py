@@ -221,6 +221,42 @@ def test_random_masked_cross_attention(hip):
         _check(y, ref, dt, cfg)
 
 
+def test_random_head_dims(hip):
+    """Any head dim (1-256 in bf16 / fp16, 1-128 in fp32): self-attention (causal or not, with an
+    additive mask or none) and cross-attention at random lengths, rows at the odd strides that
+    heads * head_dim gives (scaled_dot_product_attention takes any head dim,
+    wide_attention.py:212-231)."""
+    import wide_compiler as wc
+    rng = random.Random(23)
+    torch.manual_seed(23)
+    for _ in range(CASES):
+        dt = _dt(rng)
+        dh = rng.randint(1, 128 if dt == torch.float32 else 256)
+        n, b, heads = rng.randint(1, 3), rng.randint(1, 3), rng.choice([1, 2, 3])
+        d, sq = dh * heads, rng.randint(1, 200)
+        kind = rng.choice(["self", "causal", "mask", "cross"])
+        skv = rng.randint(1, 200) if kind == "cross" else sq
+        cfg = (n, b, d, heads, sq, skv, dt, kind)
+        mods = [nn.MultiheadAttention(d, heads, batch_first=True) for _ in range(n)]
+        for m in mods:
+            nn.init.uniform_(m.in_proj_bias, -0.1, 0.1)
+        wide = wc.WideAttention.from_modules(mods).to(DEV, dt).eval()
+        q = torch.randn(n, b, sq, d).to(dt)
+        k, v = (torch.randn(n, b, skv, d).to(dt) for _ in range(2)) if kind == "cross" else (q, q)
+        mask = torch.randn(sq, skv) * 2 if kind == "mask" else None
+        ref_mask = mask.double() if mask is not None else (
+            torch.triu(torch.full((sq, sq), float("-inf"), dtype=torch.float64), 1) if kind == "causal" else None)
+        with torch.no_grad():
+            if kind == "cross":
+                y, _ = wide(q.to(DEV), k.to(DEV), v.to(DEV))
+            else:
+                y = wide(q.to(DEV), is_causal=kind == "causal",
+                         attn_mask=None if mask is None else mask.to(DEV))
+            ref = torch.stack([m.double()(q[i].double(), k[i].double(), v[i].double(), need_weights=False,
+                                          attn_mask=ref_mask)[0] for i, m in enumerate(mods)])
+        _check(y, ref, dt, cfg)
+
+
 @pytest.mark.parametrize("kind", ["lstm", "gru"])
 def test_random_recurrences_with_initial_state(hip, kind):
     """h0 (and c0) given: the final states as well as the output sequence."""
