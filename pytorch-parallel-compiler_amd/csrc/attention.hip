@@ -1139,7 +1139,9 @@ extern "C" int32_t wc_attention(const wc_attn_args* a, void* stream) {
                   ubytes(a->v_stride_nb, es) % 16 == 0 && ubytes(a->v_stride_s, es) % 16 == 0;
   WC_REQUIRE(aligned(a->q, es) && aligned(a->k, es) && aligned(a->v, es) && aligned(a->o, es), WC_ERR_ALIGN,
              "wc_attention: q/k/v/o must be aligned to their element size");
-  WC_REQUIRE(a->head_dim < 0x7fffffffll, WC_ERR_LIMIT, "wc_attention: head dim too large");
+  // head offsets within a row (head * head_dim) are 32-bit in the kernels
+  WC_REQUIRE(a->head_dim < 0x7fffffffll && a->heads < 0x7fffffffll && a->heads * a->head_dim < 0x7fffffffll,
+             WC_ERR_LIMIT, "wc_attention: heads x head dim too large");
   WC_REQUIRE(a->sq < 0x7fffffffll && a->skv < 0x7fffffffll && a->nb < 0x7fffffffll, WC_ERR_LIMIT,
              "wc_attention: sizes too large");
   AttnParams p;

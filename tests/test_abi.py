@@ -110,6 +110,30 @@ def test_oversized_arguments_rejected_without_overflow(hip):
     assert lib.wc_conv2d(ctypes.byref(c), None) == -5
 
 
+def test_attention_arg_checks(hip):
+    """wc_attention's host checks (pointers never dereferenced): head dims past what the kernel
+    holds (256 for 16-bit types, 128 for fp32), a row of heads x head dim beyond 32-bit offsets,
+    and pointers not aligned to the element size, each rejected before any launch."""
+    lib = hip.lib()
+
+    def args(dtype, heads, dh, base=256):
+        a = hip._AttnArgs()
+        a.dtype, a.nb, a.heads, a.sq, a.skv, a.head_dim, a.scale = dtype, 1, heads, 4, 4, dh, 1.0
+        a.q = a.k = a.v = a.o = base
+        for f in ("q", "k", "v", "o"):
+            setattr(a, f + "_stride_nb", 4 * heads * dh)
+            setattr(a, f + "_stride_s", heads * dh)
+        return a
+
+    for dtype, dh, limit in ((hip.BF16, 257, "256"), (hip.F16, 300, "256"), (hip.F32, 129, "128")):
+        assert lib.wc_attention(ctypes.byref(args(dtype, 1, dh)), None) == -5, (dtype, dh)
+        assert f"above {limit}" in hip.last_error()
+    assert lib.wc_attention(ctypes.byref(args(hip.BF16, 1 << 24, 128)), None) == -5
+    assert "heads x head dim" in hip.last_error()
+    assert lib.wc_attention(ctypes.byref(args(hip.BF16, 2, 24, base=257)), None) == -4
+    assert "aligned" in hip.last_error()
+
+
 def test_empty_problems_are_noops(hip):
     lib = hip.lib()
     assert lib.wc_swap01(None, 0, 5, 0, 0, 16, None, None) == 0
