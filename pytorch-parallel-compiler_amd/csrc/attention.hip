@@ -56,9 +56,10 @@ __device__ __forceinline__ float xor_sum(float v, int m) { return v + __shfl_xor
 // any value up to DH, its rows need no alignment, and this launch computes output columns
 // [p.oc0, p.oc0 + DO) of each head: every load and store is element-wise, with the columns
 // past p.dh read as zero and not written.
-template <typename T, int DH, bool GEN = false, int DO = DH>
+template <typename T, int DH, bool GEN = false, int DO = DH, bool VEC = false>
 __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
   static_assert(GEN || DO == DH, "only the general form splits the output columns");
+  static_assert(GEN || !VEC, "VEC selects the general form's 16-byte loads");
   constexpr bool BF = sizeof(T) == 2;
   constexpr int DHP = DH < 32 ? 32 : DH;       // head dim padded to the 32-wide S^T k-step
   constexpr int KP = DHP + (BF ? 8 : 4);       // K tile pitch (elements)
@@ -92,7 +93,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
       const T* src = qb + q * p.q_ss + s * 32 + g * 8;
-      if constexpr (GEN) {
+      if constexpr (GEN && VEC) {
+        // the head dim is a whole number of 16-byte pieces: each lies inside it or past it
+        const int c = s * 32 + g * 8;
+        qf[nt][s][0] = (q < p.sq && c < hd) ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+        qf[nt][s][1] = (!BF && q < p.sq && c + 4 < hd) ? *reinterpret_cast<const uint4*>(src + (BF ? 0 : 4))
+                                                        : make_uint4(0, 0, 0, 0);
+      } else if constexpr (GEN) {
         T t8[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) t8[j] = (q < p.sq && s * 32 + g * 8 + j < hd) ? src[j] : tzero;
@@ -114,8 +121,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
   constexpr int KPPT = (KPIECES + kAttnThreads - 1) / kAttnThreads;
   constexpr int VPPT = (VPIECES + kAttnThreads - 1) / kAttnThreads;
   uint4 kreg[KPPT], vreg[VPPT];
-  // a piece of `cols` valid columns from `src` (element-wise; the rest zero)
+  // a piece of `cols` valid columns from `src` (element-wise; the rest zero).  VEC: cols is
+  // either <= 0 or at least a whole piece, and src is 16-byte aligned
   auto piece = [&](const T* src, int cols) {
+    if constexpr (VEC) return cols > 0 ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
     T t[VE];
 #pragma unroll
     for (int j = 0; j < VE; ++j) t[j] = j < cols ? src[j] : tzero;
@@ -1061,13 +1070,13 @@ int32_t launch_qkv(QkvParams p, bool causal, hipStream_t st) {
   return check_launch("wc_self_attention");
 }
 
-template <typename T, int DH, bool GEN = false, int DO = DH>
+template <typename T, int DH, bool GEN = false, int DO = DH, bool VEC = false>
 int32_t launch_attn_dh(const AttnParams& p, dim3 grid, hipStream_t st) {
   constexpr bool BF = sizeof(T) == 2;
   constexpr size_t lds = sizeof(T) * 2 * (static_cast<size_t>(kBK) * ((DH < 32 ? 32 : DH) + (BF ? 8 : 4)) +
                                           static_cast<size_t>(DO) * (kBK + (BF ? 8 : 4)));
   static_assert(lds <= 160 * 1024, "LDS");
-  auto kernel = attn_kernel<T, DH, GEN, DO>;
+  auto kernel = attn_kernel<T, DH, GEN, DO, VEC>;
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -1079,10 +1088,29 @@ int32_t launch_attn_dh(const AttnParams& p, dim3 grid, hipStream_t st) {
   return check_launch("wc_attention");
 }
 
+// The general form: the head dim padded to the next of 16, 32, 64, 96, 128 (256 for 16-bit
+// types, computed in output chunks of 128 columns, one launch per chunk, each recomputing the
+// scores).  VEC: 16-byte loads (the head dim a whole number of 16-byte pieces, rows aligned).
+template <typename T, bool VEC>
+int32_t launch_gen(AttnParams p, int dh, dim3 grid, hipStream_t st) {
+  if (dh <= 16) return launch_attn_dh<T, 16, true, 16, VEC>(p, grid, st);
+  if (dh <= 32) return launch_attn_dh<T, 32, true, 32, VEC>(p, grid, st);
+  if (dh <= 64) return launch_attn_dh<T, 64, true, 64, VEC>(p, grid, st);
+  if (dh <= 96) return launch_attn_dh<T, 96, true, 96, VEC>(p, grid, st);
+  if (dh <= 128) return launch_attn_dh<T, 128, true, 128, VEC>(p, grid, st);
+  if constexpr (sizeof(T) == 2) {
+    for (int oc0 = 0; oc0 < dh; oc0 += 128) {
+      p.oc0 = oc0;
+      const int32_t rc = launch_attn_dh<T, 256, true, 128, VEC>(p, grid, st);
+      if (rc != WC_OK) return rc;
+    }
+  }
+  return WC_OK;
+}
+
 // Head dims 16, 32, 64 and 128 with 16-byte aligned rows take the vector form; any other head
 // dim (up to 256 for 16-bit types, 128 for fp32, whose 256-wide K tiles would not fit in LDS),
-// or unaligned rows, the general form: the head dim padded to the next of those sizes, output
-// columns in chunks of at most 128, one launch per chunk (each recomputes the scores).
+// or unaligned rows, the general form above.
 template <typename T>
 int32_t launch_attn(AttnParams p, int dh, bool aligned_rows, hipStream_t st) {
   const int64_t blocks = static_cast<int64_t>(p.nb) * p.heads * p.q_tiles;
@@ -1103,18 +1131,9 @@ int32_t launch_attn(AttnParams p, int dh, bool aligned_rows, hipStream_t st) {
                      sizeof(T) == 2 ? "16-bit types" : "fp32");
   p.dh = dh;
   p.oc0 = 0;
-  if (dh <= 16) return launch_attn_dh<T, 16, true, 16>(p, grid, st);
-  if (dh <= 32) return launch_attn_dh<T, 32, true, 32>(p, grid, st);
-  if (dh <= 64) return launch_attn_dh<T, 64, true, 64>(p, grid, st);
-  if (dh <= 128) return launch_attn_dh<T, 128, true, 128>(p, grid, st);
-  if constexpr (sizeof(T) == 2) {
-    for (int oc0 = 0; oc0 < dh; oc0 += 128) {
-      p.oc0 = oc0;
-      const int32_t rc = launch_attn_dh<T, 256, true, 128>(p, grid, st);
-      if (rc != WC_OK) return rc;
-    }
-  }
-  return WC_OK;
+  // whole 16-byte pieces per head (and 16-byte aligned rows): vector loads
+  if (aligned_rows && (dh * static_cast<int>(sizeof(T))) % 16 == 0) return launch_gen<T, true>(p, dh, grid, st);
+  return launch_gen<T, false>(p, dh, grid, st);
 }
 
 }  // namespace

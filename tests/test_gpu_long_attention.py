@@ -59,7 +59,7 @@ def test_long_cross_attention(hip, dtype):
     assert rel_err(y, ref) <= BAR[dtype]
 
 
-@pytest.mark.parametrize("dh", [1, 8, 20, 24, 40, 48, 80, 96, 112, 160, 200, 256])
+@pytest.mark.parametrize("dh", [1, 8, 20, 24, 40, 48, 72, 80, 96, 112, 160, 200, 256])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("mode", ["plain", "causal", "mask", "cross"])
 def test_any_head_dim(hip, dh, dtype, mode):
