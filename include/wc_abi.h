@@ -430,8 +430,9 @@ int32_t wc_conv3d(const wc_conv3d_args* args, void* stream);
  * [N*B, S, heads*head_dim] layout of the projection outputs, read in place.
  * dtype WC_F32, WC_BF16 or WC_F16; fp32 softmax / accumulation.  Any head_dim >= 1 up to 256
  * (16-bit types) or 128 (fp32), else WC_ERR_LIMIT; pointers aligned to the element size (else
- * WC_ERR_ALIGN).  Head dims 16/32/64/128 with 16-byte aligned rows run vector loads; others run
- * element loads with the head dim zero-padded, and past 128 one launch per 128 output columns.
+ * WC_ERR_ALIGN).  Other head dims than 16/32/64/128 are zero-padded to the next of 16/32/64/96/
+ * 128/256, and past 128 take one launch per 128 output columns.  16-byte aligned rows whose head
+ * spans whole 16-byte pieces load 16-byte vectors; other rows load element by element (~2x slower).
  */
 typedef struct wc_attn_args {
   int32_t dtype, causal;
