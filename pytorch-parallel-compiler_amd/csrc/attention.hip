@@ -72,8 +72,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int fr = lane & 15, g = lane >> 4;
-  const int qt = blockIdx.x % p.q_tiles;
-  const int bh = blockIdx.x / p.q_tiles;
+  // Workgroups are dealt to the 8 XCDs round-robin.  Give XCD x the contiguous range
+  // [x * grid/8, (x+1) * grid/8) of (head, query tile) pairs, so a head's query tiles share one
+  // L2 (its K/V is fetched once per XCD, not by every XCD) and every XCD gets every tile
+  // length under a causal mask; within a head the last (longest causal) tiles start first.
+  int lin = blockIdx.x;
+  if ((gridDim.x & 7) == 0) lin = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int bh = lin / p.q_tiles;
+  const int qt = p.q_tiles - 1 - (lin - bh * p.q_tiles);
   const int nb = bh / p.heads, h = bh - (bh / p.heads) * p.heads;
   const int hd = GEN ? p.dh : DH;               // head stride within a row
   const int oc0 = GEN ? p.oc0 : 0;              // first V / O column of this launch
