@@ -56,8 +56,20 @@ __device__ __forceinline__ float xor_sum(float v, int m) { return v + __shfl_xor
 // any value up to DH, its rows need no alignment, and this launch computes output columns
 // [p.oc0, p.oc0 + DO) of each head: every load and store is element-wise, with the columns
 // past p.dh read as zero and not written.
+// At least two waves per SIMD (VGPRs + AGPRs within 256) where that compiles without scratch,
+// and for the exact 16-bit 128-wide tile, whose ~92 bytes of spills cost less than the second
+// wave gains: left to itself the compiler gives that tile 254 + 64 registers, one wave per SIMD
+// (2048 tokens, bf16: head dim 64 0.93 -> 0.68 ms, 128 2.87 -> 2.12 ms).  The general 128-wide
+// tile and fp32 past 64 would spill without gaining; they keep the compiler's choice.
+template <typename T, int DH, bool GEN>
+constexpr int attn_min_waves() {
+  if constexpr (sizeof(T) == 2) return (DH <= 96 || (DH == 128 && !GEN)) ? 2 : 1;
+  else return DH <= 64 ? 2 : 1;
+}
+
 template <typename T, int DH, bool GEN = false, int DO = DH, bool VEC = false>
-__global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnParams p) {
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(attn_min_waves<T, DH, GEN>())))
+void attn_kernel(AttnParams p) {
   static_assert(GEN || DO == DH, "only the general form splits the output columns");
   static_assert(GEN || !VEC, "VEC selects the general form's 16-byte loads");
   constexpr bool BF = sizeof(T) == 2;
