@@ -572,7 +572,7 @@ __device__ __forceinline__ void res_store_o(const ResRows<NKS, DT>& r, const int
 }
 
 template <int DH, int W, bool CAUSAL>
-__global__ __launch_bounds__(W * 64) void attn_res_kernel(AttnParams p, int skvp) {
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(W == 4 ? 2 : 1))) void attn_res_kernel(AttnParams p, int skvp) {
   constexpr int KP = res_kpitch<DH>();
   constexpr int NKS = DH / 16;                       // 16-dim k-steps of S^T = K Q^T
   constexpr int DT = DH / 32;                        // 32-row tiles of O^T
